@@ -1,0 +1,168 @@
+"""Mimi encode+decode benchmark on one MI355X (prints one JSON line).
+
+Workload: batch 1, 10 s of seeded synthetic 24 kHz
+audio, 8 codebooks, FP32, the whole round trip replayed from a captured
+hipGraph through ``MimiModel.forward``.  Inputs are resident in HBM before the
+timed region.  ``value`` is audio-seconds per second; ``ms_per_step`` the mean
+and ``median_ms`` the median round-trip latency.  The batch-16 configuration
+(configs[2]: 10 s clips, last 4 zero-padded from 6 s) is reported beside it.
+
+``roofline`` describes the dominant kernel: its algorithmic FLOPs per launch
+over its mean launch time, timed with HIP events on the stream it runs on.
+``cpu_baseline`` times the repository's CPU oracle (the reference's portable
+PyTorch path restated op for op) on the host cores, on the same 10 s input.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "fast-mimi_amd"))
+
+from fast_mimi_amd import MimiConfig, MimiModel, synthetic  # noqa: E402
+from fast_mimi_amd import _native as nat  # noqa: E402
+from fast_mimi_amd.flops import layer_table, roundtrip_flops  # noqa: E402
+
+PEAK_FP32_TFLOPS = 157.3  # MI355X dense FP32 (matrix) peak
+PEAK_HBM_GBS = 8000.0
+DOMINANT = "dec.up4"      # ConvTranspose1d 128->64, stride 4, 60000 -> 240000 rows
+
+
+def time_steps(fn, steps: int, warmup: int) -> list[float]:
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(steps):
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        fn()
+        stop.record()
+        stop.synchronize()
+        times.append(start.elapsed_time(stop))
+    return times
+
+
+def dominant_kernel(model: MimiModel, name: str, batch: int, samples: int, nq: int, iters: int):
+    """Mean launch time of one contraction at its real shape, HIP events."""
+    rt = model.runtime()
+    row = next(r for r in layer_table(model.config, batch, samples, nq) if r[0] == name)
+    flops = row[2]
+    op = rt.layer_op(name, batch, samples)
+    for _ in range(3):
+        op()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iters):
+        op()
+    stop.record()
+    stop.synchronize()
+    ms = start.elapsed_time(stop) / iters
+    achieved = flops / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "kernel": f"gemm_kernel ({name}: {row[1]} rows={row[3]} K={row[4]} N={row[5]})",
+            "flops_per_launch": flops, "avg_launch_ms": ms, "achieved": round(achieved, 3),
+            "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
+            "traffic": None}
+
+
+def cpu_baseline(audio: np.ndarray, mask: np.ndarray, nq: int, runs: int) -> dict:
+    sys.path.insert(0, str(REPO))
+    from oracle.mimi_oracle import MimiOracle
+    from fast_mimi_amd.weights import seeded_state_dict
+
+    cores = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(cores)
+    cfg = MimiConfig()
+    oracle = MimiOracle(cfg, {k: torch.from_numpy(v) for k, v in seeded_state_dict(cfg, 0).items()})
+    a, m = torch.from_numpy(audio), torch.from_numpy(mask)
+    oracle.forward(a, m, nq)  # warm-up
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter_ns()
+        oracle.forward(a, m, nq)
+        times.append((time.perf_counter_ns() - t0) / 1e6)
+    med = statistics.median(times)
+    seconds = audio.shape[0] * audio.shape[-1] / 24_000
+    return {"value": round(seconds / (med / 1e3), 3), "unit": "audio-sec/sec", "cores": cores,
+            "kind": "port", "median_ms": round(med, 2),
+            "sample": f"B1 x 10 s, nq={nq}, CPU oracle (PyTorch eager, op order of model.py), "
+                      f"median of {runs} after 1 warm-up"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-runs", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-batch16", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(clips shard data-parallel across GPUs with no exchange; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+    nat.library()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    cfg = MimiConfig()
+    model = MimiModel(cfg, device=dev, seed=0)
+
+    audio, mask, nq = synthetic.config_inputs("c2")
+    a, m = torch.from_numpy(audio).to(dev), torch.from_numpy(mask).to(dev)
+    times = time_steps(lambda: model(a, m, num_quantizers=nq), args.steps, args.warmup)
+    mean_ms = statistics.fmean(times)
+    med_ms = statistics.median(times)
+    seconds = audio.shape[0] * audio.shape[-1] / 24_000
+    flops = roundtrip_flops(cfg, 1, audio.shape[-1], nq)
+
+    result = {
+        "metric": "median ms, 10 s clip bs=1; audio-sec/sec at bs=16 (encode+decode, 8 codebooks)",
+        "value": round(seconds / (med_ms / 1e3), 3),
+        "unit": "audio-sec/sec (B=1, 10 s, median)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(mean_ms, 4), "median_ms": round(med_ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded sinusoids + pink noise; seeded random-init weights)",
+        "config": {"workload": "mimi encode+decode, B1 x 10 s @ 24 kHz, nq=8, hipGraph replay",
+                   "global_batch": 1, "samples": int(audio.shape[-1]), "num_quantizers": nq},
+        "pipeline_tflops": round(flops / (med_ms * 1e-3) / 1e12, 3),
+        "pipeline_flops": flops,
+    }
+    if not args.no_batch16:
+        a16, m16, nq16 = synthetic.config_inputs("c3")
+        a16d, m16d = torch.from_numpy(a16).to(dev), torch.from_numpy(m16).to(dev)
+        t16 = time_steps(lambda: model(a16d, m16d, num_quantizers=nq16), max(5, args.steps // 5), 2)
+        med16 = statistics.median(t16)
+        f16 = roundtrip_flops(cfg, 16, a16.shape[-1], nq16)
+        result["batch16"] = {"audio_sec_per_sec": round(16 * 10 / (med16 / 1e3), 2),
+                             "median_ms": round(med16, 3),
+                             "pipeline_tflops": round(f16 / (med16 * 1e-3) / 1e12, 3)}
+    result["roofline"] = dominant_kernel(model, DOMINANT, 1, audio.shape[-1], nq, 50)
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(audio, mask, nq, args.cpu_runs)
+        result["speedup_vs_cpu"] = round(result["value"] / result["cpu_baseline"]["value"], 2)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,47 @@
+// Shared device helpers for the gfx950 (CDNA4) Mimi kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define FM_DEVICE __device__ __forceinline__
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// Status codes returned through the C ABI (hipError_t values pass through).
+enum FmStatus {
+  FM_OK = 0,
+  FM_BAD_ARGUMENT = 1000,
+  FM_WORKSPACE_TOO_SMALL = 1001,
+  FM_UNSUPPORTED = 1002,
+};
+
+// Epilogue / loader flags of the implicit-GEMM kernel.
+enum FmGemmFlags {
+  FM_ELU_IN = 1,        // apply ELU to A operands as they are loaded
+  FM_REPLICATE = 2,     // out-of-range input positions clamp to the edge (else zero)
+  FM_EPI_ELU = 4,       // ELU on the output
+  FM_EPI_GELU = 8,      // exact-erf GELU on the output
+  FM_EPI_RES_ADD = 16,  // y = res + (acc + bias)
+  FM_EPI_RES_SCALE = 32 // y = res + scale[n] * acc
+};
+
+// ELU with alpha = 1 (torch.nn.ELU).
+FM_DEVICE float fm_elu(float x) { return x > 0.0f ? x : expm1f(x); }
+
+// Exact-erf GELU (torch.nn.functional.gelu, approximate='none').
+FM_DEVICE float fm_gelu(float x) {
+  return __fmul_rn(__fmul_rn(x, 0.5f), __fadd_rn(1.0f, erff(__fmul_rn(x, 0.70710678118654752440f))));
+}
+
+// One v_mfma_f32_32x32x2f32: D(32x32) += A(32x2) * B(2x32).
+// Lane l supplies A[l % 32][l / 32] and B[l / 32][l % 32]; the 16 results of
+// lane l are D[8*(r/4) + 4*(l/32) + (r%4)][l % 32], r = 0..15.
+FM_DEVICE floatx16 fm_mfma32(float a, float b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+FM_DEVICE int fm_mfma32_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+static inline int fm_ceil_div(long a, long b) { return (int)((a + b - 1) / b); }

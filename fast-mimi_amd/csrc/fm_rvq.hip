@@ -1,0 +1,325 @@
+// Split residual vector quantizer of the Mimi hot path.
+//
+// Encode, one launch per codebook step j (the residual chain is sequential):
+//   each block owns RB query rows and one chunk of codebook entries;
+//   prologue (j > 0): resolve step j-1's argmin from its per-chunk partials,
+//     residual_j = residual_{j-1} - e_{j-1}[code]  (one FP32 subtract, as the
+//     reference's ``residual - quantized``), chunk-0 blocks publish the
+//     residual and step j-1's code;
+//   main: distance GEMM on FP32 MFMA against the transposed codebook,
+//     d = (-2 x.e + |x|^2) + |e|^2 -> clamp(0) -> sqrt (torch cdist's mm form),
+//     and a lowest-index argmin reduced across lanes and waves.
+// A finalize launch resolves the last step.
+//
+// Decode: ordered gather-sum (0 + e_0[c_0] for the semantic branch,
+// 0 + e_1[c_1] + e_2[c_2] + ... left to right for the acoustic branch) into
+// the [rows, 2*dim] operand of the fused output projection GEMM.
+
+#include "fm_common.h"
+
+namespace {
+
+constexpr int RB = 32;  // query rows per block
+
+FM_DEVICE bool better(float v, int i, float bv, int bi) {
+  return v < bv || (v == bv && i < bi);
+}
+
+struct StepArgs {
+  const float* resid_in;   // rows entering step j-1 (or step 0), row pitch ld_in
+  int ld_in;
+  const float* prev_embed; // codebook j-1 [entries][dim]; null at step 0
+  const float* prev_val;   // step j-1 partials [chunks][M]
+  const int* prev_idx;
+  float* resid_out;        // residual_j [M][dim] (chunk-0 blocks write it); may be null at step 0
+  int64_t* prev_codes;     // codes of step j-1 (row (b,t) at b*batch_stride + t)
+  const float* embed_t;    // codebook j transposed [dim][entries]
+  const float* norms;      // |e|^2 [entries]
+  float* val;              // step j partials [chunks][M]
+  int* idx;
+  int M, dim, entries, chunk_entries, chunks, rows_per_batch, batch_stride;
+};
+
+FM_DEVICE void resolve(const float* val, const int* idx, int chunks, long M, long m, float& bv,
+                       int& bi) {
+  bv = val[m];
+  bi = idx[m];
+  for (int c = 1; c < chunks; ++c) {
+    const float v = val[(long)c * M + m];
+    const int i = idx[(long)c * M + m];
+    if (better(v, i, bv, bi)) bv = v, bi = i;
+  }
+}
+
+// Dynamic LDS: Xs[dim][RB+1] (k-major, MFMA A operand), xn[RB], best[4][RB] x2, codes[RB].
+__global__ __launch_bounds__(256) void rvq_step_kernel(StepArgs a) {
+  extern __shared__ float smem[];
+  constexpr int PX = RB + 1;
+  float* Xs = smem;
+  float* xn = Xs + a.dim * PX;
+  float* bval = xn + RB;
+  int* bidx = reinterpret_cast<int*>(bval + 4 * RB);
+  int* rcode = bidx + 4 * RB;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const long m0 = (long)blockIdx.x * RB;
+  const int chunk = blockIdx.y;
+
+  if (a.prev_embed && tid < RB) {
+    const long m = m0 + tid;
+    int code = 0;
+    if (m < a.M) {
+      float bv;
+      resolve(a.prev_val, a.prev_idx, a.chunks, a.M, m, bv, code);
+      if (chunk == 0) {
+        const long b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
+        a.prev_codes[b * a.batch_stride + t] = code;
+      }
+    }
+    rcode[tid] = code;
+  }
+  __syncthreads();
+  for (int e = tid; e < RB * a.dim; e += 256) {
+    const int r = e / a.dim, k = e % a.dim;
+    const long m = m0 + r;
+    float x = 0.0f;
+    if (m < a.M) {
+      x = a.resid_in[m * a.ld_in + k];
+      if (a.prev_embed) {
+        x = __fsub_rn(x, a.prev_embed[(long)rcode[r] * a.dim + k]);
+        if (chunk == 0 && a.resid_out) a.resid_out[m * a.dim + k] = x;
+      }
+    }
+    Xs[k * PX + r] = x;
+  }
+  __syncthreads();
+  if (tid < RB) {
+    float s = 0.0f;
+    for (int k = 0; k < a.dim; ++k) s = fmaf(Xs[k * PX + tid], Xs[k * PX + tid], s);
+    xn[tid] = s;
+  }
+  __syncthreads();
+
+  // Distances for this chunk; lane owns entry column (lane % 32) of each 32-wide tile.
+  float best_v[16];
+  int best_i[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) best_v[r] = INFINITY, best_i[r] = 0x7fffffff;
+  const int e_begin = chunk * a.chunk_entries;
+  const int e_end = min(a.entries, e_begin + a.chunk_entries);
+  const int lrow = lane >> 5, lcol = lane & 31;
+  for (int t0 = e_begin + wave * 32; t0 < e_end; t0 += 4 * 32) {
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    const int col = t0 + lcol;
+    const bool col_ok = col < e_end;
+    const float* bt = a.embed_t + col;
+#pragma unroll 8
+    for (int k = 0; k < a.dim; k += 2) {
+      const float av = Xs[(k + lrow) * PX + lcol];
+      const float bv = col_ok ? bt[(long)(k + lrow) * a.entries] : 0.0f;
+      acc = fm_mfma32(av, bv, acc);
+    }
+    if (col_ok) {
+      const float en = a.norms[col];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = fm_mfma32_row(r, lane);
+        const float d = __fadd_rn(__fadd_rn(__fmul_rn(-2.0f, acc[r]), xn[row]), en);
+        const float dist = sqrtf(fmaxf(d, 0.0f));
+        if (better(dist, col, best_v[r], best_i[r])) best_v[r] = dist, best_i[r] = col;
+      }
+    }
+  }
+  // Reduce across the 32 lanes that share each row.
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float v = best_v[r];
+    int i = best_i[r];
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) {
+      const float ov = __shfl_xor(v, o, 64);
+      const int oi = __shfl_xor(i, o, 64);
+      if (better(ov, oi, v, i)) v = ov, i = oi;
+    }
+    if (lcol == 0) {
+      const int row = fm_mfma32_row(r, lane);
+      bval[wave * RB + row] = v;
+      bidx[wave * RB + row] = i;
+    }
+  }
+  __syncthreads();
+  if (tid < RB) {
+    const long m = m0 + tid;
+    float v = bval[tid];
+    int i = bidx[tid];
+    for (int w = 1; w < 4; ++w)
+      if (better(bval[w * RB + tid], bidx[w * RB + tid], v, i)) v = bval[w * RB + tid], i = bidx[w * RB + tid];
+    if (m < a.M) {
+      a.val[(long)chunk * a.M + m] = v;
+      a.idx[(long)chunk * a.M + m] = i;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void rvq_finalize_kernel(const float* val, const int* idx,
+                                                           int chunks, int M, int64_t* codes,
+                                                           int rows_per_batch, int batch_stride) {
+  const long m = (long)blockIdx.x * 256 + threadIdx.x;
+  if (m >= M) return;
+  float bv;
+  int bi;
+  resolve(val, idx, chunks, M, m, bv, bi);
+  const long b = m / rows_per_batch, t = m - b * rows_per_batch;
+  codes[b * batch_stride + t] = bi;
+}
+
+// embed = embed_sum / max(usage, eps); transposed copy; squared norms.
+__global__ __launch_bounds__(256) void rvq_prepare_kernel(const float* embed_sum, const float* usage,
+                                                          int entries, int dim, float eps,
+                                                          float* embed, float* embed_t,
+                                                          float* norms) {
+  const int e = blockIdx.x;
+  const float u = fmaxf(usage[e], eps);
+  float s = 0.0f;
+  for (int k = threadIdx.x; k < dim; k += 256) {
+    const float v = embed_sum[(long)e * dim + k] / u;
+    embed[(long)e * dim + k] = v;
+    embed_t[(long)k * entries + e] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 0; k < dim; ++k) {
+      const float v = embed[(long)e * dim + k];
+      s = fmaf(v, v, s);
+    }
+    norms[e] = s;
+  }
+}
+
+// out[m][0:dim] = 0 + E_0[c_0];  out[m][dim:2dim] = ((0 + E_1[c_1]) + E_2[c_2]) + ...
+// Codebook j lives at embeds + j * entries * dim.  Out-of-range codes yield NaN.
+__global__ __launch_bounds__(256) void rvq_decode_kernel(const int64_t* codes, int nq, int n_sem,
+                                                         int rows_per_batch, long M,
+                                                         const float* embeds, int entries, int dim,
+                                                         float* out) {
+  const long e = (long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= M * dim) return;
+  const long m = e / dim;
+  const int k = (int)(e - m * dim);
+  const long b = m / rows_per_batch, t = m - b * rows_per_batch;
+  const int64_t* cp = codes + b * (long)nq * rows_per_batch + t;
+  float sem = 0.0f, ac = 0.0f;
+  for (int j = 0; j < nq; ++j) {
+    const int64_t c = cp[(long)j * rows_per_batch];
+    float v = (c >= 0 && c < entries) ? embeds[((long)j * entries + c) * dim + k] : NAN;
+    if (j < n_sem) sem = __fadd_rn(sem, v);
+    else ac = __fadd_rn(ac, v);
+  }
+  out[m * 2 * dim + k] = sem;
+  out[m * 2 * dim + dim + k] = ac;
+}
+
+size_t step_lds_bytes(int dim) {
+  return (size_t)dim * (RB + 1) * 4 + RB * 4 + 4 * RB * 4 + 4 * RB * 4 + RB * 4;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fm_rvq_prepare_codebook(const float* embed_sum, const float* cluster_usage, int entries,
+                            int dim, float eps, float* embed, float* embed_t, float* norms,
+                            hipStream_t stream) {
+  if (!embed_sum || !cluster_usage || !embed || !embed_t || !norms || entries <= 0 || dim <= 0)
+    return FM_BAD_ARGUMENT;
+  hipLaunchKernelGGL(rvq_prepare_kernel, dim3(entries), dim3(256), 0, stream, embed_sum,
+                     cluster_usage, entries, dim, eps, embed, embed_t, norms);
+  return (int)hipGetLastError();
+}
+
+// Partials workspace needed by fm_rvq_encode, in bytes.
+size_t fm_rvq_workspace_bytes(int rows, int dim, int entries) {
+  const int chunks = 16;
+  return (size_t)2 * rows * dim * sizeof(float) + (size_t)2 * chunks * rows * (sizeof(float) + sizeof(int)) + 256;
+}
+
+// Encodes one RVQ branch: ``count`` codebooks applied to rows x[m] (pitch ld_x).
+// embeds / embeds_t / norms hold the branch's codebooks contiguously
+// ([count][entries][dim], [count][dim][entries], [count][entries]).
+// codes: int64 base of codebook 0's codes; row (b, t) of codebook j lands at
+// codes[b * batch_stride + j * rows_per_batch + t].
+int fm_rvq_encode(const float* x, int ld_x, int rows, int rows_per_batch, int dim, int entries,
+                  int count, const float* embeds, const float* embeds_t, const float* norms,
+                  int64_t* codes, int batch_stride, void* workspace, size_t workspace_bytes,
+                  hipStream_t stream) {
+  if (!x || !embeds || !embeds_t || !norms || !codes || rows < 0 || dim <= 0 || dim % 2 ||
+      entries <= 0 || count <= 0 || rows_per_batch <= 0 || ld_x < dim)
+    return FM_BAD_ARGUMENT;
+  if (rows == 0) return FM_OK;
+  if (!workspace || workspace_bytes < fm_rvq_workspace_bytes(rows, dim, entries))
+    return FM_WORKSPACE_TOO_SMALL;
+  const int row_blocks = (rows + RB - 1) / RB;
+  // Enough chunks to spread one step over the GPU; chunks are multiples of 128 entries.
+  int chunks = 1;
+  while (chunks < 16 && row_blocks * chunks < 512 && entries / (chunks * 2) >= 128) chunks *= 2;
+  const int chunk_entries = (entries + chunks - 1) / chunks;
+
+  char* ws = static_cast<char*>(workspace);
+  float* resid[2] = {reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws) + (size_t)rows * dim};
+  ws += (size_t)2 * rows * dim * sizeof(float);
+  float* val[2] = {reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws) + (size_t)16 * rows};
+  ws += (size_t)2 * 16 * rows * sizeof(float);
+  int* idx[2] = {reinterpret_cast<int*>(ws), reinterpret_cast<int*>(ws) + (size_t)16 * rows};
+
+  const size_t lds = step_lds_bytes(dim);
+  if (lds > 64 * 1024) return FM_UNSUPPORTED;
+  for (int j = 0; j < count; ++j) {
+    StepArgs a{};
+    const int cur = j & 1, prev = cur ^ 1;
+    if (j == 0) {
+      a.resid_in = x;
+      a.ld_in = ld_x;
+    } else {
+      a.resid_in = (j == 1) ? x : resid[prev];
+      a.ld_in = (j == 1) ? ld_x : dim;
+      a.prev_embed = embeds + (size_t)(j - 1) * entries * dim;
+      a.prev_val = val[prev];
+      a.prev_idx = idx[prev];
+      a.resid_out = resid[cur];
+      a.prev_codes = codes + (size_t)(j - 1) * rows_per_batch;
+    }
+    a.embed_t = embeds_t + (size_t)j * entries * dim;
+    a.norms = norms + (size_t)j * entries;
+    a.val = val[cur];
+    a.idx = idx[cur];
+    a.M = rows; a.dim = dim; a.entries = entries; a.chunk_entries = chunk_entries;
+    a.chunks = chunks; a.rows_per_batch = rows_per_batch; a.batch_stride = batch_stride;
+    hipLaunchKernelGGL(rvq_step_kernel, dim3(row_blocks, chunks), dim3(256), lds, stream, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+  }
+  const int last = (count - 1) & 1;
+  hipLaunchKernelGGL(rvq_finalize_kernel, dim3((rows + 255) / 256), dim3(256), 0, stream,
+                     val[last], idx[last], chunks, rows,
+                     codes + (size_t)(count - 1) * rows_per_batch, rows_per_batch, batch_stride);
+  return (int)hipGetLastError();
+}
+
+int fm_rvq_decode(const int64_t* codes, int batch, int num_codebooks, int frames,
+                  int num_semantic, const float* embeds, int entries, int dim, float* out,
+                  hipStream_t stream) {
+  if (!codes || !embeds || !out || batch < 0 || frames < 0 || num_codebooks <= 0 ||
+      num_semantic < 0 || entries <= 0 || dim <= 0)
+    return FM_BAD_ARGUMENT;
+  const long M = (long)batch * frames;
+  if (M == 0) return FM_OK;
+  const long total = M * dim;
+  hipLaunchKernelGGL(rvq_decode_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     stream, codes, num_codebooks, num_semantic, frames, M, embeds, entries, dim,
+                     out);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

@@ -1,0 +1,349 @@
+"""Device runtime: packed weights and the layer sequence of encode / decode.
+
+Every contraction and every nonlinearity runs in ``libfast_mimi_amd.so``;
+PyTorch only owns device memory (weights, activations, workspaces) and the
+stream.  Activations are channels-last ``[batch, positions, channels]``
+throughout, so the reference's NCL ``transpose(1, 2)`` hand-offs between the
+SEANet stacks and the transformers (``model.py:2964-3005``, ``:3139-3170``)
+disappear.
+
+Fusion plan (one kernel per line):
+  SEANet conv           -> implicit GEMM + bias (+ ELU when an ELU follows)
+  residual block conv1  -> ELU-on-load + k3 conv + bias + ELU
+  residual block conv2  -> 1x1 conv + bias + residual add (+ ELU when one follows)
+  ConvTranspose1d       -> stride-phase GEMM + bias
+  LayerNorm             -> one wave per row
+  q/k/v projections     -> one GEMM against the packed [hidden, 3*hidden] weight
+  attention             -> RoPE on load + causal window-250 online softmax
+  o_proj / fc2          -> GEMM + LayerScale residual (in place)
+  fc1                   -> GEMM + exact-erf GELU
+  RVQ in projections    -> one GEMM for both branches
+  RVQ codebook step     -> distance GEMM + argmin + residual subtract
+  RVQ decode            -> ordered gather-sum, then one GEMM for both out projections
+"""
+
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import _native as nat
+from .config import MimiConfig
+from .weights import decoder_layer_indices, encoder_layer_indices
+
+_WORKSPACE_BYTES = 64 << 20
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+class _Conv:
+    """Causal Conv1d packed for the implicit GEMM: W[(tap, c_in), c_out]."""
+
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None, stride: int = 1,
+                 pad_mode: str = "constant"):
+        c_out, c_in, k = weight.shape
+        self.c_in, self.c_out, self.k, self.stride = c_in, c_out, k, stride
+        self.replicate = 1 if pad_mode == "replicate" else 0
+        self.w = weight.permute(2, 1, 0).reshape(k * c_in, c_out).contiguous()
+        self.b = None if bias is None else bias.contiguous()
+
+
+class _ConvT:
+    """Causal ConvTranspose1d packed as W[(tap, c_in), (phase, c_out)].
+
+    Output row q*s + r reads inputs q - taps + 1 .. q; window slot jj holds input
+    q - (taps - 1 - jj), which meets kernel tap r + (taps - 1 - jj) * s.
+    """
+
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None, stride: int):
+        c_in, c_out, k = weight.shape
+        if k % stride:
+            raise ValueError("transposed-conv kernel must be a multiple of its stride")
+        taps = k // stride
+        self.c_in, self.c_out, self.k, self.stride = c_in, c_out, k, stride
+        w = weight.reshape(c_in, c_out, taps, stride).flip(2)  # [ci, co, jj, r]
+        self.w = w.permute(2, 0, 3, 1).reshape(taps * c_in, stride * c_out).contiguous()
+        self.b = None if bias is None else bias.contiguous()
+
+
+class _Layer:
+    def __init__(self, state, prefix, cfg: MimiConfig):
+        g = lambda n: state[f"{prefix}.{n}"]  # noqa: E731
+        self.ln1 = (g("input_layernorm.weight").contiguous(), g("input_layernorm.bias").contiguous())
+        self.ln2 = (g("post_attention_layernorm.weight").contiguous(),
+                    g("post_attention_layernorm.bias").contiguous())
+        self.wqkv = torch.cat([g("self_attn.q_proj.weight"), g("self_attn.k_proj.weight"),
+                               g("self_attn.v_proj.weight")], 0).t().contiguous()
+        self.wo = g("self_attn.o_proj.weight").t().contiguous()
+        self.w1 = g("mlp.fc1.weight").t().contiguous()
+        self.w2 = g("mlp.fc2.weight").t().contiguous()
+        self.ls1 = g("self_attn_layer_scale.scale").contiguous()
+        self.ls2 = g("mlp_layer_scale.scale").contiguous()
+
+
+def rope_tables(config: MimiConfig, length: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos/sin ``[T, head_dim]`` exactly as ``MimiRotaryEmbedding`` builds them
+    (``model.py:1499-1535``): float32 inverse frequencies, one rounded product
+    per (position, frequency), duplicated halves, CPU ``cos``/``sin``."""
+    d = config.head_dim
+    inv_freq = 1.0 / (config.rope_theta ** (torch.arange(0, d, 2, dtype=torch.int64).float() / d))
+    freqs = torch.arange(length).float()[:, None] * inv_freq[None, :]
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().contiguous(), emb.sin().contiguous()
+
+
+class MimiRuntime:
+    """Executes Mimi encode / decode on one GPU through the HIP library."""
+
+    def __init__(self, config: MimiConfig, state: dict[str, torch.Tensor], device: torch.device):
+        if config.use_conv_shortcut:
+            raise NotImplementedError("learned residual shortcuts are not part of this runtime")
+        if config.num_residual_layers != 1:
+            raise NotImplementedError("only one residual block per SEANet stage (dilation 1) is supported")
+        if config.vector_quantization_hidden_dimension == config.hidden_size:
+            raise NotImplementedError("RVQ without input/output projections is not supported")
+        nat.library()
+        self.config = config
+        self.device = device
+        self.lock = threading.Lock()
+        st = {k: v.to(device=device, dtype=torch.float32) for k, v in state.items()}
+        cfg = config
+
+        def conv(prefix, stride=1, pad_mode="constant"):
+            return _Conv(st[f"{prefix}.conv.weight"], st.get(f"{prefix}.conv.bias"), stride, pad_mode)
+
+        def res(prefix):
+            return (conv(f"{prefix}.block.1"), conv(f"{prefix}.block.3"))
+
+        enc = encoder_layer_indices(cfg)
+        ratios = list(reversed(cfg.upsampling_ratios))
+        self.enc_first = conv("encoder.layers.0")
+        self.enc_stages = [(res(f"encoder.layers.{enc['res'][i][0]}"),
+                            conv(f"encoder.layers.{enc['down'][i]}", stride=r))
+                           for i, r in enumerate(ratios)]
+        self.enc_last = conv(f"encoder.layers.{enc['last'][0]}")
+        dec = decoder_layer_indices(cfg)
+        self.dec_first = conv("decoder.layers.0")
+        self.dec_stages = [(_ConvT(st[f"decoder.layers.{dec['up'][i]}.conv.weight"],
+                                   st.get(f"decoder.layers.{dec['up'][i]}.conv.bias"), r),
+                            res(f"decoder.layers.{dec['res'][i][0]}"))
+                           for i, r in enumerate(cfg.upsampling_ratios)]
+        self.dec_last = conv(f"decoder.layers.{dec['last'][0]}")
+        self.enc_tf = [_Layer(st, f"encoder_transformer.layers.{i}", cfg) for i in range(cfg.num_hidden_layers)]
+        self.dec_tf = [_Layer(st, f"decoder_transformer.layers.{i}", cfg) for i in range(cfg.num_hidden_layers)]
+        self.bottleneck = cfg.frame_rate != cfg.encodec_frame_rate
+        if self.bottleneck:
+            self.down = conv("downsample", stride=2, pad_mode="replicate")
+            self.up_w = st["upsample.conv.weight"].contiguous()
+            self.up_k = self.up_w.shape[-1]
+            if cfg.upsample_groups != cfg.hidden_size:
+                raise NotImplementedError("only a depthwise bottleneck upsample is supported")
+
+        # Quantizer: both in-projections as one GEMM, both out-projections as one.
+        sem = "quantizer.semantic_residual_vector_quantizer"
+        ac = "quantizer.acoustic_residual_vector_quantizer"
+        self.vq = cfg.vector_quantization_hidden_dimension
+        self.w_in = torch.cat([st[f"{sem}.input_proj.weight"][:, :, 0],
+                               st[f"{ac}.input_proj.weight"][:, :, 0]], 0).t().contiguous()
+        self.w_out = torch.cat([st[f"{sem}.output_proj.weight"][:, :, 0].t(),
+                                st[f"{ac}.output_proj.weight"][:, :, 0].t()], 0).contiguous()
+        n_sem = cfg.num_semantic_quantizers
+        prefixes = [f"{sem}.layers.{j}.codebook" for j in range(n_sem)]
+        prefixes += [f"{ac}.layers.{j}.codebook" for j in range(cfg.num_quantizers - n_sem)]
+        e, d = cfg.codebook_size, cfg.codebook_dim
+        self.embeds = torch.empty((len(prefixes), e, d), device=device)
+        self.embeds_t = torch.empty((len(prefixes), d, e), device=device)
+        self.norms = torch.empty((len(prefixes), e), device=device)
+        stream = torch.cuda.current_stream(device).cuda_stream
+        for j, p in enumerate(prefixes):
+            nat.call("fm_rvq_prepare_codebook", st[f"{p}.embed_sum"].contiguous().data_ptr(),
+                     st[f"{p}.cluster_usage"].contiguous().data_ptr(), e, d, 1e-5,
+                     self.embeds[j].data_ptr(), self.embeds_t[j].data_ptr(),
+                     self.norms[j].data_ptr(), stream)
+        self.workspace = torch.empty(_WORKSPACE_BYTES // 4, device=device)
+        self._rope: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
+        torch.cuda.synchronize(device)
+
+    # ------------------------------------------------------------------ ops
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _conv(self, x, B, L, layer: _Conv, flags=0, residual=None, y_len=None):
+        rows = -(-L // layer.stride)
+        y_len = rows if y_len is None else y_len
+        y = torch.empty((B, y_len, layer.c_out), device=self.device)
+        nat.call("fm_conv1d", x.data_ptr(), B, L, layer.c_in, layer.w.data_ptr(), _ptr(layer.b),
+                 layer.c_out, layer.k, layer.stride, layer.replicate, flags, _ptr(residual),
+                 y.data_ptr(), y_len, self.workspace.data_ptr(), _WORKSPACE_BYTES, self._stream())
+        return y, rows
+
+    def _convt(self, x, B, L, layer: _ConvT):
+        y = torch.empty((B, L * layer.stride, layer.c_out), device=self.device)
+        nat.call("fm_conv_transpose1d", x.data_ptr(), B, L, layer.c_in, layer.w.data_ptr(),
+                 _ptr(layer.b), layer.c_out, layer.k, layer.stride, 0, None, y.data_ptr(),
+                 self.workspace.data_ptr(), _WORKSPACE_BYTES, self._stream())
+        return y, L * layer.stride
+
+    def _linear(self, x, rows, w, flags=0, residual=None, scale=None, out=None):
+        k, n = w.shape
+        y = torch.empty((rows, n), device=self.device) if out is None else out
+        nat.call("fm_linear", x.data_ptr(), rows, k, w.data_ptr(), n, flags, _ptr(residual),
+                 _ptr(scale), y.data_ptr(), self.workspace.data_ptr(), _WORKSPACE_BYTES,
+                 self._stream())
+        return y
+
+    def _resblock(self, x, B, L, block, elu_after: bool):
+        c1, c2 = block
+        h, _ = self._conv(x, B, L, c1, nat.ELU_IN | nat.EPI_ELU)
+        flags = nat.EPI_RES_ADD | (nat.EPI_ELU if elu_after else 0)
+        y, _ = self._conv(h, B, L, c2, flags, residual=x)
+        return y
+
+    def _rope_tables(self, length):
+        tabs = self._rope.get(length)
+        if tabs is None:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("RoPE tables must be prepared before graph capture")
+            c, s = rope_tables(self.config, length)
+            tabs = (c.to(self.device), s.to(self.device))
+            self._rope[length] = tabs
+        return tabs
+
+    def prepare(self, length: int) -> None:
+        """Upload the RoPE tables a sequence of ``length`` frames needs."""
+        self._rope_tables(length)
+
+    def transformer(self, h, B, T, layers):
+        cfg = self.config
+        M = B * T
+        C = cfg.hidden_size
+        nh, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        cos, sin = self._rope_tables(T)
+        h = h.reshape(M, C)
+        xln = torch.empty((M, C), device=self.device)
+        att = torch.empty((M, nh * hd), device=self.device)
+        s = self._stream()
+        for lay in layers:
+            nat.call("fm_layer_norm", h.data_ptr(), lay.ln1[0].data_ptr(), lay.ln1[1].data_ptr(),
+                     M, C, cfg.norm_eps, xln.data_ptr(), s)
+            qkv = self._linear(xln, M, lay.wqkv)
+            ld = qkv.shape[1]
+            nat.call("fm_window_attention", qkv.data_ptr(), ld, 0, nh * hd, (nh + nkv) * hd,
+                     cos.data_ptr(), sin.data_ptr(), B, T, nh, nkv, hd, cfg.sliding_window,
+                     1.0 / (hd ** 0.5), att.data_ptr(), nh * hd, s)
+            self._linear(att, M, lay.wo, nat.EPI_RES_SCALE, residual=h, scale=lay.ls1, out=h)
+            nat.call("fm_layer_norm", h.data_ptr(), lay.ln2[0].data_ptr(), lay.ln2[1].data_ptr(),
+                     M, C, cfg.norm_eps, xln.data_ptr(), s)
+            ff = self._linear(xln, M, lay.w1, nat.EPI_GELU)
+            self._linear(ff, M, lay.w2, nat.EPI_RES_SCALE, residual=h, scale=lay.ls2, out=h)
+        return h.reshape(B, T, C)
+
+    # ------------------------------------------------------------- stages
+    def encode(self, audio: torch.Tensor, num_quantizers: int) -> torch.Tensor:
+        """``[B, C, S]`` float32 audio -> ``[B, nq, T]`` int64 codes."""
+        cfg = self.config
+        B, C, S = audio.shape
+        x = audio if C == 1 else audio.transpose(1, 2).contiguous()
+        h, L = self._conv(x, B, S, self.enc_first)
+        n = len(self.enc_stages)
+        for i, (block, down) in enumerate(self.enc_stages):
+            h = self._resblock(h, B, L, block, elu_after=True)
+            h, L = self._conv(h, B, L, down, nat.EPI_ELU if i == n - 1 else 0)
+        h, L = self._conv(h, B, L, self.enc_last)
+        h = self.transformer(h, B, L, self.enc_tf)
+        if self.bottleneck:
+            h, L = self._conv(h, B, L, self.down)
+        return self.quantize(h, B, L, num_quantizers)
+
+    def quantize(self, h, B, T, nq):
+        cfg = self.config
+        M = B * T
+        vq = self.vq
+        proj = self._linear(h.reshape(M, cfg.hidden_size), M, self.w_in)
+        codes = torch.empty((B, nq, T), dtype=torch.int64, device=self.device)
+        ws_bytes = nat.library().fm_rvq_workspace_bytes(M, vq, cfg.codebook_size)
+        ws = torch.empty((ws_bytes + 3) // 4, device=self.device)
+        n_sem = cfg.num_semantic_quantizers
+        s = self._stream()
+        branches = [(0, 0, n_sem), (vq, n_sem, nq - n_sem)]
+        for col, first, count in branches:
+            if count <= 0:
+                continue
+            nat.call("fm_rvq_encode", proj.data_ptr() + col * 4, 2 * vq, M, T, vq,
+                     cfg.codebook_size, count, self.embeds[first].data_ptr(),
+                     self.embeds_t[first].data_ptr(), self.norms[first].data_ptr(),
+                     codes.data_ptr() + first * T * 8, nq * T, ws.data_ptr(), ws_bytes, s)
+        return codes
+
+    def decode(self, codes: torch.Tensor, out_length: int | None = None) -> torch.Tensor:
+        """``[B, nq, T]`` int64 codes -> ``[B, 1, out_length]`` float32 audio."""
+        cfg = self.config
+        B, nq, T = codes.shape
+        M = B * T
+        vq = self.vq
+        q = torch.empty((M, 2 * vq), device=self.device)
+        nat.call("fm_rvq_decode", codes.data_ptr(), B, nq, T, cfg.num_semantic_quantizers,
+                 self.embeds.data_ptr(), cfg.codebook_size, vq, q.data_ptr(), self._stream())
+        h = self._linear(q, M, self.w_out).reshape(B, T, cfg.hidden_size)
+        L = T
+        if self.bottleneck:
+            up = torch.empty((B, L * 2, cfg.hidden_size), device=self.device)
+            nat.call("fm_upsample_depthwise", h.data_ptr(), B, L, cfg.hidden_size,
+                     self.up_w.data_ptr(), self.up_k, 2, up.data_ptr(), self._stream())
+            h, L = up, 2 * L
+        h = self.transformer(h, B, L, self.dec_tf)
+        h, L = self._conv(h, B, L, self.dec_first, nat.EPI_ELU)
+        n = len(self.dec_stages)
+        for i, (convt, block) in enumerate(self.dec_stages):
+            h, L = self._convt(h, B, L, convt)
+            h = self._resblock(h, B, L, block, elu_after=True)
+        full = L
+        out_length = full if out_length is None else min(out_length, full)
+        y, _ = self._conv(h, B, L, self.dec_last, y_len=out_length)
+        c_out = self.dec_last.c_out
+        if c_out == 1:
+            return y.view(B, 1, out_length)
+        return y.transpose(1, 2).contiguous()
+
+    # ------------------------------------------------------- measurement
+    def layer_op(self, name: str, batch: int, samples: int):
+        """A closure running one SEANet contraction at its real shape for a
+        ``batch x samples`` round trip (names as in ``flops.layer_table``), on
+        fixed random inputs.  Used to time a single kernel."""
+        cfg = self.config
+        specs = {}
+        L = samples
+        specs["enc.first"] = (self.enc_first, L, 0, False)
+        ch = cfg.num_filters
+        for i, r in enumerate(reversed(cfg.upsampling_ratios)):
+            (c1, c2), down = self.enc_stages[i]
+            specs[f"enc.res{ch}.c1"] = (c1, L, nat.ELU_IN | nat.EPI_ELU, False)
+            specs[f"enc.res{ch}.c2"] = (c2, L, nat.EPI_RES_ADD | nat.EPI_ELU, True)
+            specs[f"enc.down{r}"] = (down, L, 0, False)
+            L = -(-L // r)
+            ch *= 2
+        specs["enc.last"] = (self.enc_last, L, 0, False)
+        if self.bottleneck:
+            L = 2 * (-(-L // 2))
+        specs["dec.first"] = (self.dec_first, L, nat.EPI_ELU, False)
+        for i, r in enumerate(cfg.upsampling_ratios):
+            convt, (c1, c2) = self.dec_stages[i]
+            specs[f"dec.up{r}"] = (convt, L, 0, False)
+            L *= r
+            ch = convt.c_out
+            specs[f"dec.res{ch}.c1"] = (c1, L, nat.ELU_IN | nat.EPI_ELU, False)
+            specs[f"dec.res{ch}.c2"] = (c2, L, nat.EPI_RES_ADD | nat.EPI_ELU, True)
+        specs["dec.last"] = (self.dec_last, L, 0, False)
+        layer, length, flags, needs_res = specs[name]
+        g = torch.Generator(device=self.device).manual_seed(0)
+        x = torch.randn((batch, length, layer.c_in), device=self.device, generator=g)
+        if isinstance(layer, _ConvT):
+            return lambda: self._convt(x, batch, length, layer)
+        res = None
+        if needs_res:
+            res = torch.randn((batch, -(-length // layer.stride), layer.c_out), device=self.device,
+                              generator=g)
+        return lambda: self._conv(x, batch, length, layer, flags, residual=res)

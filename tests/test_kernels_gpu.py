@@ -1,0 +1,345 @@
+"""Per-kernel parity of the HIP library against float64 CPU references.
+
+Every call goes through the C ABI (``fast_mimi_amd._native``) with device
+pointers.  Floating-point kernels are held to FP32 accumulation error against
+a float64 evaluation of the same formula (the oracle's op definitions); the
+RVQ gather-sum and argmin are held to exact equality (near-ties excepted and
+reported for the argmin).
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from fast_mimi_amd import _native as nat
+from fast_mimi_amd.runtime import _Conv, _ConvT, rope_tables
+from fast_mimi_amd.config import MimiConfig
+from oracle.mimi_oracle import causal_conv1d, causal_conv_transpose1d, MimiOracle
+from rvq_check import certify, reference_rvq_rows
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+WS_BYTES = 64 << 20
+
+
+@pytest.fixture(scope="module")
+def ws():
+    return torch.empty(WS_BYTES // 4, device=DEV)
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def close(got, want, rel=2e-5):
+    """FP32-accumulation bound against a float64 result."""
+    got = got.double().cpu()
+    want = want.double().cpu()
+    scale = want.abs().max().item() + 1e-30
+    err = (got - want).abs().max().item()
+    assert err <= rel * scale, f"max err {err:.3e} vs scale {scale:.3e}"
+
+
+def run_conv(x_ncl, w, b, stride, pad_mode, flags, ws, residual_ncl=None, y_len=None):
+    B, C, L = x_ncl.shape
+    layer = _Conv(w.to(DEV), None if b is None else b.to(DEV), stride, pad_mode)
+    x = x_ncl.transpose(1, 2).contiguous().to(DEV)
+    rows = -(-L // stride)
+    y_len = rows if y_len is None else y_len
+    y = torch.empty((B, y_len, layer.c_out), device=DEV)
+    res = None if residual_ncl is None else residual_ncl.transpose(1, 2).contiguous().to(DEV)
+    nat.call("fm_conv1d", x.data_ptr(), B, L, C, layer.w.data_ptr(),
+             None if layer.b is None else layer.b.data_ptr(), layer.c_out, layer.k, stride,
+             layer.replicate, flags, None if res is None else res.data_ptr(), y.data_ptr(), y_len,
+             ws.data_ptr(), WS_BYTES, stream())
+    torch.cuda.synchronize()
+    return y.cpu().transpose(1, 2)
+
+
+CONV_CASES = [
+    # B, Cin, Cout, k, stride, L
+    (1, 1, 64, 7, 1, 1000),
+    (2, 64, 32, 3, 1, 777),
+    (1, 32, 64, 1, 1, 513),
+    (2, 64, 128, 8, 4, 1001),
+    (1, 128, 256, 10, 5, 303),
+    (1, 256, 512, 12, 6, 121),
+    (1, 512, 1024, 16, 8, 250),     # split-K path (small M, K = 8192)
+    (1, 1024, 512, 3, 1, 250),
+    (3, 64, 1, 3, 1, 999),          # Cout = 1
+    (2, 2, 4, 4, 2, 9),             # tiny channels, scalar loads
+    (1, 4, 2, 3, 1, 1),             # length 1
+    (1, 16, 16, 4, 2, 5),
+]
+
+
+@pytest.mark.parametrize("B,cin,cout,k,stride,L", CONV_CASES)
+def test_conv1d(B, cin, cout, k, stride, L, ws):
+    g = torch.Generator().manual_seed(B * 1000 + cin + cout + k + L)
+    x = torch.randn(B, cin, L, generator=g)
+    w = torch.randn(cout, cin, k, generator=g) / math.sqrt(cin * k)
+    b = torch.randn(cout, generator=g) * 0.1
+    got = run_conv(x, w, b, stride, "constant", 0, ws)
+    want = causal_conv1d(x.double(), w.double(), b.double(), stride)
+    assert got.shape == want.shape
+    close(got, want)
+
+
+@pytest.mark.parametrize("B,L", [(1, 250), (2, 7), (1, 1), (3, 64)])
+def test_conv1d_replicate(B, L, ws):
+    g = torch.Generator().manual_seed(L)
+    x = torch.randn(B, 64, L, generator=g)
+    w = torch.randn(64, 64, 4, generator=g) / 16
+    got = run_conv(x, w, None, 2, "replicate", 0, ws)
+    want = causal_conv1d(x.double(), w.double(), None, 2, pad_mode="replicate")
+    close(got, want)
+
+
+def test_conv1d_fused_resblock_epilogues(ws):
+    """ELU-on-load + k3 conv + ELU, then 1x1 conv + residual add + ELU."""
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 64, 300, generator=g)
+    w1 = torch.randn(32, 64, 3, generator=g) / 14
+    b1 = torch.randn(32, generator=g) * 0.1
+    w2 = torch.randn(64, 32, 1, generator=g) / 6
+    b2 = torch.randn(64, generator=g) * 0.1
+    h = run_conv(x, w1, b1, 1, "constant", nat.ELU_IN | nat.EPI_ELU, ws)
+    xd = x.double()
+    want_h = F.elu(causal_conv1d(F.elu(xd), w1.double(), b1.double()))
+    close(h, want_h)
+    y = run_conv(h.contiguous(), w2, b2, 1, "constant", nat.EPI_RES_ADD | nat.EPI_ELU, ws, residual_ncl=x)
+    want = F.elu(xd + causal_conv1d(want_h, w2.double(), b2.double()))
+    close(y, want, rel=5e-5)
+
+
+def test_conv1d_crop(ws):
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 8, 100, generator=g)
+    w = torch.randn(1, 8, 3, generator=g)
+    b = torch.randn(1, generator=g)
+    got = run_conv(x, w, b, 1, "constant", 0, ws, y_len=93)
+    want = causal_conv1d(x.double(), w.double(), b.double())[..., :93]
+    close(got, want)
+
+
+@pytest.mark.parametrize("B,cin,cout,stride,L", [
+    (1, 1024, 512, 8, 250), (2, 512, 256, 6, 40), (1, 256, 128, 5, 300),
+    (1, 128, 64, 4, 1000), (1, 4, 2, 2, 7), (2, 8, 4, 2, 1)])
+def test_conv_transpose1d(B, cin, cout, stride, L, ws):
+    g = torch.Generator().manual_seed(cin + L)
+    x = torch.randn(B, cin, L, generator=g)
+    w = torch.randn(cin, cout, 2 * stride, generator=g) / math.sqrt(cin)
+    b = torch.randn(cout, generator=g) * 0.1
+    layer = _ConvT(w.to(DEV), b.to(DEV), stride)
+    xd = x.transpose(1, 2).contiguous().to(DEV)
+    y = torch.empty((B, L * stride, cout), device=DEV)
+    nat.call("fm_conv_transpose1d", xd.data_ptr(), B, L, cin, layer.w.data_ptr(), layer.b.data_ptr(),
+             cout, 2 * stride, stride, 0, None, y.data_ptr(), ws.data_ptr(), WS_BYTES, stream())
+    torch.cuda.synchronize()
+    want = causal_conv_transpose1d(x.double(), w.double(), b.double(), stride)
+    close(y.cpu().transpose(1, 2), want)
+
+
+def run_linear(x, w_t, flags=0, res=None, scale=None, ws=None, out=None):
+    rows, k = x.shape
+    n = w_t.shape[1]
+    y = torch.empty((rows, n), device=DEV) if out is None else out
+    nat.call("fm_linear", x.data_ptr(), rows, k, w_t.data_ptr(), n, flags,
+             None if res is None else res.data_ptr(), None if scale is None else scale.data_ptr(),
+             y.data_ptr(), ws.data_ptr(), WS_BYTES, stream())
+    torch.cuda.synchronize()
+    return y
+
+
+@pytest.mark.parametrize("rows,k,n", [(250, 512, 1536), (4000, 512, 2048), (250, 2048, 512),
+                                      (1, 512, 512), (37, 16, 48), (125, 512, 512)])
+def test_linear_epilogues(rows, k, n, ws):
+    g = torch.Generator().manual_seed(rows + k + n)
+    x = torch.randn(rows, k, generator=g)
+    w = torch.randn(n, k, generator=g) * 0.05
+    xd, wd = x.to(DEV), w.t().contiguous().to(DEV)
+    close(run_linear(xd, wd, ws=ws).cpu(), x.double() @ w.double().t())
+    close(run_linear(xd, wd, nat.EPI_GELU, ws=ws).cpu(), F.gelu(x.double() @ w.double().t()))
+    res = torch.randn(rows, n, generator=g)
+    scale = torch.rand(n, generator=g) * 0.1
+    h = res.to(DEV)
+    run_linear(xd, wd, nat.EPI_RES_SCALE, res=h, scale=scale.to(DEV), ws=ws, out=h)  # in place
+    close(h.cpu(), res.double() + scale.double() * (x.double() @ w.double().t()))
+
+
+@pytest.mark.parametrize("rows,c", [(250, 512), (1, 512), (33, 16), (4000, 512)])
+def test_layer_norm(rows, c):
+    g = torch.Generator().manual_seed(rows)
+    x = torch.randn(rows, c, generator=g) * 3 + 1
+    w = torch.rand(c, generator=g) + 0.5
+    b = torch.randn(c, generator=g)
+    xd, y = x.to(DEV), torch.empty(rows, c, device=DEV)
+    wd, bd = w.to(DEV), b.to(DEV)  # keep device copies alive across the call
+    nat.call("fm_layer_norm", xd.data_ptr(), wd.data_ptr(), bd.data_ptr(), rows, c,
+             1e-5, y.data_ptr(), stream())
+    torch.cuda.synchronize()
+    close(y.cpu(), F.layer_norm(x.double(), (c,), w.double(), b.double(), 1e-5))
+
+
+def attention_reference(qkv, B, T, H, D, window, cos, sin):
+    """float64 RoPE + causal window softmax attention, the oracle's formulas."""
+    q, k, v = qkv.double().view(B, T, 3, H, D).unbind(2)
+    q, k, v = (t.transpose(1, 2) for t in (q, k, v))
+    c, s = cos.double()[None, None], sin.double()[None, None]
+    rot = MimiOracle._rotate_half
+    q = q * c + rot(q) * s
+    k = k * c + rot(k) * s
+    i = torch.arange(T)
+    allowed = (i[None, :] <= i[:, None]) & (i[None, :] > i[:, None] - window)
+    scores = (q @ k.transpose(-1, -2)) / math.sqrt(D)
+    scores = scores.masked_fill(~allowed, float("-inf"))
+    o = torch.softmax(scores, -1) @ v
+    return o.transpose(1, 2).reshape(B * T, H * D)
+
+
+@pytest.mark.parametrize("B,T,H,D,window", [(1, 250, 8, 64, 250), (1, 251, 8, 64, 250),
+                                            (2, 700, 8, 64, 250), (1, 1, 8, 64, 250),
+                                            (16, 125, 8, 64, 250), (2, 18, 2, 8, 8)])
+def test_window_attention(B, T, H, D, window):
+    g = torch.Generator().manual_seed(T + H)
+    qkv = torch.randn(B * T, 3 * H * D, generator=g)
+    cfg = MimiConfig(head_dim=D, hidden_size=H * D, num_attention_heads=H, num_key_value_heads=H)
+    cos, sin = rope_tables(cfg, T)
+    out = torch.empty(B * T, H * D, device=DEV)
+    qkv_d, cos_d, sin_d = qkv.to(DEV), cos.to(DEV), sin.to(DEV)
+    nat.call("fm_window_attention", qkv_d.data_ptr(), 3 * H * D, 0, H * D, 2 * H * D,
+             cos_d.data_ptr(), sin_d.data_ptr(), B, T, H, H, D, window,
+             1.0 / math.sqrt(D), out.data_ptr(), H * D, stream())
+    torch.cuda.synchronize()
+    close(out.cpu(), attention_reference(qkv, B, T, H, D, window, cos, sin), rel=5e-5)
+
+
+def prepare_codebooks(embed_sum, usage):
+    n, e, d = embed_sum.shape
+    emb = torch.empty(n, e, d, device=DEV)
+    emb_t = torch.empty(n, d, e, device=DEV)
+    norms = torch.empty(n, e, device=DEV)
+    es_d, us_d = embed_sum.to(DEV).contiguous(), usage.to(DEV).contiguous()
+    for j in range(n):
+        nat.call("fm_rvq_prepare_codebook", es_d[j].data_ptr(),
+                 us_d[j].data_ptr(), e, d, 1e-5, emb[j].data_ptr(),
+                 emb_t[j].data_ptr(), norms[j].data_ptr(), stream())
+    return emb, emb_t, norms
+
+
+def rvq_encode_gpu(x, emb, emb_t, norms, T, nq):
+    M, d = x.shape
+    e = emb.shape[1]
+    B = M // T
+    codes = torch.empty(B, nq, T, dtype=torch.int64, device=DEV)
+    wsb = nat.library().fm_rvq_workspace_bytes(M, d, e)
+    ws = torch.empty((wsb + 3) // 4, device=DEV)
+    xd = x.to(DEV).contiguous()
+    nat.call("fm_rvq_encode", xd.data_ptr(), d, M, T, d, e, nq, emb.data_ptr(), emb_t.data_ptr(),
+             norms.data_ptr(), codes.data_ptr(), nq * T, ws.data_ptr(), wsb, stream())
+    torch.cuda.synchronize()
+    return codes.cpu()
+
+
+def rvq_encode_oracle(x, embeds, T):
+    """The reference's residual loop (model.py:2408-2428) on flat rows."""
+    residual = x.clone()
+    out = []
+    for e in embeds:
+        idx = MimiOracle.nearest(residual, e)
+        out.append(idx)
+        residual = residual - F.embedding(idx, e)
+    codes = torch.stack(out)  # [nq, M]
+    nq, M = codes.shape
+    return codes.view(nq, M // T, T).transpose(0, 1)
+
+
+@pytest.mark.parametrize("B,T,nq", [(1, 125, 8), (4, 63, 7), (64, 125, 32), (1, 1, 3)])
+def test_rvq_encode_matches_reference_loop(B, T, nq):
+    g = torch.Generator().manual_seed(B * T + nq)
+    e, d = 2048, 256
+    embed_sum = torch.randn(nq, e, d, generator=g) / 16
+    usage = torch.ones(nq, e)
+    x = torch.randn(B * T, d, generator=g) * 0.3
+    emb, emb_t, norms = prepare_codebooks(embed_sum, usage)
+    got = rvq_encode_gpu(x, emb, emb_t, norms, T, nq)
+    embeds = [embed_sum[j] / usage[j].clamp(min=1e-5)[:, None] for j in range(nq)]
+    want = rvq_encode_oracle(x, embeds, T)
+    flat = want.transpose(0, 1).reshape(nq, B * T)
+    n, worst = certify(reference_rvq_rows(x, embeds, flat), embeds, got, want)
+    # Near-ties within FP32 summation-order noise are certified; report them.
+    print(f"rvq B={B} T={T} nq={nq}: {n} certified near-tie rows (worst gap {worst:.2e})")
+    assert n <= max(2, B * T * nq // 2000)
+
+
+def test_rvq_tie_picks_lowest_index():
+    e, d = 256, 256
+    g = torch.Generator().manual_seed(9)
+    base = torch.randn(e, d, generator=g) / 16
+    base[200] = base[17]  # exact duplicate entries: distance ties
+    base[255] = base[17]
+    x = base[17:18].repeat(64, 1) + 1e-3 * torch.randn(64, d, generator=g)
+    emb, emb_t, norms = prepare_codebooks(base[None], torch.ones(1, e))
+    got = rvq_encode_gpu(x, emb, emb_t, norms, 64, 1)
+    want = rvq_encode_oracle(x, [base], 64)
+    assert torch.equal(got, want)
+    assert (got == 17).all()
+
+
+def test_rvq_prepare_divides_by_clamped_usage():
+    g = torch.Generator().manual_seed(4)
+    es = torch.randn(1, 64, 32, generator=g)
+    usage = torch.rand(1, 64, generator=g) + 0.5
+    usage[0, 3] = 0.0  # clamps to 1e-5
+    emb, emb_t, _ = prepare_codebooks(es, usage)
+    want = es[0] / usage[0].clamp(min=1e-5)[:, None]
+    assert torch.equal(emb[0].cpu(), want)
+    assert torch.equal(emb_t[0].cpu(), want.t())
+
+
+@pytest.mark.parametrize("B,nq,T,nsem", [(1, 8, 125, 1), (2, 32, 13, 1), (3, 1, 5, 1), (1, 4, 3, 1)])
+def test_rvq_decode_gather_sum_is_exact(B, nq, T, nsem):
+    g = torch.Generator().manual_seed(nq * T)
+    e, d = 2048, 256
+    embeds = torch.randn(nq, e, d, generator=g) / 16
+    codes = torch.randint(0, e, (B, nq, T), generator=g)
+    out = torch.empty(B * T, 2 * d, device=DEV)
+    codes_d, embeds_d = codes.to(DEV), embeds.to(DEV)
+    nat.call("fm_rvq_decode", codes_d.data_ptr(), B, nq, T, nsem, embeds_d.data_ptr(),
+             e, d, out.data_ptr(), stream())
+    torch.cuda.synchronize()
+    # Reference order (model.py:2439-2441): float32 zero, then codebooks left to right.
+    sem = torch.zeros(())
+    for j in range(nsem):
+        sem = sem + F.embedding(codes[:, j], embeds[j])
+    ac = torch.zeros(())
+    for j in range(nsem, nq):
+        ac = ac + F.embedding(codes[:, j], embeds[j])
+    got = out.cpu().view(B, T, 2 * d)
+    assert torch.equal(got[..., :d], sem.expand(B, T, d))
+    assert torch.equal(got[..., d:], ac.expand(B, T, d))
+
+
+@pytest.mark.parametrize("B,L,C", [(1, 125, 512), (3, 7, 16), (2, 1, 512)])
+def test_upsample_depthwise(B, L, C):
+    g = torch.Generator().manual_seed(L)
+    x = torch.randn(B, C, L, generator=g)
+    w = torch.randn(C, 1, 4, generator=g)
+    y = torch.empty(B, 2 * L, C, device=DEV)
+    x_d, w_d = x.transpose(1, 2).contiguous().to(DEV), w.to(DEV)
+    nat.call("fm_upsample_depthwise", x_d.data_ptr(), B, L, C, w_d.data_ptr(), 4, 2, y.data_ptr(),
+             stream())
+    torch.cuda.synchronize()
+    want = causal_conv_transpose1d(x.double(), w.double(), None, 2, groups=C)
+    close(y.cpu().transpose(1, 2), want, rel=1e-6)
+
+
+def test_bad_arguments_are_rejected():
+    with pytest.raises(nat.NativeError, match="bad argument"):
+        nat.call("fm_layer_norm", None, None, None, 4, 8, 1e-5, None, stream())
+    with pytest.raises(nat.NativeError, match="unsupported"):
+        nat.call("fm_window_attention", 1, 8, 0, 0, 0, 1, 1, 1, 1, 1, 1, 12, 8, 1.0, 1, 8, stream())
