@@ -3,6 +3,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <climits>
+#include <algorithm>
 
 #define FM_DEVICE __device__ __forceinline__
 

@@ -9,7 +9,24 @@
 // reads the contiguous run x[b, t*rs - padL : t*rs - padL + K/C_in, :], which
 // in channels-last memory is K consecutive floats.  Positions outside [0, L)
 // read zero (causal / stride-alignment padding) or clamp to the edge
-// (replicate padding).  B is the packed weight [K, N] (row-major).
+// (replicate padding).  B is the packed weight W^T [N, K] (k contiguous).
+//
+// Fast kernel (C_in and K multiples of 4): both operands are staged in LDS
+// k-contiguous (row pitch BK + 4 floats) with 16-byte writes, double-buffered.
+// The MFMA k-slot of lane half h at step 4q+e carries k = (BK/2)h + 4q + e,
+// so every lane fetches its A and B fragments for four MFMAs with one 16-byte
+// LDS read each.  Tiles (256 threads; k-tile BK = 64 for the large tiles so a
+// k-tile's MFMA work outlasts the next tile's global-load latency):
+//   128x128 (2x2 waves of 64x64), 128x64 (4x1 of 32x64), 128x32 (4x1 of 32x32);
+//   32x64 with the four waves splitting K (summed through LDS in wave order)
+//   when the large tiles cannot fill the GPU, plus global K-splits summed in
+//   split order by a second kernel for very long K.  All sums are in a fixed
+//   order, so results are deterministic.
+// Blocks are renumbered so consecutive tiles of one row band land on one XCD
+// (dispatch assigns block i to XCD i % 8), keeping the band's A rows in that
+// XCD's L2.
+// A scalar generic kernel covers the remaining shapes (C_in or K not a
+// multiple of 4: the 1-channel first convolution and tiny test configs).
 
 #include "fm_common.h"
 
@@ -17,173 +34,152 @@ namespace {
 
 struct GemmArgs {
   const float* x;
-  const float* w;
+  const float* w;  // W^T [N][K]
   const float* bias;
   const float* res;
   const float* scale;
   float* y;
-  float* partial;
+  float* partial;  // global split-K partials [splits][M][N], or null
   int batch, L_in, C_in, rows, rs, padL, K, N, y_rows, bias_len, k_split, flags;
 };
 
-constexpr int BK = 32;
+constexpr int KT = 32;  // k granularity of K-splits (every tile's BK divides it or is 64)
+constexpr int NTHREADS = 256;
 
-FM_DEVICE float epilogue(float v, long m, int n, const GemmArgs& p) {
-  if (p.bias) v = __fadd_rn(v, p.bias[n % p.bias_len]);
-  if (p.flags & FM_EPI_RES_ADD) v = __fadd_rn(p.res[m * p.N + n], v);
-  if (p.flags & FM_EPI_RES_SCALE) v = __fadd_rn(p.res[m * p.N + n], __fmul_rn(p.scale[n], v));
-  if (p.flags & FM_EPI_ELU) v = fm_elu(v);
-  if (p.flags & FM_EPI_GELU) v = fm_gelu(v);
+FM_DEVICE float epilogue_v(float v, float bias, float res, float scale, int flags) {
+  v = __fadd_rn(v, bias);
+  if (flags & FM_EPI_RES_ADD) v = __fadd_rn(res, v);
+  if (flags & FM_EPI_RES_SCALE) v = __fadd_rn(res, __fmul_rn(scale, v));
+  if (flags & FM_EPI_ELU) v = fm_elu(v);
+  if (flags & FM_EPI_GELU) v = fm_gelu(v);
   return v;
 }
 
+// Epilogue for one output element (generic kernel and split-K reduction).
 FM_DEVICE void store_out(float acc, long m, int n, const GemmArgs& p) {
-  const long b = m / p.rows;
-  const long t = m - b * p.rows;
-  if (t < p.y_rows) p.y[(b * p.y_rows + t) * p.N + n] = epilogue(acc, m, n, p);
+  const float bias = p.bias ? p.bias[n % p.bias_len] : 0.0f;
+  const float scale = (p.flags & FM_EPI_RES_SCALE) ? p.scale[n] : 0.0f;
+  const float res = (p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE)) ? p.res[m * p.N + n] : 0.0f;
+  const float v = epilogue_v(acc, bias, res, scale, p.flags);
+  if (p.y_rows == p.rows) {
+    p.y[m * p.N + n] = v;
+  } else {
+    const int b = (int)(m / p.rows);
+    const int t = (int)(m - (long)b * p.rows);
+    if (t < p.y_rows) p.y[((long)b * p.y_rows + t) * p.N + n] = v;
+  }
 }
 
-template <int BM, int BN, int WM, int WN, int VA, int VB>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs p) {
-  constexpr int NT = 64 * WM * WN;
+// Block -> tile, grouping a row band's tiles on one XCD.
+FM_DEVICE int tile_index() {
+  const int nb = gridDim.x;
+  const int b = blockIdx.x;
+  if (nb % 8) return b;
+  return (b % 8) * (nb / 8) + b / 8;
+}
+
+// ---------------------------------------------------------------------------
+// Fast kernel.  WK > 1: the waves form WK groups of WM*WN waves; group g takes
+// k-tiles g, g + WK, ... and the groups' accumulators are summed in order.
+template <int BM, int BN, int WM, int WN, int WK, int BK>
+__global__ __launch_bounds__(NTHREADS) void gemm_fast_kernel(GemmArgs p) {
+  static_assert(64 * WM * WN * WK == NTHREADS, "256 threads per block");
+  constexpr int GT = 64 * WM * WN;  // threads per k-group
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 32, FN = WTN / 32;
-  constexpr int PA = BM + 1;  // As[k][m]: odd pitch keeps transposed writes conflict-light
-  constexpr int PB = BN + 4;  // Bs[k][n]: 16-byte aligned rows
-  constexpr int ACH = BM * BK / VA;  // A load chunks per tile
-  constexpr int BCH = BK * BN / VB;
-  constexpr int APT = (ACH + NT - 1) / NT;
-  constexpr int BPT = (BCH + NT - 1) / NT;
-  static_assert(FM >= 1 && FN >= 1, "wave tile must hold a 32x32 block");
+  constexpr int P = BK + 4;             // LDS row pitch (floats)
+  constexpr int CPR = BK / 4;            // float4 chunks per tile row
+  constexpr int HK = BK / 2;             // k values per MFMA lane half
+  constexpr int APT = BM * BK / 4 / GT;  // float4 A chunks per thread per k-tile
+  constexpr int BPT = BN * BK / 4 / GT;
+  constexpr int STAGE = (BM + BN) * P;   // floats per stage
+  static_assert(APT >= 1 && BPT >= 1 && APT * GT * 4 == BM * BK && BPT * GT * 4 == BN * BK, "tiling");
+  static_assert(WK == 1 || 2 * STAGE * WK >= (WK - 1) * BM * BN, "LDS reduction fits the stages");
 
-  __shared__ float As[BK * PA];
-  __shared__ float Bs[BK * PB];
+  __shared__ __attribute__((aligned(16))) float smem[2 * STAGE * WK];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm0 = (wave / WN) * WTM;
-  const int wn0 = (wave % WN) * WTN;
+  const int group = wave / (WM * WN);
+  const int gtid = tid - group * GT;
+  const int gwave = wave - group * WM * WN;
+  const int wm0 = (gwave / WN) * WTM;
+  const int wn0 = (gwave % WN) * WTN;
+  float* gsm = smem + group * 2 * STAGE;
 
   const long M = (long)p.batch * p.rows;
   const int tiles_n = (p.N + BN - 1) / BN;
-  const int tile = blockIdx.x;
+  const int tile = tile_index();
   const long m0 = (long)(tile / tiles_n) * BM;
   const int n0 = (tile % tiles_n) * BN;
   const int k_begin = blockIdx.y * p.k_split;
   const int k_end = min(p.K, k_begin + p.k_split);
+  const bool replicate = p.flags & FM_REPLICATE;
+  const bool tap_uniform = (p.C_in % BK) == 0;  // a k-tile never straddles two positions
 
-  // Per-chunk row descriptors (fixed across the K loop).
-  long a_off[APT];   // element offset of (b, p0) in x, p0 = first window position
-  int a_p0[APT];     // first window position, -1e9 when the row is out of range
-  int a_bL[APT];     // b * L_in
-  int a_r[APT], a_k[APT];
+  // Chunk c of a tile: row c / CPR, k offset 4 * (c % CPR).
+  const int ck = (gtid % CPR) * 4;
+  const float* a_base[APT];  // x + (b*L + p0) * C_in (valid rows), else null
+  int a_p0[APT], a_bL[APT];
 #pragma unroll
   for (int i = 0; i < APT; ++i) {
-    const int c = tid + i * NT;
-    const int r = c / (BK / VA);
-    const int kq = c % (BK / VA);
-    a_r[i] = r;
-    a_k[i] = kq * VA;
-    const long m = m0 + r;
-    if (c < ACH && m < M) {
-      const long b = m / p.rows;
-      const long t = m - b * p.rows;
-      const int p0 = (int)(t * p.rs - p.padL);
-      a_p0[i] = p0;
-      a_bL[i] = (int)(b * p.L_in);
-      a_off[i] = ((long)b * p.L_in + p0) * p.C_in;
-    } else {
-      a_p0[i] = -1000000000;
-      a_bL[i] = 0;
-      a_off[i] = 0;
+    const long m = m0 + gtid / CPR + i * (GT / CPR);
+    a_base[i] = nullptr;
+    a_p0[i] = 0;
+    a_bL[i] = 0;
+    if (m < M) {
+      const int b = (int)(m / p.rows);
+      const int t = (int)(m - (long)b * p.rows);
+      a_p0[i] = t * p.rs - p.padL;
+      a_bL[i] = b * p.L_in;
+      a_base[i] = p.x + ((long)b * p.L_in + a_p0[i]) * p.C_in;
     }
   }
+  const float* b_base[BPT];
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) {
+    const int n = n0 + gtid / CPR + i * (GT / CPR);
+    b_base[i] = n < p.N ? p.w + (long)n * p.K : nullptr;
+  }
 
-  float ra[APT][VA];
-  float rb[BPT][VB];
-
-  auto load_a = [&](int k0) {
+  floatx4 ra[APT], rb[BPT];
+  auto load = [&](int k0) {
+    const int kg = k0 + ck;
+    const bool kok = kg < k_end;
+    const int tap = tap_uniform ? k0 / p.C_in : kg / p.C_in;
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
-      const int kg = k0 + a_k[i];
-      bool ok = a_p0[i] > -1000000000 && kg < k_end;
-      int pos = 0;
-      if (ok) {
-        pos = a_p0[i] + kg / p.C_in;
-        if (p.flags & FM_REPLICATE) {
+      ra[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (a_base[i] && kok) {
+        int pos = a_p0[i] + tap;
+        if (replicate) {
           pos = min(max(pos, 0), p.L_in - 1);
-        } else {
-          ok = pos >= 0 && pos < p.L_in;
+          ra[i] = *reinterpret_cast<const floatx4*>(p.x + ((long)a_bL[i] + pos) * p.C_in + (kg % p.C_in));
+        } else if (pos >= 0 && pos < p.L_in) {
+          ra[i] = *reinterpret_cast<const floatx4*>(a_base[i] + kg);
         }
-      }
-      if (ok) {
-        const float* src = (p.flags & FM_REPLICATE)
-                               ? p.x + ((long)a_bL[i] + pos) * p.C_in + (kg % p.C_in)
-                               : p.x + a_off[i] + kg;
-        if constexpr (VA == 4) {
-          const floatx4 v = *reinterpret_cast<const floatx4*>(src);
-          ra[i][0] = v.x; ra[i][1] = v.y; ra[i][2] = v.z; ra[i][3] = v.w;
-        } else {
-          ra[i][0] = *src;
-        }
-        if (p.flags & FM_ELU_IN) {
-#pragma unroll
-          for (int j = 0; j < VA; ++j) ra[i][j] = fm_elu(ra[i][j]);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < VA; ++j) ra[i][j] = 0.0f;
       }
     }
-  };
-
-  auto load_b = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < BPT; ++i) {
-      const int c = tid + i * NT;
-      const int kr = c / (BN / VB);
-      const int nn = (c % (BN / VB)) * VB;
-      const int kg = k0 + kr;
-      const int n = n0 + nn;
-      if (c < BCH && kg < k_end && n < p.N) {
-        const float* src = p.w + (long)kg * p.N + n;
-        if constexpr (VB == 4) {
-          const floatx4 v = *reinterpret_cast<const floatx4*>(src);
-          rb[i][0] = v.x; rb[i][1] = v.y; rb[i][2] = v.z; rb[i][3] = v.w;
-        } else {
-          rb[i][0] = *src;
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < VB; ++j) rb[i][j] = 0.0f;
-      }
+      rb[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (b_base[i] && kok) rb[i] = *reinterpret_cast<const floatx4*>(b_base[i] + kg);
     }
   };
-
-  auto store_lds = [&]() {
+  auto store = [&](int stage) {
+    float* As = gsm + stage * STAGE;
+    float* Bs = As + BM * P;
+    const bool elu = p.flags & FM_ELU_IN;
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
-      const int c = tid + i * NT;
-      if (c < ACH) {
-#pragma unroll
-        for (int j = 0; j < VA; ++j) As[(a_k[i] + j) * PA + a_r[i]] = ra[i][j];
-      }
+      floatx4 v = ra[i];
+      if (elu) v = floatx4{fm_elu(v.x), fm_elu(v.y), fm_elu(v.z), fm_elu(v.w)};
+      *reinterpret_cast<floatx4*>(As + (gtid / CPR + i * (GT / CPR)) * P + ck) = v;
     }
 #pragma unroll
-    for (int i = 0; i < BPT; ++i) {
-      const int c = tid + i * NT;
-      if (c < BCH) {
-        const int kr = c / (BN / VB);
-        const int nn = (c % (BN / VB)) * VB;
-        if constexpr (VB == 4) {
-          floatx4 v = {rb[i][0], rb[i][1], rb[i][2], rb[i][3]};
-          *reinterpret_cast<floatx4*>(&Bs[kr * PB + nn]) = v;
-        } else {
-          Bs[kr * PB + nn] = rb[i][0];
-        }
-      }
-    }
+    for (int i = 0; i < BPT; ++i)
+      *reinterpret_cast<floatx4*>(Bs + (gtid / CPR + i * (GT / CPR)) * P + ck) = rb[i];
   };
 
   floatx16 acc[FM][FN];
@@ -194,49 +190,192 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  if (k_begin < k_end) load_a(k_begin), load_b(k_begin);
-  const int lrow = lane >> 5;
+  const int h = lane >> 5;
   const int lcol = lane & 31;
-  for (int k0 = k_begin; k0 < k_end; k0 += BK) {
-    __syncthreads();
-    store_lds();
-    __syncthreads();
-    if (k0 + BK < k_end) {
-      load_a(k0 + BK);
-      load_b(k0 + BK);
+  const int ktiles = (k_end - k_begin + BK - 1) / BK;
+  const int rounds = (ktiles + WK - 1) / WK;
+  int kq = k_begin + group * BK;
+  if (rounds > 0) {
+    load(kq);
+    store(0);
+  }
+  for (int q = 0; q < rounds; ++q) {
+    const int cur = q & 1;
+    __syncthreads();  // stage `cur` is complete; stage `cur ^ 1` is free
+    const int knext = kq + WK * BK;
+    if (q + 1 < rounds) load(knext);
+    if (kq < k_end) {
+      const float* As = gsm + cur * STAGE;
+      const float* Bs = As + BM * P;
+#pragma unroll
+      for (int s4 = 0; s4 < BK / 8; ++s4) {
+        floatx4 a[FM], b[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          a[i] = *reinterpret_cast<const floatx4*>(As + (wm0 + i * 32 + lcol) * P + h * HK + s4 * 4);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          b[j] = *reinterpret_cast<const floatx4*>(Bs + (wn0 + j * 32 + lcol) * P + h * HK + s4 * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = fm_mfma32(a[i][e], b[j][e], acc[i][j]);
+      }
     }
-#pragma unroll
-    for (int kk = 0; kk < BK; kk += 2) {
-      float a[FM], b[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i) a[i] = As[(kk + lrow) * PA + wm0 + i * 32 + lcol];
-#pragma unroll
-      for (int j = 0; j < FN; ++j) b[j] = Bs[(kk + lrow) * PB + wn0 + j * 32 + lcol];
+    if (q + 1 < rounds) store(cur ^ 1);
+    kq = knext;
+  }
+
+  if constexpr (WK > 1) {
+    // Groups 1..WK-1 park their tiles in LDS; group 0 adds them in order.
+    __syncthreads();
+    if (group > 0) {
+      float* red = smem + (group - 1) * BM * BN;
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = fm_mfma32(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            red[(wm0 + i * 32 + fm_mfma32_row(r, lane)) * BN + wn0 + j * 32 + lcol] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (group > 0) return;
+#pragma unroll
+    for (int g = 1; g < WK; ++g) {
+      const float* red = smem + (g - 1) * BM * BN;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            acc[i][j][r] = __fadd_rn(acc[i][j][r],
+                                     red[(wm0 + i * 32 + fm_mfma32_row(r, lane)) * BN + wn0 + j * 32 + lcol]);
     }
   }
 
+  if (p.partial) {
+    float* dst = p.partial + (long)blockIdx.y * M * p.N;
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn0 + j * 32 + lcol;
+      if (n >= p.N) continue;
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const long m = m0 + wm0 + i * 32 + fm_mfma32_row(r, lane);
+          if (m < M) dst[m * p.N + n] = acc[i][j][r];
+        }
+    }
+    return;
+  }
+  const bool crop = p.y_rows != p.rows;
+  const bool has_res = p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE);
+  // Residual loads first (all in flight together), then compute and store.
+  float rv[FN][FM][16];
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        rv[j][i][r] = 0.0f;
+        if (has_res) {
+          const long m = min(m0 + wm0 + i * 32 + fm_mfma32_row(r, lane), M - 1);
+          const int n = min(n0 + wn0 + j * 32 + lcol, p.N - 1);
+          rv[j][i][r] = p.res[m * p.N + n];
+        }
+      }
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int n = n0 + wn0 + j * 32 + lcol;
+    const int nc = min(n, p.N - 1);
+    const float bias = p.bias ? p.bias[nc % p.bias_len] : 0.0f;
+    const float scale = (p.flags & FM_EPI_RES_SCALE) ? p.scale[nc] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const long m = m0 + wm0 + i * 32 + fm_mfma32_row(r, lane);
-        const int n = n0 + wn0 + j * 32 + lcol;
-        if (m < M && n < p.N) {
-          if (p.partial)
-            p.partial[((long)blockIdx.y * M + m) * p.N + n] = acc[i][j][r];
-          else
-            store_out(acc[i][j][r], m, n, p);
+        const float v = epilogue_v(acc[i][j][r], bias, rv[j][i][r], scale, p.flags);
+        if (m >= M || n >= p.N) continue;
+        if (!crop) {
+          p.y[m * p.N + n] = v;
+        } else {
+          const int b = (int)(m / p.rows);
+          const int t = (int)(m - (long)b * p.rows);
+          if (t < p.y_rows) p.y[((long)b * p.y_rows + t) * p.N + n] = v;
         }
       }
+  }
 }
 
-// Sums split-K partials in split order and applies the epilogue.
+// ---------------------------------------------------------------------------
+// Generic kernel: 64x64 tiles, one output element pair per thread per step,
+// scalar loads.  Used only when C_in or K is not a multiple of 4.
+__global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
+  constexpr int TM = 64, TN = 64, TK = 16;
+  __shared__ float As[TK][TM + 1];
+  __shared__ float Bs[TK][TN + 1];
+  const long M = (long)p.batch * p.rows;
+  const int tiles_n = (p.N + TN - 1) / TN;
+  const long m0 = (long)(blockIdx.x / tiles_n) * TM;
+  const int n0 = (blockIdx.x % tiles_n) * TN;
+  const int k_begin = blockIdx.y * p.k_split;
+  const int k_end = min(p.K, k_begin + p.k_split);
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;  // 16 x 16 threads, 4 x 4 outputs each
+  float acc[4][4] = {};
+  for (int k0 = k_begin; k0 < k_end; k0 += TK) {
+    for (int e = threadIdx.x; e < TK * TM; e += 256) {
+      const int r = e / TK, kk = e % TK;
+      const long m = m0 + r;
+      const int kg = k0 + kk;
+      float v = 0.0f;
+      if (m < M && kg < k_end) {
+        const int b = (int)(m / p.rows);
+        const int t = (int)(m - (long)b * p.rows);
+        int pos = t * p.rs - p.padL + kg / p.C_in;
+        bool ok = true;
+        if (p.flags & FM_REPLICATE) pos = min(max(pos, 0), p.L_in - 1);
+        else ok = pos >= 0 && pos < p.L_in;
+        if (ok) v = p.x[((long)b * p.L_in + pos) * p.C_in + kg % p.C_in];
+        if (p.flags & FM_ELU_IN) v = fm_elu(v);
+      }
+      As[kk][r] = v;
+    }
+    for (int e = threadIdx.x; e < TK * TN; e += 256) {
+      const int c = e / TK, kk = e % TK;
+      const int n = n0 + c, kg = k0 + kk;
+      Bs[kk][c] = (n < p.N && kg < k_end) ? p.w[(long)n * p.K + kg] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < TK; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(As[kk][ty + 16 * i], Bs[kk][tx + 16 * j], acc[i][j]);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const long m = m0 + ty + 16 * i;
+      const int n = n0 + tx + 16 * j;
+      if (m >= M || n >= p.N) continue;
+      if (p.partial)
+        p.partial[((long)blockIdx.y * M + m) * p.N + n] = acc[i][j];
+      else
+        store_out(acc[i][j], m, n, p);
+    }
+}
+
+// Sums global split-K partials in split order and applies the epilogue.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int splits) {
   const long M = (long)p.batch * p.rows;
   const long total = M * p.N;
@@ -249,21 +388,112 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int spli
   }
 }
 
-enum TileKind { TILE_N32, TILE_N64, TILE_BIG, TILE_SMALLM };
+// ---------------------------------------------------------------------------
+// Single-input-channel causal conv (the waveform -> num_filters first layer):
+// y[b, t, c] = bias[c] + sum_j w[c, j] * x[b, t - pad + j].  HBM-bound on the
+// output; a block stages its 256 positions plus the causal halo in LDS and
+// writes 4 channels per thread with 16-byte stores.
+template <int K>
+__global__ __launch_bounds__(256) void conv_cin1_kernel(const float* __restrict__ x, int L,
+                                                        const float* __restrict__ w,  // [C][K]
+                                                        const float* __restrict__ bias, int C,
+                                                        int flags, float* __restrict__ y) {
+  constexpr int TB = 256;
+  __shared__ float xs[TB + K];
+  const long b = blockIdx.y;
+  const int t0 = blockIdx.x * TB;
+  const int groups = C / 4;           // threads per row; divides 256 (C in {4,8,...,1024})
+  const int rows_per_pass = 256 / groups;
+  const int c = (threadIdx.x % groups) * 4;
+  const int r0 = threadIdx.x / groups;
+  float wr[4][K], bv[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    bv[u] = bias ? bias[c + u] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < K; ++j) wr[u][j] = w[(c + u) * K + j];
+  }
+  for (int i = threadIdx.x; i < TB + K - 1; i += 256) {
+    const int t = t0 - (K - 1) + i;
+    xs[i] = (t >= 0 && t < L) ? x[b * L + t] : 0.0f;
+  }
+  __syncthreads();
+  for (int r = r0; r < TB; r += rows_per_pass) {
+    const int t = t0 + r;
+    if (t >= L) break;
+    float acc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      acc[u] = bv[u];
+#pragma unroll
+      for (int j = 0; j < K; ++j) acc[u] = fmaf(wr[u][j], xs[r + j], acc[u]);
+    }
+    floatx4 v = {acc[0], acc[1], acc[2], acc[3]};
+    if (flags & FM_EPI_ELU) v = floatx4{fm_elu(v.x), fm_elu(v.y), fm_elu(v.z), fm_elu(v.w)};
+    *reinterpret_cast<floatx4*>(y + (b * L + t) * (long)C + c) = v;
+  }
+}
 
-template <int BM, int BN, int WM, int WN>
-hipError_t launch_cfg(GemmArgs p, int splits, hipStream_t s) {
-  const long M = (long)p.batch * p.rows;
-  const int tiles = (int)(((M + BM - 1) / BM) * ((p.N + BN - 1) / BN));
-  dim3 grid(tiles, splits);
-  dim3 block(64 * WM * WN);
-  const bool va = (p.C_in % 4 == 0) && (p.K % 4 == 0) && !(p.flags & FM_REPLICATE && p.C_in % 4);
-  const bool vb = (p.N % 4 == 0);
-  if (va && vb) hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, 4, 4>), grid, block, 0, s, p);
-  else if (va) hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, 4, 1>), grid, block, 0, s, p);
-  else if (vb) hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, 1, 4>), grid, block, 0, s, p);
-  else hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, 1, 1>), grid, block, 0, s, p);
-  return hipGetLastError();
+// Single-output-channel causal conv (the num_filters -> waveform last layer):
+// y[b, t] = bias + sum_{j, c} w[j*C + c] * act(x[b, t - pad + j, c]) for t < y_len.
+// Four threads per output position each sum a quarter of the channels (their
+// weights held in registers, all 16-byte input loads issued up front), then
+// the four partial sums combine in order.
+template <int C, int K>
+__global__ __launch_bounds__(256) void conv_cout1_kernel(const float* __restrict__ x, int L,
+                                                         const float* __restrict__ w,
+                                                         const float* __restrict__ bias,
+                                                         int flags, int y_len,
+                                                         float* __restrict__ y) {
+  constexpr int CQ = C / 4;  // channels per thread
+  const long b = blockIdx.y;
+  const int t = blockIdx.x * 64 + threadIdx.x / 4;
+  const int part = threadIdx.x % 4;
+  float wr[K][CQ];
+#pragma unroll
+  for (int j = 0; j < K; ++j)
+#pragma unroll
+    for (int c = 0; c < CQ; ++c) wr[j][c] = w[j * C + part * CQ + c];
+  floatx4 v[K][CQ / 4];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const int tin = t - (K - 1) + j;
+    const bool ok = t < y_len && tin >= 0 && tin < L;
+    const float* row = x + (b * L + (ok ? tin : 0)) * (long)C + part * CQ;
+#pragma unroll
+    for (int c = 0; c < CQ / 4; ++c)
+      v[j][c] = ok ? *reinterpret_cast<const floatx4*>(row + 4 * c) : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < K; ++j)
+#pragma unroll
+    for (int c = 0; c < CQ / 4; ++c) {
+      floatx4 a = v[j][c];
+      if (flags & FM_ELU_IN) a = floatx4{fm_elu(a.x), fm_elu(a.y), fm_elu(a.z), fm_elu(a.w)};
+      acc = fmaf(wr[j][4 * c], a.x, acc);
+      acc = fmaf(wr[j][4 * c + 1], a.y, acc);
+      acc = fmaf(wr[j][4 * c + 2], a.z, acc);
+      acc = fmaf(wr[j][4 * c + 3], a.w, acc);
+    }
+  // Ordered combine of the four partial sums.
+  const float p1 = __shfl_down(acc, 1, 4), p2 = __shfl_down(acc, 2, 4), p3 = __shfl_down(acc, 3, 4);
+  if (part == 0 && t < y_len) {
+    float r = __fadd_rn(__fadd_rn(__fadd_rn(acc, p1), p2), p3);
+    if (bias) r = __fadd_rn(r, bias[0]);
+    y[b * y_len + t] = r;
+  }
+}
+
+struct TileCfg {
+  int BM, BN, WK, BK, id;
+};
+// Candidates in order of preference; the first that gives >= 2 blocks per CU wins.
+constexpr TileCfg kTiles[] = {{128, 128, 1, 64, 0}, {128, 64, 1, 64, 1}, {128, 32, 1, 64, 2},
+                              {32, 64, 4, 32, 3}};
+
+long tile_count(long M, int N, const TileCfg& t) {
+  return ((M + t.BM - 1) / t.BM) * ((N + t.BN - 1) / t.BN);
 }
 
 int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s) {
@@ -275,42 +505,52 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
   if (p.bias && p.bias_len <= 0) return FM_BAD_ARGUMENT;
   const long M = (long)p.batch * p.rows;
   if (M == 0 || p.y_rows == 0) return FM_OK;
-  if (p.L_in == 0) return FM_BAD_ARGUMENT;
+  if (p.L_in == 0 || M > INT_MAX / 2) return FM_BAD_ARGUMENT;
 
-  int BM, BN;
-  TileKind kind;
-  if (p.N <= 32) { kind = TILE_N32; BM = 128; BN = 32; }
-  else if (p.N <= 64) { kind = TILE_N64; BM = 128; BN = 64; }
-  else if (M <= 1024) { kind = TILE_SMALLM; BM = 32; BN = 128; }
-  else { kind = TILE_BIG; BM = 128; BN = 128; }
-
-  const long tiles = ((M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  const int ktiles = (p.K + BK - 1) / BK;
+  const bool fast = (p.C_in % 4 == 0) && (p.K % 4 == 0);
+  TileCfg cfg = kTiles[3];
+  long tiles = 0;
+  if (!fast) {
+    cfg = TileCfg{64, 64, 1, 16, -1};
+    tiles = tile_count(M, p.N, cfg);
+  } else {
+    // Skip shapes wider than the output (by more than 2x for the narrowest).
+    for (const TileCfg& t : kTiles) {
+      if (t.WK == 1 && t.BN > 32 && t.BN / 2 >= p.N) continue;
+      cfg = t;
+      tiles = tile_count(M, p.N, t);
+      if (tiles >= 512) break;
+    }
+  }
+  // Global K-split for long K when even the K-split tile leaves CUs idle.
+  const int kchunks = (p.K + KT - 1) / KT;
   int splits = 1;
-  const long target = 1024;  // blocks to fill 256 CUs several times over
-  if (tiles < target && ktiles >= 8 && workspace) {
-    splits = (int)((target + tiles - 1) / tiles);
-    splits = min(splits, ktiles / 4);
-    splits = min(splits, 32);
+  if (cfg.WK > 1 && tiles < 384 && kchunks >= 32 && workspace) {
+    splits = (int)std::min<long>((512 + tiles - 1) / tiles, kchunks / 16);
     const size_t per = (size_t)M * p.N * sizeof(float);
     while (splits > 1 && per * splits > workspace_bytes) --splits;
-    if (splits < 1) splits = 1;
+    splits = std::max(splits, 1);
   }
-  p.k_split = ((ktiles + splits - 1) / splits) * BK;
+  // Split boundaries are multiples of the kernel's k-tile.
+  const int kt = std::max(cfg.BK, KT);
+  const int ktiles = (p.K + kt - 1) / kt;
+  p.k_split = ((ktiles + splits - 1) / splits) * kt;
   splits = (p.K + p.k_split - 1) / p.k_split;
   p.partial = splits > 1 ? workspace : nullptr;
 
-  hipError_t e;
-  switch (kind) {
-    case TILE_N32: e = launch_cfg<128, 32, 4, 1>(p, splits, s); break;
-    case TILE_N64: e = launch_cfg<128, 64, 4, 1>(p, splits, s); break;
-    case TILE_SMALLM: e = launch_cfg<32, 128, 1, 4>(p, splits, s); break;
-    default: e = launch_cfg<128, 128, 2, 2>(p, splits, s); break;
+  dim3 grid((unsigned)tiles, splits);
+  switch (cfg.id) {
+    case 0: hipLaunchKernelGGL((gemm_fast_kernel<128, 128, 2, 2, 1, 64>), grid, dim3(NTHREADS), 0, s, p); break;
+    case 1: hipLaunchKernelGGL((gemm_fast_kernel<128, 64, 4, 1, 1, 64>), grid, dim3(NTHREADS), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((gemm_fast_kernel<128, 32, 4, 1, 1, 64>), grid, dim3(NTHREADS), 0, s, p); break;
+    case 3: hipLaunchKernelGGL((gemm_fast_kernel<32, 64, 1, 1, 4, 32>), grid, dim3(NTHREADS), 0, s, p); break;
+    default: hipLaunchKernelGGL(gemm_generic_kernel, grid, dim3(256), 0, s, p); break;
   }
+  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   if (splits > 1) {
     const long total = M * p.N;
-    const int blocks = (int)min((total + 255) / 256, (long)4096);
+    const int blocks = (int)std::min<long>((total + 255) / 256, 2048);
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, p, splits);
     e = hipGetLastError();
   }
@@ -335,6 +575,23 @@ int fm_conv1d(const float* x, int batch, int length, int in_channels, const floa
   p.y_rows = y_length; p.bias_len = out_channels;
   p.flags = (flags & ~FM_REPLICATE) | (pad_mode == 1 ? FM_REPLICATE : 0);
   if (p.flags & FM_EPI_RES_SCALE) return FM_BAD_ARGUMENT;
+  const int plain = p.flags & ~(FM_EPI_ELU | FM_ELU_IN);
+  if (x && weight_packed && y && batch > 0 && length > 0 && stride == 1 && plain == 0 &&
+      y_length >= 0 && y_length <= length) {
+    // The packed layout W^T[c_out][(tap, c_in)] doubles as [C][k] / [k*C] here.
+    if (in_channels == 1 && kernel == 7 && out_channels % 4 == 0 && out_channels <= 1024 &&
+        256 % (out_channels / 4) == 0 && !(p.flags & FM_ELU_IN) && y_length == length) {
+      hipLaunchKernelGGL(conv_cin1_kernel<7>, dim3((length + 255) / 256, batch), dim3(256), 0,
+                         stream, x, length, weight_packed, bias, out_channels, p.flags, y);
+      return (int)hipGetLastError();
+    }
+    if (out_channels == 1 && in_channels == 64 && kernel == 3 && !(p.flags & FM_EPI_ELU)) {
+      if (y_length == 0) return FM_OK;
+      hipLaunchKernelGGL((conv_cout1_kernel<64, 3>), dim3((y_length + 63) / 64, batch), dim3(256), 0,
+                         stream, x, length, weight_packed, bias, p.flags, y_length, y);
+      return (int)hipGetLastError();
+    }
+  }
   return run_gemm(p, workspace, workspace_bytes, stream);
 }
 

@@ -51,12 +51,18 @@ FM_DEVICE void resolve(const float* val, const int* idx, int chunks, long M, lon
   }
 }
 
-// Dynamic LDS: Xs[dim][RB+1] (k-major, MFMA A operand), xn[RB], best[4][RB] x2, codes[RB].
+constexpr int NT = 128;  // entries per sub-tile (4 waves x 32)
+constexpr int KSL = 32;  // codebook dims per staged slice
+constexpr int PB = NT + 4;
+
+// Dynamic LDS: Xs[dim][RB+1] (k-major, MFMA A operand), Bs[KSL][NT+4]
+// (staged codebook slice), xn[RB], per-wave best (value, index), codes[RB].
 __global__ __launch_bounds__(256) void rvq_step_kernel(StepArgs a) {
   extern __shared__ float smem[];
   constexpr int PX = RB + 1;
   float* Xs = smem;
-  float* xn = Xs + a.dim * PX;
+  float* Bs = Xs + a.dim * PX;
+  float* xn = Bs + KSL * PB;
   float* bval = xn + RB;
   int* bidx = reinterpret_cast<int*>(bval + 4 * RB);
   int* rcode = bidx + 4 * RB;
@@ -79,18 +85,47 @@ __global__ __launch_bounds__(256) void rvq_step_kernel(StepArgs a) {
     rcode[tid] = code;
   }
   __syncthreads();
-  for (int e = tid; e < RB * a.dim; e += 256) {
-    const int r = e / a.dim, k = e % a.dim;
-    const long m = m0 + r;
-    float x = 0.0f;
-    if (m < a.M) {
-      x = a.resid_in[m * a.ld_in + k];
-      if (a.prev_embed) {
-        x = __fsub_rn(x, a.prev_embed[(long)rcode[r] * a.dim + k]);
-        if (chunk == 0 && a.resid_out) a.resid_out[m * a.dim + k] = x;
+  // Residual rows into LDS.  All loads of a batch are issued before any
+  // store, so they overlap instead of queueing behind possibly-aliasing stores.
+  {
+    const int dv = a.dim / 4;  // dim is a multiple of 4 on this path
+    const int total = RB * dv;
+    constexpr int UNR = 8;
+    for (int c0 = 0; c0 < total; c0 += 256 * UNR) {
+      floatx4 xv[UNR], ev[UNR];
+#pragma unroll
+      for (int u = 0; u < UNR; ++u) {
+        const int c = c0 + u * 256 + tid;
+        const int r = c / dv, k = (c % dv) * 4;
+        const long m = m0 + r;
+        xv[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        ev[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (c < total && m < a.M) {
+          xv[u] = *reinterpret_cast<const floatx4*>(a.resid_in + m * a.ld_in + k);
+          if (a.prev_embed)
+            ev[u] = *reinterpret_cast<const floatx4*>(a.prev_embed + (long)rcode[r] * a.dim + k);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < UNR; ++u) {
+        const int c = c0 + u * 256 + tid;
+        if (c >= total) continue;
+        const int r = c / dv, k = (c % dv) * 4;
+        const long m = m0 + r;
+        floatx4 x = xv[u];
+        if (a.prev_embed && m < a.M) {
+          x.x = __fsub_rn(x.x, ev[u].x);
+          x.y = __fsub_rn(x.y, ev[u].y);
+          x.z = __fsub_rn(x.z, ev[u].z);
+          x.w = __fsub_rn(x.w, ev[u].w);
+          if (chunk == 0 && a.resid_out) *reinterpret_cast<floatx4*>(a.resid_out + m * a.dim + k) = x;
+        }
+        Xs[(k + 0) * PX + r] = x.x;
+        Xs[(k + 1) * PX + r] = x.y;
+        Xs[(k + 2) * PX + r] = x.z;
+        Xs[(k + 3) * PX + r] = x.w;
       }
     }
-    Xs[k * PX + r] = x;
   }
   __syncthreads();
   if (tid < RB) {
@@ -98,9 +133,7 @@ __global__ __launch_bounds__(256) void rvq_step_kernel(StepArgs a) {
     for (int k = 0; k < a.dim; ++k) s = fmaf(Xs[k * PX + tid], Xs[k * PX + tid], s);
     xn[tid] = s;
   }
-  __syncthreads();
 
-  // Distances for this chunk; lane owns entry column (lane % 32) of each 32-wide tile.
   float best_v[16];
   int best_i[16];
 #pragma unroll
@@ -108,20 +141,40 @@ __global__ __launch_bounds__(256) void rvq_step_kernel(StepArgs a) {
   const int e_begin = chunk * a.chunk_entries;
   const int e_end = min(a.entries, e_begin + a.chunk_entries);
   const int lrow = lane >> 5, lcol = lane & 31;
-  for (int t0 = e_begin + wave * 32; t0 < e_end; t0 += 4 * 32) {
+  const bool vec = (a.entries % 4 == 0);
+  for (int n0 = e_begin; n0 < e_end; n0 += NT) {
     floatx16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-    const int col = t0 + lcol;
-    const bool col_ok = col < e_end;
-    const float* bt = a.embed_t + col;
+    for (int k0 = 0; k0 < a.dim; k0 += KSL) {
+      __syncthreads();
+      // Stage codebook dims [k0, k0+KSL) x entries [n0, n0+NT) (rows contiguous in entries).
+      if (vec) {
+        for (int c = tid; c < KSL * NT / 4; c += 256) {
+          const int kr = c / (NT / 4), nn = (c % (NT / 4)) * 4;
+          const int k = k0 + kr, n = n0 + nn;
+          floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+          if (k < a.dim && n < e_end) v = *reinterpret_cast<const floatx4*>(a.embed_t + (long)k * a.entries + n);
+          *reinterpret_cast<floatx4*>(&Bs[kr * PB + nn]) = v;
+        }
+      } else {
+        for (int c = tid; c < KSL * NT; c += 256) {
+          const int kr = c / NT, nn = c % NT;
+          const int k = k0 + kr, n = n0 + nn;
+          Bs[kr * PB + nn] = (k < a.dim && n < e_end) ? a.embed_t[(long)k * a.entries + n] : 0.0f;
+        }
+      }
+      __syncthreads();
+      const int kmax = min(KSL, a.dim - k0);
 #pragma unroll 8
-    for (int k = 0; k < a.dim; k += 2) {
-      const float av = Xs[(k + lrow) * PX + lcol];
-      const float bv = col_ok ? bt[(long)(k + lrow) * a.entries] : 0.0f;
-      acc = fm_mfma32(av, bv, acc);
+      for (int kk = 0; kk < kmax; kk += 2) {
+        const float av = Xs[(k0 + kk + lrow) * PX + lcol];
+        const float bv = Bs[(kk + lrow) * PB + wave * 32 + lcol];
+        acc = fm_mfma32(av, bv, acc);
+      }
     }
-    if (col_ok) {
+    const int col = n0 + wave * 32 + lcol;
+    if (col < e_end) {
       const float en = a.norms[col];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -222,7 +275,8 @@ __global__ __launch_bounds__(256) void rvq_decode_kernel(const int64_t* codes, i
 }
 
 size_t step_lds_bytes(int dim) {
-  return (size_t)dim * (RB + 1) * 4 + RB * 4 + 4 * RB * 4 + 4 * RB * 4 + RB * 4;
+  return (size_t)dim * (RB + 1) * 4 + (size_t)KSL * PB * 4 + RB * 4 + 4 * RB * 4 + 4 * RB * 4 +
+         RB * 4;
 }
 
 }  // namespace
@@ -254,7 +308,7 @@ int fm_rvq_encode(const float* x, int ld_x, int rows, int rows_per_batch, int di
                   int count, const float* embeds, const float* embeds_t, const float* norms,
                   int64_t* codes, int batch_stride, void* workspace, size_t workspace_bytes,
                   hipStream_t stream) {
-  if (!x || !embeds || !embeds_t || !norms || !codes || rows < 0 || dim <= 0 || dim % 2 ||
+  if (!x || !embeds || !embeds_t || !norms || !codes || rows < 0 || dim <= 0 || dim % 4 || ld_x % 4 ||
       entries <= 0 || count <= 0 || rows_per_batch <= 0 || ld_x < dim)
     return FM_BAD_ARGUMENT;
   if (rows == 0) return FM_OK;
@@ -263,8 +317,8 @@ int fm_rvq_encode(const float* x, int ld_x, int rows, int rows_per_batch, int di
   const int row_blocks = (rows + RB - 1) / RB;
   // Enough chunks to spread one step over the GPU; chunks are multiples of 128 entries.
   int chunks = 1;
-  while (chunks < 16 && row_blocks * chunks < 512 && entries / (chunks * 2) >= 128) chunks *= 2;
-  const int chunk_entries = (entries + chunks - 1) / chunks;
+  while (chunks < 16 && row_blocks * chunks < 512 && entries / (chunks * 2) >= NT) chunks *= 2;
+  const int chunk_entries = ((entries + chunks - 1) / chunks + NT - 1) / NT * NT;
 
   char* ws = static_cast<char*>(workspace);
   float* resid[2] = {reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws) + (size_t)rows * dim};

@@ -38,116 +38,188 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float* __restrict
     yr[c] = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(xr[c], mean), rstd), gamma[c]), beta[c]);
 }
 
-constexpr int QB = 32;  // queries per block
-constexpr int KC = 64;  // keys per staged chunk
+constexpr int QB = 32;  // queries per block (one MFMA column tile)
+constexpr int KB = 32;  // keys per MFMA row tile
+constexpr int NW = 4;   // waves per block; they split the key range
 
-// RoPE as the reference writes it: x*cos + rotate_half(x)*sin, no contraction.
-FM_DEVICE float rope(const float* v, int d, int D, const float* cs, const float* sn) {
-  const int h = D / 2;
-  const float rot = d < h ? -v[d + h] : v[d - h];
-  return __fadd_rn(__fmul_rn(v[d], cs[d]), __fmul_rn(rot, sn[d]));
+// RoPE as the reference writes it: x*cos + rotate_half(x)*sin, each product
+// and the sum rounded separately.
+FM_DEVICE float rope1(float x, float partner, int d, int half, float c, float s) {
+  const float rot = d < half ? -partner : partner;
+  return __fadd_rn(__fmul_rn(x, c), __fmul_rn(rot, s));
 }
 
-// Grid: (ceil(T / QB), heads, batch); 256 threads = 8 threads per query.
+// Stages rows t0 .. t0+31 (rows past t_last read as zero) of one head of the
+// packed projection into a transposed LDS tile dst[d * P + r] with RoPE
+// applied.  Each of the NTH cooperating threads owns N elements; all global
+// loads are issued before any use so they overlap.
+template <int N, int NTH, int D, int DP, int P>
+FM_DEVICE void stage_rope_t(float* dst, int tid, const float* __restrict__ qkv, int ld, int col0,
+                            const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                            long base, int t0, int t_last) {
+  constexpr int HALF = D / 2;
+  float x[N], xp[N], c[N], sn[N];
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const int e = tid + u * NTH;
+    const int r = e / DP, d = e % DP;
+    const int t = t0 + r;
+    x[u] = xp[u] = c[u] = sn[u] = 0.0f;
+    if (t <= t_last && d < D) {
+      const float* row = qkv + (base + t) * ld + col0;
+      x[u] = row[d];
+      xp[u] = row[d < HALF ? d + HALF : d - HALF];
+      c[u] = cos_t[(long)t * D + d];
+      sn[u] = sin_t[(long)t * D + d];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const int e = tid + u * NTH;
+    const int r = e / DP, d = e % DP;
+    dst[d * P + r] = rope1(x[u], xp[u], d, HALF, c[u], sn[u]);
+  }
+}
+
+// Sliding-window causal attention on FP32 MFMA.
+// Grid: (ceil(T / QB), heads, batch), 256 threads.  Block = 32 queries of one
+// head; its key range [q0 - window + 1, q0 + 31] is cut into 32-key tiles that
+// the 4 waves take round-robin, one tile per wave per round.  Q (once) and
+// each wave's K tile are staged through LDS with row-contiguous loads and RoPE
+// applied on the way in, stored transposed ([dim][32], odd pitch).  Per tile a
+// wave computes S^T = K Q^T (keys on MFMA rows, queries on columns, lane l
+// owns query q0 + l % 32), applies the window mask and an online softmax per
+// column, then accumulates O^T += V^T P^T with P^T fed straight from the S^T
+// registers: MFMA step s takes keys 8*(s/4) + 4*h + s%4 (h = lane / 32),
+// exactly the rows that lane holds in accumulator slot s.  V is read straight
+// from global memory (lanes read consecutive dims).  The waves' (max, sum, O)
+// are merged through LDS.
 template <int D>
 __global__ __launch_bounds__(256) void window_attention_kernel(
     const float* __restrict__ qkv, int ld, int q_off, int k_off, int v_off,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, int T, int heads,
     int kv_heads, int window, float scale, float* __restrict__ out, int ld_out) {
-  constexpr int P = D + 1;
-  __shared__ float Qs[QB * P];
-  __shared__ float Ks[KC * P];
-  __shared__ float Vs[KC * P];
-  __shared__ float Ps[QB * (KC + 1)];
+  constexpr int DT = (D + 31) / 32;  // 32-row tiles of O^T
+  constexpr int DP = DT * 32;        // padded head dim
+  constexpr int KS = DP / 2;         // MFMA k-steps of the QK^T product
+  constexpr int HALF = D / 2;
+  constexpr int P = QB + 1;          // pitch of the transposed [dim][32] tiles
+  // Region 0: per-wave K tiles during the loop, per-wave O^T at the merge.
+  __shared__ float stage[NW][DP * P];
+  __shared__ float Qt[DP * P];
+  __shared__ float Mm[NW][QB];
+  __shared__ float Lm[NW][QB];
 
-  const int tid = threadIdx.x;
-  const int qi = tid >> 3;   // query within block
-  const int sub = tid & 7;   // lane within the query's group of 8
-  const int h = blockIdx.y;
-  const int hk = h / (heads / kv_heads);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, col = lane & 31;
+  const int head = blockIdx.y;
+  const int hk = head / (heads / kv_heads);
   const long b = blockIdx.z;
   const int q0 = blockIdx.x * QB;
-  const int qlast = min(q0 + QB, T) - 1;
+  const int q = q0 + col;
   const int k_lo = max(0, q0 - window + 1);
-  const int k_hi = qlast;
+  const int k_hi = min(T, q0 + QB) - 1;
   const long base = b * (long)T;
 
-  // Stage Q with RoPE.
-  for (int e = tid; e < QB * D; e += 256) {
-    const int r = e / D, d = e % D;
-    const int t = q0 + r;
-    float v = 0.0f;
-    if (t < T) {
-      const float* src = qkv + (base + t) * ld + q_off + h * D;
-      v = rope(src, d, D, cos_t + (long)t * D, sin_t + (long)t * D);
-    }
-    Qs[r * P + d] = v;
-  }
-
-  const int qg = q0 + qi;
-  float m_run = -INFINITY, l_run = 0.0f;
-  float o[D / 8];
+  // Stage Q^T with RoPE (zero for padded dims / rows past T).
+  stage_rope_t<QB * DP / 256, 256, D, DP, P>(Qt, tid, qkv, ld, q_off + head * D, cos_t, sin_t,
+                                            base, q0, T - 1);
+  __syncthreads();
+  float qv[KS];
 #pragma unroll
-  for (int i = 0; i < D / 8; ++i) o[i] = 0.0f;
+  for (int i = 0; i < KS; ++i) qv[i] = Qt[(2 * i + h) * P + col];
 
-  for (int k0 = k_lo; k0 <= k_hi; k0 += KC) {
-    __syncthreads();
-    for (int e = tid; e < KC * D; e += 256) {
-      const int r = e / D, d = e % D;
-      const int t = k0 + r;
-      float kv = 0.0f, vv = 0.0f;
-      if (t <= k_hi) {
-        const float* row = qkv + (base + t) * ld;
-        kv = rope(row + k_off + hk * D, d, D, cos_t + (long)t * D, sin_t + (long)t * D);
-        vv = row[v_off + hk * D + d];
-      }
-      Ks[r * P + d] = kv;
-      Vs[r * P + d] = vv;
-    }
-    __syncthreads();
+  float m_run = -INFINITY, l_run = 0.0f;
+  floatx16 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
 
-    float s[KC / 8];
+  float* Kt = stage[wave];
+  const int ntiles = (k_hi - k_lo + KB) / KB;
+  const int rounds = (ntiles + NW - 1) / NW;
+  for (int round = 0; round < rounds; ++round) {
+    const int tile = round * NW + wave;
+    const int k0 = k_lo + tile * KB;
+    const bool active = tile < ntiles;
+    __syncthreads();  // previous round's reads of Kt are done
+    if (active)
+      stage_rope_t<KB * DP / 64, 64, D, DP, P>(Kt, lane, qkv, ld, k_off + hk * D, cos_t, sin_t,
+                                              base, k0, k_hi);
+    __syncthreads();
+    if (!active) continue;
+
+    floatx16 s;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KS; ++i) s = fm_mfma32(Kt[(2 * i + h) * P + col], qv[i], s);
+
     float cmax = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < KC / 8; ++i) {
-      const int kk = sub + 8 * i;
-      const int kg = k0 + kk;
-      float acc = 0.0f;
-#pragma unroll 16
-      for (int d = 0; d < D; ++d) acc = fmaf(Qs[qi * P + d], Ks[kk * P + d], acc);
-      const bool ok = qg < T && kg <= k_hi && kg <= qg && kg > qg - window;
-      s[i] = ok ? acc * scale : -INFINITY;
-      cmax = fmaxf(cmax, s[i]);
+    for (int r = 0; r < 16; ++r) {
+      const int key = k0 + fm_mfma32_row(r, lane);
+      const bool ok = q < T && key <= k_hi && key <= q && key > q - window;
+      s[r] = ok ? s[r] * scale : -INFINITY;
+      cmax = fmaxf(cmax, s[r]);
     }
-#pragma unroll
-    for (int o2 = 1; o2 < 8; o2 <<= 1) cmax = fmaxf(cmax, __shfl_xor(cmax, o2, 64));
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
     const float m_new = fmaxf(m_run, cmax);
     float psum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < KC / 8; ++i) {
-      const float pv = (m_new == -INFINITY || s[i] == -INFINITY) ? 0.0f : expf(s[i] - m_new);
-      Ps[qi * (KC + 1) + sub + 8 * i] = pv;
+    for (int r = 0; r < 16; ++r) {
+      const float pv = (s[r] == -INFINITY) ? 0.0f : expf(s[r] - m_new);
+      s[r] = pv;
       psum += pv;
     }
-#pragma unroll
-    for (int o2 = 1; o2 < 8; o2 <<= 1) psum += __shfl_xor(psum, o2, 64);
+    psum += __shfl_xor(psum, 32, 64);
     const float corr = (m_run == -INFINITY) ? 0.0f : expf(m_run - m_new);
     l_run = l_run * corr + psum;
     m_run = m_new;
-    __syncthreads();
 #pragma unroll
-    for (int i = 0; i < D / 8; ++i) {
-      const int d = sub + 8 * i;
-      float acc = o[i] * corr;
-      for (int kk = 0; kk < KC; ++kk) acc = fmaf(Ps[qi * (KC + 1) + kk], Vs[kk * P + d], acc);
-      o[i] = acc;
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+      const int key = k0 + 8 * (st >> 2) + 4 * h + (st & 3);
+      const bool vok = key <= k_hi;
+      const float* vrow = qkv + (base + (vok ? key : k_lo)) * ld + v_off + hk * D;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const int d = t * 32 + col;
+        const float vv = (vok && d < D) ? vrow[d] : 0.0f;
+        o[t] = fm_mfma32(vv, s[st], o[t]);
+      }
     }
   }
-  if (qg < T) {
-    float* dst = out + (base + qg) * ld_out + h * D;
-    const float inv = 1.0f / l_run;
+
+  // Merge the waves: O = sum_w O_w exp(m_w - M), L = sum_w l_w exp(m_w - M).
+  __syncthreads();
+  float* Om = stage[wave];
+  if (h == 0) Mm[wave][col] = m_run, Lm[wave][col] = l_run;
 #pragma unroll
-    for (int i = 0; i < D / 8; ++i) dst[sub + 8 * i] = o[i] * inv;
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) Om[(t * 32 + fm_mfma32_row(r, lane)) * P + col] = o[t][r];
+  __syncthreads();
+  for (int e = tid; e < QB * D; e += 256) {
+    const int qi = e / D, d = e % D;
+    const int qg = q0 + qi;
+    if (qg >= T) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, Mm[w][qi]);
+    float num = 0.0f, den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      if (Mm[w][qi] == -INFINITY) continue;
+      const float f = expf(Mm[w][qi] - M);
+      num += stage[w][d * P + qi] * f;
+      den += Lm[w][qi] * f;
+    }
+    out[(base + qg) * ld_out + head * D + d] = num / den;
   }
 }
 

@@ -40,19 +40,19 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 
 
 class _Conv:
-    """Causal Conv1d packed for the implicit GEMM: W[(tap, c_in), c_out]."""
+    """Causal Conv1d packed for the implicit GEMM as W^T[c_out, (tap, c_in)]."""
 
     def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None, stride: int = 1,
                  pad_mode: str = "constant"):
         c_out, c_in, k = weight.shape
         self.c_in, self.c_out, self.k, self.stride = c_in, c_out, k, stride
         self.replicate = 1 if pad_mode == "replicate" else 0
-        self.w = weight.permute(2, 1, 0).reshape(k * c_in, c_out).contiguous()
+        self.w = weight.permute(0, 2, 1).reshape(c_out, k * c_in).contiguous()
         self.b = None if bias is None else bias.contiguous()
 
 
 class _ConvT:
-    """Causal ConvTranspose1d packed as W[(tap, c_in), (phase, c_out)].
+    """Causal ConvTranspose1d packed as W^T[(phase, c_out), (tap, c_in)].
 
     Output row q*s + r reads inputs q - taps + 1 .. q; window slot jj holds input
     q - (taps - 1 - jj), which meets kernel tap r + (taps - 1 - jj) * s.
@@ -65,7 +65,7 @@ class _ConvT:
         taps = k // stride
         self.c_in, self.c_out, self.k, self.stride = c_in, c_out, k, stride
         w = weight.reshape(c_in, c_out, taps, stride).flip(2)  # [ci, co, jj, r]
-        self.w = w.permute(2, 0, 3, 1).reshape(taps * c_in, stride * c_out).contiguous()
+        self.w = w.permute(3, 1, 2, 0).reshape(stride * c_out, taps * c_in).contiguous()
         self.b = None if bias is None else bias.contiguous()
 
 
@@ -75,11 +75,12 @@ class _Layer:
         self.ln1 = (g("input_layernorm.weight").contiguous(), g("input_layernorm.bias").contiguous())
         self.ln2 = (g("post_attention_layernorm.weight").contiguous(),
                     g("post_attention_layernorm.bias").contiguous())
+        # Linear weights are [out, in] = W^T already.
         self.wqkv = torch.cat([g("self_attn.q_proj.weight"), g("self_attn.k_proj.weight"),
-                               g("self_attn.v_proj.weight")], 0).t().contiguous()
-        self.wo = g("self_attn.o_proj.weight").t().contiguous()
-        self.w1 = g("mlp.fc1.weight").t().contiguous()
-        self.w2 = g("mlp.fc2.weight").t().contiguous()
+                               g("self_attn.v_proj.weight")], 0).contiguous()
+        self.wo = g("self_attn.o_proj.weight").contiguous()
+        self.w1 = g("mlp.fc1.weight").contiguous()
+        self.w2 = g("mlp.fc2.weight").contiguous()
         self.ls1 = g("self_attn_layer_scale.scale").contiguous()
         self.ls2 = g("mlp_layer_scale.scale").contiguous()
 
@@ -147,9 +148,9 @@ class MimiRuntime:
         ac = "quantizer.acoustic_residual_vector_quantizer"
         self.vq = cfg.vector_quantization_hidden_dimension
         self.w_in = torch.cat([st[f"{sem}.input_proj.weight"][:, :, 0],
-                               st[f"{ac}.input_proj.weight"][:, :, 0]], 0).t().contiguous()
-        self.w_out = torch.cat([st[f"{sem}.output_proj.weight"][:, :, 0].t(),
-                                st[f"{ac}.output_proj.weight"][:, :, 0].t()], 0).contiguous()
+                               st[f"{ac}.input_proj.weight"][:, :, 0]], 0).contiguous()
+        self.w_out = torch.cat([st[f"{sem}.output_proj.weight"][:, :, 0],
+                                st[f"{ac}.output_proj.weight"][:, :, 0]], 1).contiguous()
         n_sem = cfg.num_semantic_quantizers
         prefixes = [f"{sem}.layers.{j}.codebook" for j in range(n_sem)]
         prefixes += [f"{ac}.layers.{j}.codebook" for j in range(cfg.num_quantizers - n_sem)]
@@ -165,40 +166,70 @@ class MimiRuntime:
                      self.norms[j].data_ptr(), stream)
         self.workspace = torch.empty(_WORKSPACE_BYTES // 4, device=device)
         self._rope: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
+        # Optional per-op timing: a list of (tag, start_event, end_event).
+        self.profile: list | None = None
+        self._tag = ""
         torch.cuda.synchronize(device)
 
     # ------------------------------------------------------------------ ops
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
 
+    def _call(self, name: str, *args) -> None:
+        if self.profile is None:
+            nat.call(name, *args)
+            return
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        nat.call(name, *args)
+        stop.record()
+        self.profile.append((f"{self._tag}:{name}", start, stop))
+
+    def profile_report(self) -> list[tuple[str, float]]:
+        """(tag, milliseconds) per recorded op; clears the record."""
+        torch.cuda.synchronize(self.device)
+        out = [(tag, a.elapsed_time(b)) for tag, a, b in (self.profile or [])]
+        self.profile = [] if self.profile is not None else None
+        return out
+
     def _conv(self, x, B, L, layer: _Conv, flags=0, residual=None, y_len=None):
         rows = -(-L // layer.stride)
         y_len = rows if y_len is None else y_len
         y = torch.empty((B, y_len, layer.c_out), device=self.device)
-        nat.call("fm_conv1d", x.data_ptr(), B, L, layer.c_in, layer.w.data_ptr(), _ptr(layer.b),
+        self._call("fm_conv1d", x.data_ptr(), B, L, layer.c_in, layer.w.data_ptr(), _ptr(layer.b),
                  layer.c_out, layer.k, layer.stride, layer.replicate, flags, _ptr(residual),
                  y.data_ptr(), y_len, self.workspace.data_ptr(), _WORKSPACE_BYTES, self._stream())
         return y, rows
 
     def _convt(self, x, B, L, layer: _ConvT):
         y = torch.empty((B, L * layer.stride, layer.c_out), device=self.device)
-        nat.call("fm_conv_transpose1d", x.data_ptr(), B, L, layer.c_in, layer.w.data_ptr(),
+        self._call("fm_conv_transpose1d", x.data_ptr(), B, L, layer.c_in, layer.w.data_ptr(),
                  _ptr(layer.b), layer.c_out, layer.k, layer.stride, 0, None, y.data_ptr(),
                  self.workspace.data_ptr(), _WORKSPACE_BYTES, self._stream())
         return y, L * layer.stride
 
     def _linear(self, x, rows, w, flags=0, residual=None, scale=None, out=None):
-        k, n = w.shape
+        n, k = w.shape
         y = torch.empty((rows, n), device=self.device) if out is None else out
-        nat.call("fm_linear", x.data_ptr(), rows, k, w.data_ptr(), n, flags, _ptr(residual),
+        self._call("fm_linear", x.data_ptr(), rows, k, w.data_ptr(), n, flags, _ptr(residual),
                  _ptr(scale), y.data_ptr(), self.workspace.data_ptr(), _WORKSPACE_BYTES,
                  self._stream())
         return y
 
-    def _resblock(self, x, B, L, block, elu_after: bool):
+    def _resblock(self, x, B, L, block, elu_after: bool, tag: str = "res"):
         c1, c2 = block
+        if c1.k == 3 and nat.library().fm_resblock_supported(c2.c_out):
+            self._tag = tag
+            y = torch.empty_like(x)
+            self._call("fm_resblock", x.data_ptr(), B, L, c2.c_out, c1.w.data_ptr(), c1.b.data_ptr(),
+                       c2.w.data_ptr(), c2.b.data_ptr(), 1 if elu_after else 0, y.data_ptr(),
+                       self._stream())
+            return y
+        self._tag = f"{tag}.c1"
         h, _ = self._conv(x, B, L, c1, nat.ELU_IN | nat.EPI_ELU)
         flags = nat.EPI_RES_ADD | (nat.EPI_ELU if elu_after else 0)
+        self._tag = f"{tag}.c2"
         y, _ = self._conv(h, B, L, c2, flags, residual=x)
         return y
 
@@ -216,7 +247,7 @@ class MimiRuntime:
         """Upload the RoPE tables a sequence of ``length`` frames needs."""
         self._rope_tables(length)
 
-    def transformer(self, h, B, T, layers):
+    def transformer(self, h, B, T, layers, tag: str = "tf"):
         cfg = self.config
         M = B * T
         C = cfg.hidden_size
@@ -226,18 +257,25 @@ class MimiRuntime:
         xln = torch.empty((M, C), device=self.device)
         att = torch.empty((M, nh * hd), device=self.device)
         s = self._stream()
-        for lay in layers:
-            nat.call("fm_layer_norm", h.data_ptr(), lay.ln1[0].data_ptr(), lay.ln1[1].data_ptr(),
+        for li, lay in enumerate(layers):
+            self._tag = f"{tag}{li}.ln1"
+            self._call("fm_layer_norm", h.data_ptr(), lay.ln1[0].data_ptr(), lay.ln1[1].data_ptr(),
                      M, C, cfg.norm_eps, xln.data_ptr(), s)
+            self._tag = f"{tag}{li}.qkv"
             qkv = self._linear(xln, M, lay.wqkv)
             ld = qkv.shape[1]
-            nat.call("fm_window_attention", qkv.data_ptr(), ld, 0, nh * hd, (nh + nkv) * hd,
+            self._tag = f"{tag}{li}.attn"
+            self._call("fm_window_attention", qkv.data_ptr(), ld, 0, nh * hd, (nh + nkv) * hd,
                      cos.data_ptr(), sin.data_ptr(), B, T, nh, nkv, hd, cfg.sliding_window,
                      1.0 / (hd ** 0.5), att.data_ptr(), nh * hd, s)
+            self._tag = f"{tag}{li}.o"
             self._linear(att, M, lay.wo, nat.EPI_RES_SCALE, residual=h, scale=lay.ls1, out=h)
-            nat.call("fm_layer_norm", h.data_ptr(), lay.ln2[0].data_ptr(), lay.ln2[1].data_ptr(),
+            self._tag = f"{tag}{li}.ln2"
+            self._call("fm_layer_norm", h.data_ptr(), lay.ln2[0].data_ptr(), lay.ln2[1].data_ptr(),
                      M, C, cfg.norm_eps, xln.data_ptr(), s)
+            self._tag = f"{tag}{li}.fc1"
             ff = self._linear(xln, M, lay.w1, nat.EPI_GELU)
+            self._tag = f"{tag}{li}.fc2"
             self._linear(ff, M, lay.w2, nat.EPI_RES_SCALE, residual=h, scale=lay.ls2, out=h)
         return h.reshape(B, T, C)
 
@@ -247,14 +285,18 @@ class MimiRuntime:
         cfg = self.config
         B, C, S = audio.shape
         x = audio if C == 1 else audio.transpose(1, 2).contiguous()
+        self._tag = "enc.first"
         h, L = self._conv(x, B, S, self.enc_first)
         n = len(self.enc_stages)
         for i, (block, down) in enumerate(self.enc_stages):
-            h = self._resblock(h, B, L, block, elu_after=True)
+            h = self._resblock(h, B, L, block, elu_after=True, tag=f"enc.res{down.c_in}")
+            self._tag = f"enc.down{down.stride}"
             h, L = self._conv(h, B, L, down, nat.EPI_ELU if i == n - 1 else 0)
+        self._tag = "enc.last"
         h, L = self._conv(h, B, L, self.enc_last)
-        h = self.transformer(h, B, L, self.enc_tf)
+        h = self.transformer(h, B, L, self.enc_tf, "enc.tf")
         if self.bottleneck:
+            self._tag = "down"
             h, L = self._conv(h, B, L, self.down)
         return self.quantize(h, B, L, num_quantizers)
 
@@ -262,7 +304,9 @@ class MimiRuntime:
         cfg = self.config
         M = B * T
         vq = self.vq
+        self._tag = "rvq.in"
         proj = self._linear(h.reshape(M, cfg.hidden_size), M, self.w_in)
+        self._tag = "rvq.encode"
         codes = torch.empty((B, nq, T), dtype=torch.int64, device=self.device)
         ws_bytes = nat.library().fm_rvq_workspace_bytes(M, vq, cfg.codebook_size)
         ws = torch.empty((ws_bytes + 3) // 4, device=self.device)
@@ -272,7 +316,7 @@ class MimiRuntime:
         for col, first, count in branches:
             if count <= 0:
                 continue
-            nat.call("fm_rvq_encode", proj.data_ptr() + col * 4, 2 * vq, M, T, vq,
+            self._call("fm_rvq_encode", proj.data_ptr() + col * 4, 2 * vq, M, T, vq,
                      cfg.codebook_size, count, self.embeds[first].data_ptr(),
                      self.embeds_t[first].data_ptr(), self.norms[first].data_ptr(),
                      codes.data_ptr() + first * T * 8, nq * T, ws.data_ptr(), ws_bytes, s)
@@ -285,23 +329,29 @@ class MimiRuntime:
         M = B * T
         vq = self.vq
         q = torch.empty((M, 2 * vq), device=self.device)
-        nat.call("fm_rvq_decode", codes.data_ptr(), B, nq, T, cfg.num_semantic_quantizers,
+        self._tag = "rvq.decode"
+        self._call("fm_rvq_decode", codes.data_ptr(), B, nq, T, cfg.num_semantic_quantizers,
                  self.embeds.data_ptr(), cfg.codebook_size, vq, q.data_ptr(), self._stream())
+        self._tag = "rvq.out"
         h = self._linear(q, M, self.w_out).reshape(B, T, cfg.hidden_size)
+        self._tag = "up"
         L = T
         if self.bottleneck:
             up = torch.empty((B, L * 2, cfg.hidden_size), device=self.device)
-            nat.call("fm_upsample_depthwise", h.data_ptr(), B, L, cfg.hidden_size,
+            self._call("fm_upsample_depthwise", h.data_ptr(), B, L, cfg.hidden_size,
                      self.up_w.data_ptr(), self.up_k, 2, up.data_ptr(), self._stream())
             h, L = up, 2 * L
-        h = self.transformer(h, B, L, self.dec_tf)
+        h = self.transformer(h, B, L, self.dec_tf, "dec.tf")
+        self._tag = "dec.first"
         h, L = self._conv(h, B, L, self.dec_first, nat.EPI_ELU)
         n = len(self.dec_stages)
         for i, (convt, block) in enumerate(self.dec_stages):
+            self._tag = f"dec.up{convt.stride}"
             h, L = self._convt(h, B, L, convt)
-            h = self._resblock(h, B, L, block, elu_after=True)
+            h = self._resblock(h, B, L, block, elu_after=True, tag=f"dec.res{convt.c_out}")
         full = L
         out_length = full if out_length is None else min(out_length, full)
+        self._tag = "dec.last"
         y, _ = self._conv(h, B, L, self.dec_last, y_len=out_length)
         c_out = self.dec_last.c_out
         if c_out == 1:

@@ -74,6 +74,9 @@ CONV_CASES = [
     (2, 2, 4, 4, 2, 9),             # tiny channels, scalar loads
     (1, 4, 2, 3, 1, 1),             # length 1
     (1, 16, 16, 4, 2, 5),
+    (1, 64, 32, 3, 1, 140000),     # 256x32 tiles
+    (1, 32, 64, 1, 1, 70000),      # 128x64 tiles
+    (1, 64, 256, 4, 2, 70000),     # 128x128 tiles
 ]
 
 
@@ -116,6 +119,31 @@ def test_conv1d_fused_resblock_epilogues(ws):
     close(y, want, rel=5e-5)
 
 
+@pytest.mark.parametrize("B,C,L", [(1, 64, 1000), (2, 64, 129), (1, 128, 777), (3, 128, 1),
+                                   (1, 256, 300), (2, 256, 33), (1, 64, 240000)])
+@pytest.mark.parametrize("elu_out", [1, 0])
+def test_fused_resblock(B, C, L, elu_out):
+    """fm_resblock equals the reference block x + conv1x1(ELU(conv_k3(ELU(x))))."""
+    g = torch.Generator().manual_seed(C + L)
+    x = torch.randn(B, C, L, generator=g)
+    w1 = torch.randn(C // 2, C, 3, generator=g) / math.sqrt(3 * C)
+    b1 = torch.randn(C // 2, generator=g) * 0.1
+    w2 = torch.randn(C, C // 2, 1, generator=g) / math.sqrt(C // 2)
+    b2 = torch.randn(C, generator=g) * 0.1
+    c1, c2 = _Conv(w1.to(DEV), b1.to(DEV)), _Conv(w2.to(DEV), b2.to(DEV))
+    xd = x.transpose(1, 2).contiguous().to(DEV)
+    y = torch.empty_like(xd)
+    nat.call("fm_resblock", xd.data_ptr(), B, L, C, c1.w.data_ptr(), c1.b.data_ptr(), c2.w.data_ptr(),
+             c2.b.data_ptr(), elu_out, y.data_ptr(), stream())
+    torch.cuda.synchronize()
+    xd64 = x.double()
+    h = F.elu(causal_conv1d(F.elu(xd64), w1.double(), b1.double()))
+    want = xd64 + causal_conv1d(h, w2.double(), b2.double())
+    if elu_out:
+        want = F.elu(want)
+    close(y.cpu().transpose(1, 2), want, rel=5e-5)
+
+
 def test_conv1d_crop(ws):
     g = torch.Generator().manual_seed(5)
     x = torch.randn(2, 8, 100, generator=g)
@@ -128,7 +156,7 @@ def test_conv1d_crop(ws):
 
 @pytest.mark.parametrize("B,cin,cout,stride,L", [
     (1, 1024, 512, 8, 250), (2, 512, 256, 6, 40), (1, 256, 128, 5, 300),
-    (1, 128, 64, 4, 1000), (1, 4, 2, 2, 7), (2, 8, 4, 2, 1)])
+    (1, 128, 64, 4, 1000), (1, 4, 2, 2, 7), (2, 8, 4, 2, 1), (1, 128, 64, 4, 40000)])
 def test_conv_transpose1d(B, cin, cout, stride, L, ws):
     g = torch.Generator().manual_seed(cin + L)
     x = torch.randn(B, cin, L, generator=g)
@@ -144,11 +172,12 @@ def test_conv_transpose1d(B, cin, cout, stride, L, ws):
     close(y.cpu().transpose(1, 2), want)
 
 
-def run_linear(x, w_t, flags=0, res=None, scale=None, ws=None, out=None):
+def run_linear(x, w, flags=0, res=None, scale=None, ws=None, out=None):
+    """y = x @ w^T with w given as [out, in] (the packed W^T layout)."""
     rows, k = x.shape
-    n = w_t.shape[1]
+    n = w.shape[0]
     y = torch.empty((rows, n), device=DEV) if out is None else out
-    nat.call("fm_linear", x.data_ptr(), rows, k, w_t.data_ptr(), n, flags,
+    nat.call("fm_linear", x.data_ptr(), rows, k, w.data_ptr(), n, flags,
              None if res is None else res.data_ptr(), None if scale is None else scale.data_ptr(),
              y.data_ptr(), ws.data_ptr(), WS_BYTES, stream())
     torch.cuda.synchronize()
@@ -161,7 +190,7 @@ def test_linear_epilogues(rows, k, n, ws):
     g = torch.Generator().manual_seed(rows + k + n)
     x = torch.randn(rows, k, generator=g)
     w = torch.randn(n, k, generator=g) * 0.05
-    xd, wd = x.to(DEV), w.t().contiguous().to(DEV)
+    xd, wd = x.to(DEV), w.to(DEV)
     close(run_linear(xd, wd, ws=ws).cpu(), x.double() @ w.double().t())
     close(run_linear(xd, wd, nat.EPI_GELU, ws=ws).cpu(), F.gelu(x.double() @ w.double().t()))
     res = torch.randn(rows, n, generator=g)
@@ -343,3 +372,15 @@ def test_bad_arguments_are_rejected():
         nat.call("fm_layer_norm", None, None, None, 4, 8, 1e-5, None, stream())
     with pytest.raises(nat.NativeError, match="unsupported"):
         nat.call("fm_window_attention", 1, 8, 0, 0, 0, 1, 1, 1, 1, 1, 1, 12, 8, 1.0, 1, 8, stream())
+
+
+def test_split_k_is_deterministic(ws):
+    """Small-M, large-K GEMMs split K across the waves of a block and across
+    blocks; both sums run in a fixed order, so repeated calls agree bit for bit."""
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(250, 8192, generator=g).to(DEV)
+    w = (torch.randn(1024, 8192, generator=g) * 0.01).to(DEV)
+    first = run_linear(x, w, ws=ws).clone()
+    second = run_linear(x, w, ws=ws)
+    assert torch.equal(first, second)
+    close(first.cpu(), x.double().cpu() @ w.double().cpu().t())
