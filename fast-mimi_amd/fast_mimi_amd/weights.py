@@ -158,17 +158,17 @@ def state_dict_spec(config: MimiConfig) -> list[TensorSpec]:
                 ("acoustic", config.num_quantizers - config.num_semantic_quantizers))
     for branch, count in branches:
         p = f"quantizer.{branch}_residual_vector_quantizer"
-        if vq != config.hidden_size:
-            specs.append(TensorSpec(f"{p}.input_proj.weight", (vq, config.hidden_size, 1),
-                                    "conv_w", fan_in=config.hidden_size))
-            specs.append(TensorSpec(f"{p}.output_proj.weight", (config.hidden_size, vq, 1),
-                                    "conv_w", fan_in=vq))
         for j in range(count):
             cb = f"{p}.layers.{j}.codebook"
             specs.append(TensorSpec(f"{cb}.initialized", (1,), "ones"))
             specs.append(TensorSpec(f"{cb}.cluster_usage", (config.codebook_size,), "ones"))
             specs.append(TensorSpec(f"{cb}.embed_sum",
                                     (config.codebook_size, config.codebook_dim), "codebook"))
+        if vq != config.hidden_size:
+            specs.append(TensorSpec(f"{p}.input_proj.weight", (vq, config.hidden_size, 1),
+                                    "conv_w", fan_in=config.hidden_size))
+            specs.append(TensorSpec(f"{p}.output_proj.weight", (config.hidden_size, vq, 1),
+                                    "conv_w", fan_in=vq))
     return specs
 
 

@@ -1,0 +1,180 @@
+/*
+ * fast_mimi_amd.h — C ABI of libfast_mimi_amd.so, the MI355X (gfx950) kernels
+ * of the Mimi codec encode/decode hot path.
+ *
+ * Conventions (all entry points):
+ *   - Pointers are device pointers (hipMalloc / torch CUDA tensors); sizes are
+ *     element counts.  Activations are FP32, channels-last: a tensor of `batch`
+ *     items, `length` positions and `channels` channels is the contiguous array
+ *     [batch][length][channels].  The reference keeps NCL ([batch][channels]
+ *     [length]); for 1-channel audio the two layouts coincide.
+ *   - Work is enqueued on `stream`; nothing synchronizes.  Calls sharing a
+ *     `workspace` must be ordered on one stream.
+ *   - Return value: 0 on success, 1000 bad argument, 1001 workspace too small,
+ *     1002 unsupported shape, otherwise the hipError_t of the launch.
+ *   - Packed weights ("W^T layout") are [N][K] row-major with K contiguous:
+ *       Conv1d weight [C_out][C_in][k]     -> [C_out][k * C_in], k-major:
+ *                                             element (co, tap*C_in + ci) = w[co][ci][tap]
+ *       ConvTranspose1d weight [C_in][C_out][k], k = taps * stride
+ *                                          -> [stride * C_out][taps * C_in]:
+ *                                             element (r*C_out + co, jj*C_in + ci)
+ *                                             = w[ci][co][r + (taps - 1 - jj) * stride]
+ *       Linear weight [out][in]            -> unchanged.
+ *
+ * Each entry point names the reference interface (kadirnar/fast-mimi,
+ * src/fast_mimi/...) whose computation it replaces.
+ */
+#ifndef FAST_MIMI_AMD_H_
+#define FAST_MIMI_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hipStream_t;
+
+/* Epilogue / loader flags (bit set). */
+enum {
+  FM_ELU_IN = 1,        /* ELU applied to the input as it is loaded            */
+  FM_REPLICATE = 2,     /* internal: replicate padding (use pad_mode = 1)      */
+  FM_EPI_ELU = 4,       /* ELU on the output                                   */
+  FM_EPI_GELU = 8,      /* exact-erf GELU on the output                        */
+  FM_EPI_RES_ADD = 16,  /* y = residual + (acc + bias)                         */
+  FM_EPI_RES_SCALE = 32 /* y = residual + scale[n] * acc   (fm_linear only)    */
+};
+
+/* ABI version of the library (bumped when a contract changes). */
+int fm_abi_version(void);
+
+/*
+ * Causal Conv1d, dilation 1: left zero (pad_mode 0) or edge (pad_mode 1)
+ * padding of kernel - stride, right padding to a multiple of the stride;
+ * output length ceil(length / stride), of which the first y_length rows per
+ * batch item are written (y is [batch][y_length][out_channels]).
+ * Replaces MimiConv1d.forward + _pad1d + _get_extra_padding_for_conv1d
+ * (model.py:697-797) and the cuDNN exact encoder convs (_optimized_runtime.py:937-1218).
+ * workspace: optional scratch for K-split partial sums (may be NULL).
+ */
+int fm_conv1d(const float* x, int batch, int length, int in_channels, const float* weight_packed,
+              const float* bias, int out_channels, int kernel, int stride, int pad_mode, int flags,
+              const float* residual, float* y, int y_length, float* workspace,
+              size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Causal ConvTranspose1d with the full right trim (trim ratio 1): output
+ * [batch][length * stride][out_channels].  kernel must be a multiple of stride.
+ * Replaces MimiConvTranspose1d.forward (model.py:886-897),
+ * mimi_cutlass_bias_dgrad (cutlass_bias_dgrad.cu:147-157) and the cuDNN
+ * deconvolutions (_optimized_runtime.py:571-753).
+ */
+int fm_conv_transpose1d(const float* x, int batch, int length, int in_channels,
+                        const float* weight_packed, const float* bias, int out_channels, int kernel,
+                        int stride, int flags, const float* residual, float* y, float* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * y[rows][out] = epilogue(x[rows][in] . W^T), no bias.  residual/scale feed
+ * FM_EPI_RES_SCALE (LayerScale residual; y may alias residual).
+ * Replaces the nn.Linear projections of MimiAttention / MimiMLP
+ * (model.py:1870-1961, :1990-1999), the RVQ 1x1 in/out projections
+ * (model.py:2408-2444) and _packed_qkv.py:139-150.
+ */
+int fm_linear(const float* x, int rows, int in_features, const float* weight_packed,
+              int out_features, int flags, const float* residual, const float* scale, float* y,
+              float* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Fused SEANet residual block: y = ELU?(x + conv1x1(ELU(conv_k3(ELU(x))))),
+ * hidden width channels/2, x and y [batch][length][channels], x != y.
+ * Supported widths: fm_resblock_supported(channels) != 0.
+ * Replaces MimiResnetBlock.forward (model.py:947-971), decoder9_fused_wmma
+ * (decoder9_fused_wmma.cu:87-112) and the Triton _add_elu_half_kernel
+ * (_optimized_runtime.py:37-77).
+ */
+int fm_resblock_supported(int channels);
+int fm_resblock(const float* x, int batch, int length, int channels, const float* w1_packed,
+                const float* b1, const float* w2_packed, const float* b2, int elu_out, float* y,
+                hipStream_t stream);
+
+/*
+ * LayerNorm over the last dimension (biased variance).
+ * Replaces nn.LayerNorm in MimiTransformerLayer (model.py:2028-2061).
+ */
+int fm_layer_norm(const float* x, const float* gamma, const float* beta, long rows, int channels,
+                  float eps, float* y, hipStream_t stream);
+
+/*
+ * Causal sliding-window attention with RoPE: q, k, v are read from the
+ * packed projection qkv ([batch*length][ld_qkv], head h of q at column
+ * q_offset + h*head_dim, likewise k / v with kv_heads heads); cos/sin tables
+ * are [length][head_dim].  Key k is visible from query q iff
+ * q - window < k <= q.  out is [batch*length][ld_out], head h at h*head_dim.
+ * head_dim in {8, 16, 32, 64}.
+ * Replaces _apply_rope + F.scaled_dot_product_attention / the eager path of
+ * MimiAttention.forward (model.py:1551-1569, :1870-1961), _attention_mask
+ * (model.py:1627-1688), _native_window_attention (model.py:1589-1624), the
+ * Triton _rope_kernel / _packed_qkv_rope_kernel / _attention_pack_nlc_kernel
+ * (_optimized_runtime.py:80-258, _packed_qkv.py:14-131).
+ */
+int fm_window_attention(const float* qkv, int ld_qkv, int q_offset, int k_offset, int v_offset,
+                        const float* cos_table, const float* sin_table, int batch, int length,
+                        int heads, int kv_heads, int head_dim, int window, float scale, float* out,
+                        int ld_out, hipStream_t stream);
+
+/*
+ * Codebook preparation: embed = embed_sum / max(cluster_usage, eps), its
+ * transpose [dim][entries] and squared norms [entries].
+ * Replaces MimiEuclideanCodebook.embed (model.py:2263-2275).
+ */
+int fm_rvq_prepare_codebook(const float* embed_sum, const float* cluster_usage, int entries,
+                            int dim, float eps, float* embed, float* embed_t, float* norms,
+                            hipStream_t stream);
+
+/* Bytes of workspace fm_rvq_encode needs for `rows` query rows. */
+size_t fm_rvq_workspace_bytes(int rows, int dim, int entries);
+
+/*
+ * Residual VQ encode of one branch: for codebooks 0..count-1 in order,
+ * code = argmin_e sqrt(max(|x|^2 + |e|^2 - 2 x.e, 0)) (lowest index on ties),
+ * x -= embed[code].  x rows have pitch ld_x; dim a multiple of 4.
+ * Codes are int64, row (b, t) of codebook j at
+ * codes[b * batch_stride + j * rows_per_batch + t].
+ * embeds / embeds_t / norms: the branch's codebooks, contiguous per codebook.
+ * Replaces MimiResidualVectorQuantizer.encode + MimiEuclideanCodebook.quantize
+ * (model.py:2277-2291, :2408-2428) and the compiled RVQ encode.
+ */
+int fm_rvq_encode(const float* x, int ld_x, int rows, int rows_per_batch, int dim, int entries,
+                  int count, const float* embeds, const float* embeds_t, const float* norms,
+                  int64_t* codes, int batch_stride, void* workspace, size_t workspace_bytes,
+                  hipStream_t stream);
+
+/*
+ * Split-RVQ decode gather-sum: out[(b*frames + t)][0:dim] = 0 + E_0[c_0]
+ * (the num_semantic first codebooks summed left to right),
+ * out[...][dim:2*dim] = 0 + E_s[c_s] + E_{s+1}[c_{s+1}] + ... left to right.
+ * codes int64 [batch][num_codebooks][frames]; embeds [num_codebooks][entries][dim].
+ * Out-of-range codes produce NaN.
+ * Replaces launch_split_rvq_decode_q32 (_cuda_rvq.py:77-89) and
+ * MimiResidualVectorQuantizer.decode (model.py:2430-2444).
+ */
+int fm_rvq_decode(const int64_t* codes, int batch, int num_codebooks, int frames,
+                  int num_semantic, const float* embeds, int entries, int dim, float* out,
+                  hipStream_t stream);
+
+/*
+ * Depthwise causal ConvTranspose1d (groups == channels), right-trimmed to
+ * length * stride; weight is the reference [channels][1][kernel].
+ * Replaces the bottleneck upsample (model.py:2744-2752).
+ */
+int fm_upsample_depthwise(const float* x, int batch, int length, int channels,
+                          const float* weight, int kernel, int stride, float* y,
+                          hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FAST_MIMI_AMD_H_ */
