@@ -17,7 +17,9 @@
 // so every lane fetches its A and B fragments for four MFMAs with one 16-byte
 // LDS read each.  Tiles (256 threads; k-tile BK = 64 for the large tiles so a
 // k-tile's MFMA work outlasts the next tile's global-load latency):
-//   128x128 (2x2 waves of 64x64), 128x64 (4x1 of 32x64), 128x32 (4x1 of 32x32);
+//   256x128 / 256x64 (8 waves of 64x64 / 64x32, one k-tile prefetched in
+//   registers), 128x128 (2x2 waves of 64x64), 128x64 (4x1 of 32x64),
+//   128x32 (4x1 of 32x32);
 //   32x64 with the four waves splitting K (summed through LDS in wave order)
 //   when the large tiles cannot fill the GPU, plus global K-splits summed in
 //   split order by a second kernel for very long K.  All sums are in a fixed
@@ -315,6 +317,162 @@ __global__ __launch_bounds__(NTHREADS) void gemm_fast_kernel(GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Large-tile kernel: BM = 256 rows, BN in {64, 128}, BK = 32, 8 waves (two
+// per SIMD) of up to 64x64 outputs each.  A
+// k-tile carries far more MFMA work than the next tile's global-load latency,
+// so a single LDS stage refilled from a one-tile register prefetch keeps the
+// MFMA pipes busy; the second wave per SIMD overlaps one wave's load/store
+// code with the other's MFMAs.  Loads are branch-free (clamped address plus a
+// select) so the in-order instruction stream stays short.
+template <int BN, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
+  constexpr int NTH = 64 * WM * WN;
+  constexpr int BM = 256, BK = 32, P = BK + 4, CPR = BK / 4, HK = BK / 2;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int RPP = NTH / CPR;               // tile rows covered per pass
+  constexpr int APT = BM / RPP, BPT = BN / RPP;
+  static_assert(FM >= 1 && FN >= 1 && BPT >= 1 && APT * RPP == BM && BPT * RPP == BN, "tiling");
+
+  __shared__ __attribute__((aligned(16))) float As[BM * P];
+  __shared__ __attribute__((aligned(16))) float Bs[BN * P];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
+  const long M = (long)p.batch * p.rows;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int tile = tile_index();
+  const long m0 = (long)(tile / tiles_n) * BM;
+  const int n0 = (tile % tiles_n) * BN;
+  const int k_begin = blockIdx.y * p.k_split;
+  const int k_end = min(p.K, k_begin + p.k_split);
+  const bool replicate = p.flags & FM_REPLICATE;
+  const bool tap_uniform = (p.C_in % BK) == 0;
+  const int ck = (tid % CPR) * 4;
+  const int rrow = tid / CPR;
+
+  // Per-row window origin: element offset of position p0 of batch b, p0 and
+  // b*L.  Rows past M get p0 = INT_MIN / 2 so every position test fails.
+  long a_org[APT];
+  int a_p0[APT], a_bL[APT];
+#pragma unroll
+  for (int i = 0; i < APT; ++i) {
+    const long m = min(m0 + rrow + i * RPP, M - 1);
+    const int b = (int)(m / p.rows);
+    const int t = (int)(m - (long)b * p.rows);
+    a_p0[i] = (m0 + rrow + i * RPP < M) ? t * p.rs - p.padL : INT_MIN / 2;
+    a_bL[i] = b * p.L_in;
+    a_org[i] = (long)b * p.L_in * p.C_in;
+  }
+  int b_n[BPT];
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) b_n[i] = n0 + rrow + i * RPP;
+
+  floatx4 ra[APT], rb[BPT];
+  auto load = [&](int k0) {
+    const int kg = k0 + ck;
+    const bool kok = kg < k_end;
+    const int kc = min(kg, p.K - 4);
+    const int tap = tap_uniform ? k0 / p.C_in : kc / p.C_in;
+    const int cin = kc - tap * p.C_in;  // channel within the position
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+      const int pos = a_p0[i] + tap;
+      const bool ok = kok && (replicate ? a_p0[i] > INT_MIN / 2 : (pos >= 0 && pos < p.L_in));
+      const int pc = min(max(pos, 0), p.L_in - 1);
+      const floatx4 v = *reinterpret_cast<const floatx4*>(p.x + a_org[i] + (long)pc * p.C_in + cin);
+      ra[i] = ok ? v : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      const bool ok = kok && b_n[i] < p.N;
+      const floatx4 v = *reinterpret_cast<const floatx4*>(p.w + (long)min(b_n[i], p.N - 1) * p.K + kc);
+      rb[i] = ok ? v : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  };
+
+  floatx16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int h = lane >> 5, lcol = lane & 31;
+  const bool elu_in = p.flags & FM_ELU_IN;
+  if (k_begin < k_end) load(k_begin);
+  for (int k0 = k_begin; k0 < k_end; k0 += BK) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+      floatx4 v = ra[i];
+      if (elu_in) v = floatx4{fm_elu(v.x), fm_elu(v.y), fm_elu(v.z), fm_elu(v.w)};
+      *reinterpret_cast<floatx4*>(As + (rrow + i * RPP) * P + ck) = v;
+    }
+#pragma unroll
+    for (int i = 0; i < BPT; ++i)
+      *reinterpret_cast<floatx4*>(Bs + (rrow + i * RPP) * P + ck) = rb[i];
+    __syncthreads();
+    if (k0 + BK < k_end) load(k0 + BK);
+#pragma unroll
+    for (int s4 = 0; s4 < BK / 8; ++s4) {
+      floatx4 a[FM], b[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        a[i] = *reinterpret_cast<const floatx4*>(As + (wm0 + i * 32 + lcol) * P + h * HK + s4 * 4);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        b[j] = *reinterpret_cast<const floatx4*>(Bs + (wn0 + j * 32 + lcol) * P + h * HK + s4 * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) acc[i][j] = fm_mfma32(a[i][e], b[j][e], acc[i][j]);
+    }
+  }
+
+  const bool crop = p.y_rows != p.rows;
+  const bool has_res = p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE);
+  float* part = p.partial ? p.partial + (long)blockIdx.y * M * p.N : nullptr;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int n = n0 + wn0 + j * 32 + lcol;
+    const int nc = min(n, p.N - 1);
+    const float bias = p.bias ? p.bias[nc % p.bias_len] : 0.0f;
+    const float scale = (p.flags & FM_EPI_RES_SCALE) ? p.scale[nc] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      // Residual loads of this 32-row block first, then its 16 stores.
+      float rv[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const long m = min(m0 + wm0 + i * 32 + fm_mfma32_row(r, lane), M - 1);
+        rv[r] = (has_res && !part) ? p.res[m * p.N + nc] : 0.0f;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const long m = m0 + wm0 + i * 32 + fm_mfma32_row(r, lane);
+        if (m >= M || n >= p.N) continue;
+        if (part) {
+          part[m * p.N + n] = acc[i][j][r];
+          continue;
+        }
+        const float v = epilogue_v(acc[i][j][r], bias, rv[r], scale, p.flags);
+        if (!crop) {
+          p.y[m * p.N + n] = v;
+        } else {
+          const int b = (int)(m / p.rows);
+          const int t = (int)(m - (long)b * p.rows);
+          if (t < p.y_rows) p.y[((long)b * p.y_rows + t) * p.N + n] = v;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Generic kernel: 64x64 tiles, one output element pair per thread per step,
 // scalar loads.  Used only when C_in or K is not a multiple of 4.
 __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
@@ -488,9 +646,11 @@ __global__ __launch_bounds__(256) void conv_cout1_kernel(const float* __restrict
 struct TileCfg {
   int BM, BN, WK, BK, id;
 };
-// Candidates in order of preference; the first that gives >= 2 blocks per CU wins.
-constexpr TileCfg kTiles[] = {{128, 128, 1, 64, 0}, {128, 64, 1, 64, 1}, {128, 32, 1, 64, 2},
+// Candidates, largest first: the first whose tile count covers the CUs wins.
+constexpr TileCfg kTiles[] = {{256, 128, 1, 32, 5}, {256, 64, 1, 32, 6},
+                              {128, 128, 1, 64, 0}, {128, 64, 1, 64, 1}, {128, 32, 1, 64, 2},
                               {32, 64, 4, 32, 3}};
+constexpr long kFillBlocks = 224;  // ~0.9 blocks per CU
 
 long tile_count(long M, int N, const TileCfg& t) {
   return ((M + t.BM - 1) / t.BM) * ((N + t.BN - 1) / t.BN);
@@ -514,12 +674,13 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     cfg = TileCfg{64, 64, 1, 16, -1};
     tiles = tile_count(M, p.N, cfg);
   } else {
-    // Skip shapes wider than the output (by more than 2x for the narrowest).
+    // Largest tile that still fills the GPU; tiles more than 2x wider than
+    // the output are skipped (the narrowest fallback is always eligible).
     for (const TileCfg& t : kTiles) {
       if (t.WK == 1 && t.BN > 32 && t.BN / 2 >= p.N) continue;
       cfg = t;
       tiles = tile_count(M, p.N, t);
-      if (tiles >= 512) break;
+      if (tiles >= kFillBlocks) break;
     }
   }
   // Global K-split for long K when even the K-split tile leaves CUs idle.
@@ -544,6 +705,8 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     case 1: hipLaunchKernelGGL((gemm_fast_kernel<128, 64, 4, 1, 1, 64>), grid, dim3(NTHREADS), 0, s, p); break;
     case 2: hipLaunchKernelGGL((gemm_fast_kernel<128, 32, 4, 1, 1, 64>), grid, dim3(NTHREADS), 0, s, p); break;
     case 3: hipLaunchKernelGGL((gemm_fast_kernel<32, 64, 1, 1, 4, 32>), grid, dim3(NTHREADS), 0, s, p); break;
+    case 5: hipLaunchKernelGGL((gemm_big_kernel<128, 4, 2>), grid, dim3(512), 0, s, p); break;
+    case 6: hipLaunchKernelGGL((gemm_big_kernel<64, 4, 2>), grid, dim3(512), 0, s, p); break;
     default: hipLaunchKernelGGL(gemm_generic_kernel, grid, dim3(256), 0, s, p); break;
   }
   hipError_t e = hipGetLastError();

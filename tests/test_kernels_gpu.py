@@ -77,6 +77,9 @@ CONV_CASES = [
     (1, 64, 32, 3, 1, 140000),     # 256x32 tiles
     (1, 32, 64, 1, 1, 70000),      # 128x64 tiles
     (1, 64, 256, 4, 2, 70000),     # 128x128 tiles
+    (1, 64, 128, 8, 4, 240000),    # 256x128 tiles
+    (1, 64, 64, 3, 1, 60000),      # 256x64 tiles
+    (2, 128, 256, 10, 5, 300000),  # 256x256 tiles, batch seam inside a tile
 ]
 
 
@@ -156,7 +159,8 @@ def test_conv1d_crop(ws):
 
 @pytest.mark.parametrize("B,cin,cout,stride,L", [
     (1, 1024, 512, 8, 250), (2, 512, 256, 6, 40), (1, 256, 128, 5, 300),
-    (1, 128, 64, 4, 1000), (1, 4, 2, 2, 7), (2, 8, 4, 2, 1), (1, 128, 64, 4, 40000)])
+    (1, 128, 64, 4, 1000), (1, 4, 2, 2, 7), (2, 8, 4, 2, 1), (1, 128, 64, 4, 40000),
+    (1, 128, 64, 4, 60000)])
 def test_conv_transpose1d(B, cin, cout, stride, L, ws):
     g = torch.Generator().manual_seed(cin + L)
     x = torch.randn(B, cin, L, generator=g)
@@ -185,7 +189,8 @@ def run_linear(x, w, flags=0, res=None, scale=None, ws=None, out=None):
 
 
 @pytest.mark.parametrize("rows,k,n", [(250, 512, 1536), (4000, 512, 2048), (250, 2048, 512),
-                                      (1, 512, 512), (37, 16, 48), (125, 512, 512)])
+                                      (1, 512, 512), (37, 16, 48), (125, 512, 512),
+                                      (60000, 256, 256), (60001, 96, 200)])
 def test_linear_epilogues(rows, k, n, ws):
     g = torch.Generator().manual_seed(rows + k + n)
     x = torch.randn(rows, k, generator=g)
