@@ -50,8 +50,8 @@ FM_DEVICE float rope1(float x, float partner, int d, int half, float c, float s)
 }
 
 // Stages rows t0 .. t0+31 (rows past t_last read as zero) of one head of the
-// packed projection into a transposed LDS tile dst[d * P + r] with RoPE
-// applied.  Each of the NTH cooperating threads owns N elements; all global
+// packed projection into a transposed LDS tile dst[d * P + r], with RoPE
+// applied unless cos_t is null (rows already rotated by their producer).  Each of the NTH cooperating threads owns N elements; all global
 // loads are issued before any use so they overlap.
 template <int N, int NTH, int D, int DP, int P>
 FM_DEVICE void stage_rope_t(float* dst, int tid, const float* __restrict__ qkv, int ld, int col0,
@@ -68,16 +68,18 @@ FM_DEVICE void stage_rope_t(float* dst, int tid, const float* __restrict__ qkv, 
     if (t <= t_last && d < D) {
       const float* row = qkv + (base + t) * ld + col0;
       x[u] = row[d];
-      xp[u] = row[d < HALF ? d + HALF : d - HALF];
-      c[u] = cos_t[(long)t * D + d];
-      sn[u] = sin_t[(long)t * D + d];
+      if (cos_t) {
+        xp[u] = row[d < HALF ? d + HALF : d - HALF];
+        c[u] = cos_t[(long)t * D + d];
+        sn[u] = sin_t[(long)t * D + d];
+      }
     }
   }
 #pragma unroll
   for (int u = 0; u < N; ++u) {
     const int e = tid + u * NTH;
     const int r = e / DP, d = e % DP;
-    dst[d * P + r] = rope1(x[u], xp[u], d, HALF, c[u], sn[u]);
+    dst[d * P + r] = cos_t ? rope1(x[u], xp[u], d, HALF, c[u], sn[u]) : x[u];
   }
 }
 
@@ -223,9 +225,197 @@ __global__ __launch_bounds__(256) void window_attention_kernel(
   }
 }
 
+
+// Row-block linear layer for the transformer projections (K = hidden = 512):
+//   y = epilogue( LN?(x) . W^T )
+// A block of NWV waves owns 32 rows x BN output columns.  Its 32 input rows
+// are loaded once, TPR = 2*NWV consecutive lanes per row; when gamma is given
+// the LayerNorm statistics are reduced from those registers with lane
+// shuffles and the rows are normalised before they are written to LDS, so the
+// LayerNorm costs no launch or LDS pass of its own.  The waves split K; each
+// wave fetches its weight fragments straight from global memory into
+// registers (all issued before any use), so no staging or barrier sits in the
+// MFMA loop.  The k-slot of lane half h at step 4q+e carries k = 16h + 4q + e,
+// matching 16-byte LDS reads of A.  Partial tiles are summed through LDS in
+// wave order, then the epilogue applies, per flag: RoPE (x*cos +
+// rotate_half(x)*sin within each 64-wide head, for columns < rope_cols; needs
+// BN == 64), exact GELU, or y = res + scale * acc.
+template <int K, int BN, int NWV>
+__global__ __launch_bounds__(64 * NWV) void row_linear_kernel(
+    const float* __restrict__ x, int rows, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float eps, const float* __restrict__ w, int N, int flags,
+    const float* res, const float* __restrict__ scale, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, int rope_cols, int rows_per_seq, float* y) {
+  constexpr int BM = 32, NTH = 64 * NWV, PA = K + 4, KW = K / NWV, KT = KW / 32, NJ = BN / 32;
+  constexpr int PR = BN + 4, TPR = NTH / BM, CH = K / 4 / TPR, OPT = BM * BN / NTH;
+  static_assert(KW % 32 == 0 && CH >= 1 && OPT % 2 == 0, "tile shape");
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  float* As = sm;   // [BM][PA]
+  float* red = sm;  // after the MFMAs: [NWV][BM][PR]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, lcol = lane & 31;
+  const long m0 = (long)blockIdx.x * BM;
+  const int n0 = blockIdx.y * BN;
+  const int kw0 = wave * KW;
+
+  // Weight fragments for this wave's k-slice.
+  floatx4 bw[NJ][KT][4];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const float* wr = w + (long)(n0 + j * 32 + lcol) * K + kw0 + 16 * h;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bw[j][kt][q] = *reinterpret_cast<const floatx4*>(wr + kt * 32 + 4 * q);
+  }
+  // Row r = tid / TPR; lane part p holds float4 chunks p, p + TPR, ...
+  {
+    const int r = tid / TPR, p = tid % TPR;
+    const bool valid = m0 + r < rows;
+    const float* xr = x + min(m0 + r, (long)rows - 1) * K;
+    floatx4 v[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) v[u] = *reinterpret_cast<const floatx4*>(xr + 4 * (p + TPR * u));
+    if (gamma) {
+      floatx4 gv[CH], bv[CH];
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        gv[u] = *reinterpret_cast<const floatx4*>(gamma + 4 * (p + TPR * u));
+        bv[u] = *reinterpret_cast<const floatx4*>(beta + 4 * (p + TPR * u));
+      }
+      float s = 0.0f;
+#pragma unroll
+      for (int u = 0; u < CH; ++u) s += (v[u][0] + v[u][1]) + (v[u][2] + v[u][3]);
+#pragma unroll
+      for (int o = 1; o < TPR; o <<= 1) s += __shfl_xor(s, o, 64);
+      const float mean = s / (float)K;
+      float var = 0.0f;
+#pragma unroll
+      for (int u = 0; u < CH; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float d = v[u][e] - mean;
+          var = fmaf(d, d, var);
+        }
+#pragma unroll
+      for (int o = 1; o < TPR; o <<= 1) var += __shfl_xor(var, o, 64);
+      const float rstd = 1.0f / sqrtf(var / (float)K + eps);
+#pragma unroll
+      for (int u = 0; u < CH; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[u][e] = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(v[u][e], mean), rstd), gv[u][e]), bv[u][e]);
+    }
+#pragma unroll
+    for (int u = 0; u < CH; ++u)
+      *reinterpret_cast<floatx4*>(As + r * PA + 4 * (p + TPR * u)) =
+          valid ? v[u] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  __syncthreads();
+
+  floatx16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const floatx4 a = *reinterpret_cast<const floatx4*>(As + lcol * PA + kw0 + kt * 32 + 16 * h + 4 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) acc[j] = fm_mfma32(a[e], bw[j][kt][q][e], acc[j]);
+    }
+  __syncthreads();  // all waves are done with As; reuse it for the partial tiles
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[(wave * BM + fm_mfma32_row(r, lane)) * PR + j * 32 + lcol] = acc[j][r];
+  __syncthreads();
+  // Sum the partial tiles in wave order (OPT consecutive outputs per thread).
+  const int er = tid / TPR, ec = (tid % TPR) * OPT;
+  float out[OPT];
+#pragma unroll
+  for (int c = 0; c < OPT; ++c) {
+    float v = red[er * PR + ec + c];
+#pragma unroll
+    for (int g = 1; g < NWV; ++g) v = __fadd_rn(v, red[(g * BM + er) * PR + ec + c]);
+    out[c] = v;
+  }
+  const long m = m0 + er;
+  const bool rope = BN == 64 && cos_t && n0 < rope_cols;
+  if (rope) {
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < OPT; ++c) red[er * PR + ec + c] = out[c];
+    __syncthreads();
+  }
+  if (m >= rows) return;
+  const int t = (int)(m % rows_per_seq);
+#pragma unroll
+  for (int c = 0; c < OPT; ++c) {
+    const int n = n0 + ec + c;
+    float v = out[c];
+    if (rope) {
+      const int d = ec + c;  // dim within the 64-wide head
+      const float partner = red[er * PR + (d < 32 ? d + 32 : d - 32)];
+      const float rot = d < 32 ? -partner : partner;
+      v = __fadd_rn(__fmul_rn(v, cos_t[(long)t * 64 + d]), __fmul_rn(rot, sin_t[(long)t * 64 + d]));
+    }
+    if (flags & FM_EPI_GELU) v = fm_gelu(v);
+    if (flags & FM_EPI_RES_SCALE) v = __fadd_rn(res[m * N + n], __fmul_rn(scale[n], v));
+    out[c] = v;
+  }
+  float* dst = y + m * N + n0 + ec;
+#pragma unroll
+  for (int c = 0; c < OPT; c += 2) *reinterpret_cast<float2*>(dst + c) = float2{out[c], out[c + 1]};
+}
+
 }  // namespace
 
 extern "C" {
+
+// Transformer projection with optional fused LayerNorm prologue (gamma/beta
+// non-null), RoPE epilogue on columns < rope_cols (cos/sin non-null; head_dim
+// 64, tables [rows_per_seq][64]), GELU or LayerScale-residual epilogue.
+// in_features must be 512 (Mimi's hidden width); out_features a multiple of 64.
+int fm_row_linear_supported(int in_features, int out_features) {
+  return in_features == 512 && out_features % 64 == 0;
+}
+
+int fm_row_linear(const float* x, int rows, int in_features, const float* ln_gamma,
+                  const float* ln_beta, float ln_eps, const float* weight, int out_features,
+                  int flags, const float* residual, const float* scale, const float* rope_cos,
+                  const float* rope_sin, int rope_cols, int rows_per_seq, float* y,
+                  hipStream_t stream) {
+  if (!x || !weight || !y || rows < 0 || rows_per_seq <= 0 || (ln_gamma && !ln_beta))
+    return FM_BAD_ARGUMENT;
+  if (!fm_row_linear_supported(in_features, out_features)) return FM_UNSUPPORTED;
+  if ((flags & FM_EPI_RES_SCALE) && (!residual || !scale)) return FM_BAD_ARGUMENT;
+  if (rope_cos && (!rope_sin || rope_cols % 64)) return FM_BAD_ARGUMENT;
+  if (rows == 0) return FM_OK;
+  constexpr int K = 512;
+  // 64-wide column tiles where RoPE needs whole heads, else 32-wide tiles (twice the blocks,
+  // half the MFMA chain per wave); 8 waves split K.
+  const bool wide = rope_cos != nullptr;
+#define FM_ROWLIN(BN, NWV)                                                                       \
+  {                                                                                              \
+    const size_t lds = std::max<size_t>((size_t)32 * (K + 4), (size_t)NWV * 32 * (BN + 4)) * 4;  \
+    hipLaunchKernelGGL((row_linear_kernel<K, BN, NWV>), dim3((rows + 31) / 32, out_features / BN), \
+                       dim3(64 * NWV), lds, stream, x, rows, ln_gamma, ln_beta, ln_eps, weight,   \
+                       out_features, flags, residual, scale, rope_cos, rope_sin, rope_cols,      \
+                       rows_per_seq, y);                                                         \
+  }
+  if (wide)
+    FM_ROWLIN(64, 8)
+  else
+    FM_ROWLIN(32, 8)
+#undef FM_ROWLIN
+  return (int)hipGetLastError();
+}
 
 int fm_layer_norm(const float* x, const float* gamma, const float* beta, long rows, int channels,
                   float eps, float* y, hipStream_t stream) {
@@ -241,7 +431,7 @@ int fm_window_attention(const float* qkv, int ld_qkv, int q_offset, int k_offset
                         const float* cos_table, const float* sin_table, int batch, int length,
                         int heads, int kv_heads, int head_dim, int window, float scale, float* out,
                         int ld_out, hipStream_t stream) {
-  if (!qkv || !cos_table || !sin_table || !out || batch < 0 || length < 0 || heads <= 0 ||
+  if (!qkv || !cos_table != !sin_table || !out || batch < 0 || length < 0 || heads <= 0 ||
       kv_heads <= 0 || heads % kv_heads || window <= 0)
     return FM_BAD_ARGUMENT;
   if (batch == 0 || length == 0) return FM_OK;

@@ -35,6 +35,11 @@ from .weights import decoder_layer_indices, encoder_layer_indices
 _WORKSPACE_BYTES = 64 << 20
 
 
+# Up to this many rows the transformer projections run as row-block kernels with
+# LayerNorm / RoPE fused; above it, tiled GEMMs amortise the weight reads better.
+_ROW_LINEAR_MAX_ROWS = 1024
+
+
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -217,6 +222,18 @@ class MimiRuntime:
                  self._stream())
         return y
 
+    def _row_linear(self, x, rows, w, flags=0, residual=None, scale=None, out=None, ln=None,
+                    rope=None):
+        """Transformer projection with LayerNorm prologue / RoPE epilogue fused."""
+        n, k = w.shape
+        y = torch.empty((rows, n), device=self.device) if out is None else out
+        g, b = (ln[0].data_ptr(), ln[1].data_ptr()) if ln is not None else (None, None)
+        cos, sin, rope_cols, per_seq = rope if rope is not None else (None, None, 0, 1)
+        self._call("fm_row_linear", x.data_ptr(), rows, k, g, b, self.config.norm_eps,
+                   w.data_ptr(), n, flags, _ptr(residual), _ptr(scale), _ptr(cos), _ptr(sin),
+                   rope_cols, per_seq, y.data_ptr(), self._stream())
+        return y
+
     def _resblock(self, x, B, L, block, elu_after: bool, tag: str = "res"):
         c1, c2 = block
         if c1.k == 3 and nat.library().fm_resblock_supported(c2.c_out):
@@ -257,24 +274,39 @@ class MimiRuntime:
         xln = torch.empty((M, C), device=self.device)
         att = torch.empty((M, nh * hd), device=self.device)
         s = self._stream()
+        lib = nat.library()
+        fused = (M <= _ROW_LINEAR_MAX_ROWS and hd == 64 and lib.fm_row_linear_supported(C, layers[0].wqkv.shape[0])
+                 and lib.fm_row_linear_supported(C, layers[0].w1.shape[0])
+                 and lib.fm_row_linear_supported(nh * hd, C))
+        rope_cols = (nh + nkv) * hd
         for li, lay in enumerate(layers):
-            self._tag = f"{tag}{li}.ln1"
-            self._call("fm_layer_norm", h.data_ptr(), lay.ln1[0].data_ptr(), lay.ln1[1].data_ptr(),
-                     M, C, cfg.norm_eps, xln.data_ptr(), s)
-            self._tag = f"{tag}{li}.qkv"
-            qkv = self._linear(xln, M, lay.wqkv)
+            if fused:
+                self._tag = f"{tag}{li}.qkv"
+                qkv = self._row_linear(h, M, lay.wqkv, ln=lay.ln1, rope=(cos, sin, rope_cols, T))
+            else:
+                self._tag = f"{tag}{li}.ln1"
+                self._call("fm_layer_norm", h.data_ptr(), lay.ln1[0].data_ptr(),
+                           lay.ln1[1].data_ptr(), M, C, cfg.norm_eps, xln.data_ptr(), s)
+                self._tag = f"{tag}{li}.qkv"
+                qkv = self._linear(xln, M, lay.wqkv)
             ld = qkv.shape[1]
             self._tag = f"{tag}{li}.attn"
+            tabs = (None, None) if fused else (cos.data_ptr(), sin.data_ptr())
             self._call("fm_window_attention", qkv.data_ptr(), ld, 0, nh * hd, (nh + nkv) * hd,
-                     cos.data_ptr(), sin.data_ptr(), B, T, nh, nkv, hd, cfg.sliding_window,
-                     1.0 / (hd ** 0.5), att.data_ptr(), nh * hd, s)
+                       tabs[0], tabs[1], B, T, nh, nkv, hd, cfg.sliding_window,
+                       1.0 / (hd ** 0.5), att.data_ptr(), nh * hd, s)
             self._tag = f"{tag}{li}.o"
-            self._linear(att, M, lay.wo, nat.EPI_RES_SCALE, residual=h, scale=lay.ls1, out=h)
-            self._tag = f"{tag}{li}.ln2"
-            self._call("fm_layer_norm", h.data_ptr(), lay.ln2[0].data_ptr(), lay.ln2[1].data_ptr(),
-                     M, C, cfg.norm_eps, xln.data_ptr(), s)
-            self._tag = f"{tag}{li}.fc1"
-            ff = self._linear(xln, M, lay.w1, nat.EPI_GELU)
+            if fused:
+                self._row_linear(att, M, lay.wo, nat.EPI_RES_SCALE, residual=h, scale=lay.ls1, out=h)
+                self._tag = f"{tag}{li}.fc1"
+                ff = self._row_linear(h, M, lay.w1, nat.EPI_GELU, ln=lay.ln2)
+            else:
+                self._linear(att, M, lay.wo, nat.EPI_RES_SCALE, residual=h, scale=lay.ls1, out=h)
+                self._tag = f"{tag}{li}.ln2"
+                self._call("fm_layer_norm", h.data_ptr(), lay.ln2[0].data_ptr(),
+                           lay.ln2[1].data_ptr(), M, C, cfg.norm_eps, xln.data_ptr(), s)
+                self._tag = f"{tag}{li}.fc1"
+                ff = self._linear(xln, M, lay.w1, nat.EPI_GELU)
             self._tag = f"{tag}{li}.fc2"
             self._linear(ff, M, lay.w2, nat.EPI_RES_SCALE, residual=h, scale=lay.ls2, out=h)
         return h.reshape(B, T, C)

@@ -100,6 +100,28 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
                 hipStream_t stream);
 
 /*
+ * Transformer projection y[rows][out] = epilogue(LN?(x) . W^T), no bias:
+ *   - ln_gamma/ln_beta non-NULL: x rows are layer-normalised (biased variance,
+ *     eps ln_eps) inside the kernel first;
+ *   - rope_cos/rope_sin non-NULL ([rows_per_seq][64] tables): columns below
+ *     rope_cols (a multiple of 64) get RoPE per 64-wide head, position
+ *     row % rows_per_seq;
+ *   - flags: FM_EPI_GELU, or FM_EPI_RES_SCALE (y = residual + scale[n] * acc,
+ *     y may alias residual).
+ * Supported shapes: fm_row_linear_supported(in, out) != 0 (in == 512, out a
+ * multiple of 64).  Replaces the LayerNorm + q/k/v projection + _apply_rope
+ * and LayerNorm + fc1 + GELU sequences of MimiTransformerLayer
+ * (model.py:2028-2061, :1870-1961, :1551-1569, :1990-1999) and the Triton
+ * _packed_qkv_rope_kernel (_packed_qkv.py:14-131).
+ */
+int fm_row_linear_supported(int in_features, int out_features);
+int fm_row_linear(const float* x, int rows, int in_features, const float* ln_gamma,
+                  const float* ln_beta, float ln_eps, const float* weight, int out_features,
+                  int flags, const float* residual, const float* scale, const float* rope_cos,
+                  const float* rope_sin, int rope_cols, int rows_per_seq, float* y,
+                  hipStream_t stream);
+
+/*
  * LayerNorm over the last dimension (biased variance).
  * Replaces nn.LayerNorm in MimiTransformerLayer (model.py:2028-2061).
  */
@@ -110,7 +132,8 @@ int fm_layer_norm(const float* x, const float* gamma, const float* beta, long ro
  * Causal sliding-window attention with RoPE: q, k, v are read from the
  * packed projection qkv ([batch*length][ld_qkv], head h of q at column
  * q_offset + h*head_dim, likewise k / v with kv_heads heads); cos/sin tables
- * are [length][head_dim].  Key k is visible from query q iff
+ * are [length][head_dim]; with both tables NULL, q and k are taken as already
+ * rotated (e.g. by fm_row_linear's RoPE epilogue).  Key k is visible from query q iff
  * q - window < k <= q.  out is [batch*length][ld_out], head h at h*head_dim.
  * head_dim in {8, 16, 32, 64}.
  * Replaces _apply_rope + F.scaled_dot_product_attention / the eager path of

@@ -252,6 +252,84 @@ def test_window_attention(B, T, H, D, window):
     close(out.cpu(), attention_reference(qkv, B, T, H, D, window, cos, sin), rel=5e-5)
 
 
+def test_window_attention_prerotated():
+    """NULL RoPE tables: q/k are consumed as given (rotated by their producer)."""
+    B, T, H, D, window = 1, 300, 8, 64, 250
+    g = torch.Generator().manual_seed(5)
+    qkv = torch.randn(B * T, 3 * H * D, generator=g)
+    cfg = MimiConfig()
+    cos, sin = rope_tables(cfg, T)
+    q, k, v = qkv.view(T, 3, H, D).unbind(1)
+    rot = MimiOracle._rotate_half
+    pre = torch.stack([q * cos[:, None] + rot(q) * sin[:, None],
+                       k * cos[:, None] + rot(k) * sin[:, None], v], 1).reshape(T, 3 * H * D)
+    out = torch.empty(B * T, H * D, device=DEV)
+    pre_d = pre.contiguous().to(DEV)
+    nat.call("fm_window_attention", pre_d.data_ptr(), 3 * H * D, 0, H * D, 2 * H * D, None, None,
+             B, T, H, H, D, window, 1.0 / math.sqrt(D), out.data_ptr(), H * D, stream())
+    torch.cuda.synchronize()
+    close(out.cpu(), attention_reference(qkv, B, T, H, D, window, cos, sin), rel=5e-5)
+
+
+def run_row_linear(x, w, flags=0, ln=None, rope=None, res=None, scale=None, out=None):
+    rows, k = x.shape
+    n = w.shape[0]
+    y = torch.empty(rows, n, device=DEV) if out is None else out
+    g, b = ln if ln is not None else (None, None)
+    cos, sin, rope_cols, per_seq = rope if rope is not None else (None, None, 0, 1)
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    nat.call("fm_row_linear", x.data_ptr(), rows, k, p(g), p(b), 1e-5, w.data_ptr(), n, flags,
+             p(res), p(scale), p(cos), p(sin), rope_cols, per_seq, y.data_ptr(), stream())
+    torch.cuda.synchronize()
+    return y
+
+
+@pytest.mark.parametrize("rows", [250, 1, 33, 500, 4000])
+def test_row_linear(rows):
+    """LayerNorm prologue + RoPE / GELU / LayerScale-residual epilogues vs float64."""
+    g = torch.Generator().manual_seed(rows)
+    k, H, D = 512, 8, 64
+    x = torch.randn(rows, k, generator=g) * 2 + 0.5
+    gamma, beta = torch.rand(k, generator=g) + 0.5, torch.randn(k, generator=g) * 0.1
+    wqkv = torch.randn(3 * k, k, generator=g) * 0.04
+    w1 = torch.randn(2048, k, generator=g) * 0.04
+    wo = torch.randn(k, k, generator=g) * 0.04
+    T = 250 if rows >= 250 else rows
+    cos, sin = rope_tables(MimiConfig(), T)
+    d = {name: t.to(DEV) for name, t in dict(x=x, gamma=gamma, beta=beta, wqkv=wqkv, w1=w1, wo=wo,
+                                             cos=cos, sin=sin).items()}
+    xn = F.layer_norm(x.double(), (k,), gamma.double(), beta.double(), 1e-5)
+    # Plain product and LN + product.
+    close(run_row_linear(d["x"], d["wo"]).cpu(), x.double() @ wo.double().t())
+    # LN + qkv + RoPE on q and k (positions row % T).
+    got = run_row_linear(d["x"], d["wqkv"], ln=(d["gamma"], d["beta"]),
+                         rope=(d["cos"], d["sin"], 2 * k, T)).cpu()
+    want = xn @ wqkv.double().t()
+    t = torch.arange(rows) % T
+    c, s = cos.double()[t][:, None], sin.double()[t][:, None]
+    qk = want[:, : 2 * k].reshape(rows, 2 * H, D)
+    want[:, : 2 * k] = (qk * c + MimiOracle._rotate_half(qk) * s).reshape(rows, 2 * k)
+    close(got, want)
+    # LN + fc1 + GELU.
+    close(run_row_linear(d["x"], d["w1"], nat.EPI_GELU, ln=(d["gamma"], d["beta"])).cpu(),
+          F.gelu(xn @ w1.double().t()))
+    # LayerScale residual, in place.
+    res = torch.randn(rows, k, generator=g)
+    scale = torch.rand(k, generator=g) * 0.1
+    h = res.to(DEV)
+    run_row_linear(d["x"], d["wo"], nat.EPI_RES_SCALE, res=h, scale=scale.to(DEV), out=h)
+    close(h.cpu(), res.double() + scale.double() * (x.double() @ wo.double().t()))
+
+
+def test_row_linear_rejects():
+    lib = nat.library()
+    assert lib.fm_row_linear_supported(512, 1536) and not lib.fm_row_linear_supported(2048, 512)
+    x = torch.zeros(4, 2048, device=DEV)
+    w = torch.zeros(512, 2048, device=DEV)
+    with pytest.raises(nat.NativeError, match="unsupported"):
+        run_row_linear(x, w)
+
+
 def prepare_codebooks(embed_sum, usage):
     n, e, d = embed_sum.shape
     emb = torch.empty(n, e, d, device=DEV)
