@@ -43,72 +43,118 @@ constexpr int KB = 32;  // keys per MFMA row tile
 constexpr int NW = 4;   // waves per block; they split the key range
 
 // RoPE as the reference writes it: x*cos + rotate_half(x)*sin, each product
-// and the sum rounded separately.
-FM_DEVICE float rope1(float x, float partner, int d, int half, float c, float s) {
-  const float rot = d < half ? -partner : partner;
-  return __fadd_rn(__fmul_rn(x, c), __fmul_rn(rot, s));
+// and the sum rounded separately.  For the pair (x_d, x_{d+half}) with the
+// shared angle (cos, sin): lo' = lo*c - hi*s, hi' = hi*c + lo*s.
+FM_DEVICE void rope_pair(floatx4& lo, floatx4& hi, const floatx4& c, const floatx4& s) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float l = lo[e], u = hi[e];
+    lo[e] = __fadd_rn(__fmul_rn(l, c[e]), __fmul_rn(-u, s[e]));
+    hi[e] = __fadd_rn(__fmul_rn(u, c[e]), __fmul_rn(l, s[e]));
+  }
 }
 
-// Stages rows t0 .. t0+31 (rows past t_last read as zero) of one head of the
-// packed projection into a transposed LDS tile dst[d * P + r], with RoPE
-// applied unless cos_t is null (rows already rotated by their producer).  Each of the NTH cooperating threads owns N elements; all global
-// loads are issued before any use so they overlap.
-template <int N, int NTH, int D, int DP, int P>
-FM_DEVICE void stage_rope_t(float* dst, int tid, const float* __restrict__ qkv, int ld, int col0,
-                            const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-                            long base, int t0, int t_last) {
-  constexpr int HALF = D / 2;
-  float x[N], xp[N], c[N], sn[N];
+// Rows t0 .. t0+31 of one head of Q or K (D dims, row pitch ld), held as
+// float4 pairs (dims 4c.. and 4c + D/2..) so that RoPE's partners sit in the
+// same lane; rows past t_last read as zero.  NTH threads share the tile.
+template <int D, int NTH, bool ROPE>
+struct RowTile {
+  static constexpr int HALF = D / 2, PAIRS = QB * D / 8;
+  static constexpr int N = (PAIRS + NTH - 1) / NTH;
+  floatx4 lo[N], hi[N], c[N], s[N];
+
+  FM_DEVICE void load(int tid, const float* __restrict__ src, long ld, int t0, int t_last,
+                      const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
 #pragma unroll
-  for (int u = 0; u < N; ++u) {
-    const int e = tid + u * NTH;
-    const int r = e / DP, d = e % DP;
-    const int t = t0 + r;
-    x[u] = xp[u] = c[u] = sn[u] = 0.0f;
-    if (t <= t_last && d < D) {
-      const float* row = qkv + (base + t) * ld + col0;
-      x[u] = row[d];
-      if (cos_t) {
-        xp[u] = row[d < HALF ? d + HALF : d - HALF];
-        c[u] = cos_t[(long)t * D + d];
-        sn[u] = sin_t[(long)t * D + d];
+    for (int u = 0; u < N; ++u) {
+      const int e = tid + u * NTH;
+      const int r = e / (D / 8), d = (e % (D / 8)) * 4;
+      const int t = min(t0 + r, t_last);
+      const bool ok = e < PAIRS && t0 + r <= t_last;
+      const float* row = src + (long)t * ld;
+      lo[u] = *reinterpret_cast<const floatx4*>(row + d);
+      hi[u] = *reinterpret_cast<const floatx4*>(row + d + HALF);
+      if (ROPE) {
+        c[u] = *reinterpret_cast<const floatx4*>(cos_t + (long)t * D + d);
+        s[u] = *reinterpret_cast<const floatx4*>(sin_t + (long)t * D + d);
       }
+      if (!ok) lo[u] = hi[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
   }
+  // Writes the tile to dst[row * pitch + dim], rotated when ROPE.
+  FM_DEVICE void store(int tid, float* dst, int pitch) {
 #pragma unroll
-  for (int u = 0; u < N; ++u) {
-    const int e = tid + u * NTH;
-    const int r = e / DP, d = e % DP;
-    dst[d * P + r] = cos_t ? rope1(x[u], xp[u], d, HALF, c[u], sn[u]) : x[u];
+    for (int u = 0; u < N; ++u) {
+      const int e = tid + u * NTH;
+      if (PAIRS % NTH && e >= PAIRS) continue;
+      const int r = e / (D / 8), d = (e % (D / 8)) * 4;
+      floatx4 l = lo[u], h = hi[u];
+      if (ROPE) rope_pair(l, h, c[u], s[u]);
+      *reinterpret_cast<floatx4*>(dst + r * pitch + d) = l;
+      *reinterpret_cast<floatx4*>(dst + r * pitch + d + HALF) = h;
+    }
   }
+};
+
+// V rows t0 .. t0+31 (zero past t_last and in the padded dims D..DP).
+template <int D, int DP>
+struct VTile {
+  static constexpr int CHUNKS = QB * DP / 4, N = (CHUNKS + 63) / 64;
+  floatx4 v[N];
+  FM_DEVICE void load(int lane, const float* __restrict__ src, long ld, int t0, int t_last) {
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
+      const int e = lane + u * 64;
+      const int r = e / (DP / 4), d = (e % (DP / 4)) * 4;
+      const int t = min(t0 + r, t_last);
+      v[u] = *reinterpret_cast<const floatx4*>(src + (long)t * ld + min(d, D - 4));
+      if (!(e < CHUNKS && t0 + r <= t_last && d < D)) v[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+  FM_DEVICE void store(int lane, float* dst, int pitch) {
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
+      const int e = lane + u * 64;
+      if (CHUNKS % 64 && e >= CHUNKS) continue;
+      const int r = e / (DP / 4), d = (e % (DP / 4)) * 4;
+      *reinterpret_cast<floatx4*>(dst + r * pitch + d) = v[u];
+    }
+  }
+};
+
+// Orders this wave's LDS accesses: everything before completes before
+// anything after is issued (the compiler may not move memory ops across).
+FM_DEVICE void wave_lds_fence() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
 }
 
 // Sliding-window causal attention on FP32 MFMA.
 // Grid: (ceil(T / QB), heads, batch), 256 threads.  Block = 32 queries of one
 // head; its key range [q0 - window + 1, q0 + 31] is cut into 32-key tiles that
-// the 4 waves take round-robin, one tile per wave per round.  Q (once) and
-// each wave's K tile are staged through LDS with row-contiguous loads and RoPE
-// applied on the way in, stored transposed ([dim][32], odd pitch).  Per tile a
-// wave computes S^T = K Q^T (keys on MFMA rows, queries on columns, lane l
-// owns query q0 + l % 32), applies the window mask and an online softmax per
+// the 4 waves take round-robin.  Waves run independently after the shared Q
+// stage: each keeps its next K/V tile in flight in registers while it
+// computes on the current one from its own LDS slot (rows contiguous, K pitch
+// D+4, V pitch DP+8).  Per tile a wave computes S^T = K Q^T (keys on MFMA
+// rows, queries on columns, lane l owns query q0 + l % 32; the k-slot of lane
+// half h at step 4j+e carries dim D/2*h + 4j + e so both operands come from
+// 16-byte LDS reads), applies the window mask and an online softmax per
 // column, then accumulates O^T += V^T P^T with P^T fed straight from the S^T
-// registers: MFMA step s takes keys 8*(s/4) + 4*h + s%4 (h = lane / 32),
-// exactly the rows that lane holds in accumulator slot s.  V is read straight
-// from global memory (lanes read consecutive dims).  The waves' (max, sum, O)
-// are merged through LDS.
-template <int D>
+// registers: MFMA step s takes keys 8*(s/4) + 4*h + s%4, exactly the rows
+// that lane holds in accumulator slot s.  The waves' (max, sum, O) are merged
+// through LDS.  ROPE: rotate Q and K while staging (else they arrive rotated).
+template <int D, bool ROPE>
 __global__ __launch_bounds__(256) void window_attention_kernel(
     const float* __restrict__ qkv, int ld, int q_off, int k_off, int v_off,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, int T, int heads,
     int kv_heads, int window, float scale, float* __restrict__ out, int ld_out) {
   constexpr int DT = (D + 31) / 32;  // 32-row tiles of O^T
-  constexpr int DP = DT * 32;        // padded head dim
-  constexpr int KS = DP / 2;         // MFMA k-steps of the QK^T product
-  constexpr int HALF = D / 2;
-  constexpr int P = QB + 1;          // pitch of the transposed [dim][32] tiles
-  // Region 0: per-wave K tiles during the loop, per-wave O^T at the merge.
-  __shared__ float stage[NW][DP * P];
-  __shared__ float Qt[DP * P];
+  constexpr int DP = DT * 32;        // padded head dim of V / O
+  constexpr int PK = D + 4, PV = DP + 8, P = QB + 1;
+  constexpr int SLOT = QB * PK + KB * PV;  // per-wave K + V tile
+  static_assert(DP * P <= SLOT, "merge tile fits the slot");
+  __shared__ __attribute__((aligned(16))) float stage[NW][SLOT];
+  __shared__ __attribute__((aligned(16))) float Qs[QB * PK];
   __shared__ float Mm[NW][QB];
   __shared__ float Lm[NW][QB];
 
@@ -121,15 +167,30 @@ __global__ __launch_bounds__(256) void window_attention_kernel(
   const int q = q0 + col;
   const int k_lo = max(0, q0 - window + 1);
   const int k_hi = min(T, q0 + QB) - 1;
-  const long base = b * (long)T;
+  const float* seq = qkv + b * (long)T * ld;
+  const float* kcol = seq + k_off + hk * D;
+  const float* vcol = seq + v_off + hk * D;
 
-  // Stage Q^T with RoPE (zero for padded dims / rows past T).
-  stage_rope_t<QB * DP / 256, 256, D, DP, P>(Qt, tid, qkv, ld, q_off + head * D, cos_t, sin_t,
-                                            base, q0, T - 1);
+  const int ntiles = (k_hi - k_lo + KB) / KB;
+  RowTile<D, 64, ROPE> kr;
+  VTile<D, DP> vr;
+  if (wave < ntiles) {
+    kr.load(lane, kcol, ld, k_lo + wave * KB, k_hi, cos_t, sin_t);
+    vr.load(lane, vcol, ld, k_lo + wave * KB, k_hi);
+  }
+  {
+    RowTile<D, 256, ROPE> qr;
+    qr.load(tid, seq + q_off + head * D, ld, q0, T - 1, cos_t, sin_t);
+    qr.store(tid, Qs, PK);
+  }
   __syncthreads();
-  float qv[KS];
+  float qv[D / 2];
 #pragma unroll
-  for (int i = 0; i < KS; ++i) qv[i] = Qt[(2 * i + h) * P + col];
+  for (int j = 0; j < D / 8; ++j) {
+    const floatx4 t4 = *reinterpret_cast<const floatx4*>(Qs + col * PK + (D / 2) * h + 4 * j);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qv[4 * j + e] = t4[e];
+  }
 
   float m_run = -INFINITY, l_run = 0.0f;
   floatx16 o[DT];
@@ -138,25 +199,27 @@ __global__ __launch_bounds__(256) void window_attention_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
 
-  float* Kt = stage[wave];
-  const int ntiles = (k_hi - k_lo + KB) / KB;
-  const int rounds = (ntiles + NW - 1) / NW;
-  for (int round = 0; round < rounds; ++round) {
-    const int tile = round * NW + wave;
+  float* Ks = stage[wave];
+  float* Vs = Ks + QB * PK;
+  for (int tile = wave; tile < ntiles; tile += NW) {
     const int k0 = k_lo + tile * KB;
-    const bool active = tile < ntiles;
-    __syncthreads();  // previous round's reads of Kt are done
-    if (active)
-      stage_rope_t<KB * DP / 64, 64, D, DP, P>(Kt, lane, qkv, ld, k_off + hk * D, cos_t, sin_t,
-                                              base, k0, k_hi);
-    __syncthreads();
-    if (!active) continue;
+    kr.store(lane, Ks, PK);
+    vr.store(lane, Vs, PV);
+    wave_lds_fence();
+    if (tile + NW < ntiles) {  // next tile's loads overlap this tile's math
+      kr.load(lane, kcol, ld, k0 + NW * KB, k_hi, cos_t, sin_t);
+      vr.load(lane, vcol, ld, k0 + NW * KB, k_hi);
+    }
 
     floatx16 s;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < KS; ++i) s = fm_mfma32(Kt[(2 * i + h) * P + col], qv[i], s);
+    for (int j = 0; j < D / 8; ++j) {
+      const floatx4 a4 = *reinterpret_cast<const floatx4*>(Ks + col * PK + (D / 2) * h + 4 * j);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s = fm_mfma32(a4[e], qv[4 * j + e], s);
+    }
 
     float cmax = -INFINITY;
 #pragma unroll
@@ -185,16 +248,11 @@ __global__ __launch_bounds__(256) void window_attention_kernel(
       for (int r = 0; r < 16; ++r) o[t][r] *= corr;
 #pragma unroll
     for (int st = 0; st < 16; ++st) {
-      const int key = k0 + 8 * (st >> 2) + 4 * h + (st & 3);
-      const bool vok = key <= k_hi;
-      const float* vrow = qkv + (base + (vok ? key : k_lo)) * ld + v_off + hk * D;
+      const float* vrow = Vs + (8 * (st >> 2) + 4 * h + (st & 3)) * PV + col;
 #pragma unroll
-      for (int t = 0; t < DT; ++t) {
-        const int d = t * 32 + col;
-        const float vv = (vok && d < D) ? vrow[d] : 0.0f;
-        o[t] = fm_mfma32(vv, s[st], o[t]);
-      }
+      for (int t = 0; t < DT; ++t) o[t] = fm_mfma32(vrow[t * 32], s[st], o[t]);
     }
+    wave_lds_fence();  // this tile's LDS reads are done before the slot is rewritten
   }
 
   // Merge the waves: O = sum_w O_w exp(m_w - M), L = sum_w l_w exp(m_w - M).
@@ -221,7 +279,7 @@ __global__ __launch_bounds__(256) void window_attention_kernel(
       num += stage[w][d * P + qi] * f;
       den += Lm[w][qi] * f;
     }
-    out[(base + qg) * ld_out + head * D + d] = num / den;
+    out[(b * (long)T + qg) * ld_out + head * D + d] = num / den;
   }
 }
 
@@ -434,12 +492,19 @@ int fm_window_attention(const float* qkv, int ld_qkv, int q_offset, int k_offset
   if (!qkv || !cos_table != !sin_table || !out || batch < 0 || length < 0 || heads <= 0 ||
       kv_heads <= 0 || heads % kv_heads || window <= 0)
     return FM_BAD_ARGUMENT;
+  // Q/K/V rows are read as float4s.
+  if ((ld_qkv | q_offset | k_offset | v_offset) % 4) return FM_BAD_ARGUMENT;
   if (batch == 0 || length == 0) return FM_OK;
   dim3 grid((length + QB - 1) / QB, heads, batch);
-#define FM_ATT(DV)                                                                          \
-  hipLaunchKernelGGL(window_attention_kernel<DV>, grid, dim3(256), 0, stream, qkv, ld_qkv,  \
-                     q_offset, k_offset, v_offset, cos_table, sin_table, length, heads,     \
-                     kv_heads, window, scale, out, ld_out)
+#define FM_ATT(DV)                                                                         \
+  if (cos_table)                                                                           \
+    hipLaunchKernelGGL((window_attention_kernel<DV, true>), grid, dim3(256), 0, stream, qkv, \
+                       ld_qkv, q_offset, k_offset, v_offset, cos_table, sin_table, length,  \
+                       heads, kv_heads, window, scale, out, ld_out);                        \
+  else                                                                                     \
+    hipLaunchKernelGGL((window_attention_kernel<DV, false>), grid, dim3(256), 0, stream,   \
+                       qkv, ld_qkv, q_offset, k_offset, v_offset, cos_table, sin_table,     \
+                       length, heads, kv_heads, window, scale, out, ld_out)
   switch (head_dim) {
     case 8: FM_ATT(8); break;
     case 16: FM_ATT(16); break;

@@ -135,7 +135,7 @@ int fm_layer_norm(const float* x, const float* gamma, const float* beta, long ro
  * are [length][head_dim]; with both tables NULL, q and k are taken as already
  * rotated (e.g. by fm_row_linear's RoPE epilogue).  Key k is visible from query q iff
  * q - window < k <= q.  out is [batch*length][ld_out], head h at h*head_dim.
- * head_dim in {8, 16, 32, 64}.
+ * head_dim in {8, 16, 32, 64}; ld_qkv and the offsets are multiples of 4.
  * Replaces _apply_rope + F.scaled_dot_product_attention / the eager path of
  * MimiAttention.forward (model.py:1551-1569, :1870-1961), _attention_mask
  * (model.py:1627-1688), _native_window_attention (model.py:1589-1624), the
