@@ -20,6 +20,7 @@
 namespace {
 
 constexpr int RB = 32;  // query rows per block
+constexpr int kMaxChunks = 64;  // entry chunks per step (partials per row)
 
 FM_DEVICE bool better(float v, int i, float bv, int bi) {
   return v < bv || (v == bv && i < bi);
@@ -216,6 +217,188 @@ __global__ __launch_bounds__(256) void rvq_step_kernel(StepArgs a) {
   }
 }
 
+// Fast step kernel for dim in {64, 128, 256}.  Block = RB query rows x one
+// chunk of entries, 4 waves = EG entry groups x KP k-parts (KP * EG == 4).
+// MFMA rows are codebook entries (A operand loaded straight from the
+// row-major codebook into registers, one 64-dim piece ahead of its use),
+// columns are queries (B operand from the LDS residual rows).  In a 64-dim
+// piece the k-slot of lane half h at step 4j+e carries dim 32h + 4j + e, so
+// both operands are 16-byte reads.  Each lane then holds the 16 candidate
+// distances of its query for one 32-entry sub-tile, so the argmin is a
+// register scan plus one cross-half shuffle.  With KP > 1 every wave owns one
+// sub-tile and one k-part; partial dot products are summed through LDS in
+// k-part order before the distances.  The prologue resolves step j-1 (eight
+// lanes per row, shuffle-reduced) and forms residual_j and |residual_j|^2.
+template <int DIM, int KP>
+__global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a, const float* __restrict__ embed) {
+  constexpr int EG = 4 / KP, KW = DIM / KP, NPC = KW / 64, PX = DIM + 4, PR = RB + 1;
+  constexpr int CH = DIM / 32;  // float4 chunks per lane in the prologue (8 lanes per row)
+  static_assert(KW % 64 == 0, "k-part of whole 64-dim pieces");
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  float* Xs = smem;                      // [RB][PX]
+  float* xnS = Xs + RB * PX;             // [RB]
+  float* bestv = xnS + RB;               // [EG][RB]
+  int* besti = reinterpret_cast<int*>(bestv + EG * RB);
+  float* red = reinterpret_cast<float*>(besti + EG * RB);  // [KP-1][EG][32 * PR]
+  float* normS = red + (KP - 1) * EG * 32 * PR;            // [chunk_entries]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = wave % EG, p = wave / EG;
+  const int h = lane >> 5, col = lane & 31;
+  const long m0 = (long)blockIdx.x * RB;
+  const int chunk = blockIdx.y;
+  const int e_begin = chunk * a.chunk_entries;
+  const int e_end = min(a.entries, e_begin + a.chunk_entries);
+
+  // ---- prologue: row r = tid / 8, lane part pt = tid % 8.
+  {
+    const int r = tid >> 3, pt = tid & 7;
+    const long m = m0 + r;
+    const long mc = min(m, (long)a.M - 1);
+    const bool valid = m < a.M;
+    int code = 0;
+    if (a.prev_embed) {
+      float bv = INFINITY;
+      int bi = 0x7fffffff;
+      for (int c = pt; c < a.chunks; c += 8) {
+        const float v = a.prev_val[(long)c * a.M + mc];
+        const int i = a.prev_idx[(long)c * a.M + mc];
+        if (better(v, i, bv, bi)) bv = v, bi = i;
+      }
+#pragma unroll
+      for (int o = 1; o < 8; o <<= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (better(ov, oi, bv, bi)) bv = ov, bi = oi;
+      }
+      code = bi;
+      if (chunk == 0 && pt == 0 && valid) {
+        const long b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
+        a.prev_codes[b * a.batch_stride + t] = code;
+      }
+    }
+    floatx4 xv[CH], ev[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      xv[u] = *reinterpret_cast<const floatx4*>(a.resid_in + mc * a.ld_in + 4 * (pt + 8 * u));
+      if (a.prev_embed)
+        ev[u] = *reinterpret_cast<const floatx4*>(a.prev_embed + (long)code * DIM + 4 * (pt + 8 * u));
+    }
+    for (int c = tid; c < e_end - e_begin; c += 256) normS[c] = a.norms[e_begin + c];
+    float xn = 0.0f;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      floatx4 x = xv[u];
+      if (a.prev_embed) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = __fsub_rn(x[e], ev[u][e]);
+        if (chunk == 0 && valid && a.resid_out)
+          *reinterpret_cast<floatx4*>(a.resid_out + m * DIM + 4 * (pt + 8 * u)) = x;
+      }
+      if (!valid) x = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xn = fmaf(x[e], x[e], xn);
+      *reinterpret_cast<floatx4*>(Xs + r * PX + 4 * (pt + 8 * u)) = x;
+    }
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) xn += __shfl_xor(xn, o, 64);
+    if (pt == 0) xnS[r] = xn;
+  }
+  __syncthreads();
+
+  // ---- distance tiles.
+  const float xq = xnS[col];
+  float best_v = INFINITY;
+  int best_i = 0x7fffffff;
+  const int nsub = (e_end - e_begin + 31) / 32;
+  const int my_sub = (nsub - g + EG - 1) / EG;  // sub-tiles g, g+EG, ...
+  const int items = (KP == 1) ? my_sub * NPC : NPC;
+  const int kbase = p * KW;
+  floatx4 cur[8], nxt[8];
+  auto load_piece = [&](floatx4* dst, int item) {
+    const int st = g + EG * ((KP == 1) ? item / NPC : 0);
+    const int pc = item % NPC;
+    const int entry = min(e_begin + 32 * st + col, a.entries - 1);
+    const float* src = embed + (long)entry * DIM + kbase + 64 * pc + 32 * h;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dst[j] = *reinterpret_cast<const floatx4*>(src + 4 * j);
+  };
+  floatx16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  const bool has_work = KP == 1 ? items > 0 : g < nsub;
+  if (has_work) load_piece(cur, 0);
+  for (int it = 0; it < (has_work ? items : 0); ++it) {
+    if (it + 1 < items) load_piece(nxt, it + 1);
+    const int pc = it % NPC;
+    const float* xrow = Xs + col * PX + kbase + 64 * pc + 32 * h;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const floatx4 b4 = *reinterpret_cast<const floatx4*>(xrow + 4 * j);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = fm_mfma32(cur[j][e], b4[e], acc);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cur[j] = nxt[j];
+    if (KP == 1 && pc == NPC - 1) {
+      const int n0 = e_begin + 32 * (g + EG * (it / NPC));
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int entry = n0 + fm_mfma32_row(r, lane);
+        if (entry < e_end) {
+          const float d = __fadd_rn(__fadd_rn(__fmul_rn(-2.0f, acc[r]), xq), normS[entry - e_begin]);
+          const float dist = sqrtf(fmaxf(d, 0.0f));
+          if (better(dist, entry, best_v, best_i)) best_v = dist, best_i = entry;
+        }
+        acc[r] = 0.0f;
+      }
+    }
+  }
+  if (KP > 1) {
+    if (p > 0) {
+      float* dst = red + ((p - 1) * EG + g) * 32 * PR;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dst[fm_mfma32_row(r, lane) * PR + col] = acc[r];
+    }
+    __syncthreads();
+    if (p == 0 && g < nsub) {
+      const int n0 = e_begin + 32 * g;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = fm_mfma32_row(r, lane);
+        float v = acc[r];
+#pragma unroll
+        for (int pp = 1; pp < KP; ++pp) v = __fadd_rn(v, red[((pp - 1) * EG + g) * 32 * PR + row * PR + col]);
+        const int entry = n0 + row;
+        if (entry < e_end) {
+          const float d = __fadd_rn(__fadd_rn(__fmul_rn(-2.0f, v), xq), normS[entry - e_begin]);
+          const float dist = sqrtf(fmaxf(d, 0.0f));
+          if (better(dist, entry, best_v, best_i)) best_v = dist, best_i = entry;
+        }
+      }
+    }
+  }
+  {
+    const float ov = __shfl_xor(best_v, 32, 64);
+    const int oi = __shfl_xor(best_i, 32, 64);
+    if (better(ov, oi, best_v, best_i)) best_v = ov, best_i = oi;
+  }
+  if (p == 0 && h == 0) bestv[g * RB + col] = best_v, besti[g * RB + col] = best_i;
+  __syncthreads();
+  if (tid < RB) {
+    const long m = m0 + tid;
+    float v = bestv[tid];
+    int i = besti[tid];
+#pragma unroll
+    for (int gg = 1; gg < EG; ++gg)
+      if (better(bestv[gg * RB + tid], besti[gg * RB + tid], v, i)) v = bestv[gg * RB + tid], i = besti[gg * RB + tid];
+    if (m < a.M) {
+      a.val[(long)chunk * a.M + m] = v;
+      a.idx[(long)chunk * a.M + m] = i;
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void rvq_finalize_kernel(const float* val, const int* idx,
                                                            int chunks, int M, int64_t* codes,
                                                            int rows_per_batch, int batch_stride) {
@@ -295,7 +478,8 @@ int fm_rvq_prepare_codebook(const float* embed_sum, const float* cluster_usage, 
 
 // Partials workspace needed by fm_rvq_encode, in bytes.
 size_t fm_rvq_workspace_bytes(int rows, int dim, int entries) {
-  const int chunks = 16;
+  (void)entries;
+  const int chunks = kMaxChunks;
   return (size_t)2 * rows * dim * sizeof(float) + (size_t)2 * chunks * rows * (sizeof(float) + sizeof(int)) + 256;
 }
 
@@ -315,19 +499,41 @@ int fm_rvq_encode(const float* x, int ld_x, int rows, int rows_per_batch, int di
   if (!workspace || workspace_bytes < fm_rvq_workspace_bytes(rows, dim, entries))
     return FM_WORKSPACE_TOO_SMALL;
   const int row_blocks = (rows + RB - 1) / RB;
-  // Enough chunks to spread one step over the GPU; chunks are multiples of 128 entries.
-  int chunks = 1;
-  while (chunks < 16 && row_blocks * chunks < 512 && entries / (chunks * 2) >= NT) chunks *= 2;
-  const int chunk_entries = ((entries + chunks - 1) / chunks + NT - 1) / NT * NT;
+  // Fast kernel: KP k-parts per 32-entry sub-tile while the launch stays
+  // within ~1024 blocks, else 128-entry (or larger) chunks.  General kernel:
+  // chunks doubling until the launch has 512 blocks, multiples of NT entries.
+  const bool fast = (dim == 64 || dim == 128 || dim == 256);
+  int chunks = 1, kp = 1;
+  if (fast) {
+    const int sub = (entries + 31) / 32;
+    if (dim >= 256 && sub <= kMaxChunks && row_blocks * sub <= 1024) {
+      kp = 4, chunks = sub;
+    } else if (dim >= 128 && (sub + 1) / 2 <= kMaxChunks && row_blocks * ((sub + 1) / 2) <= 1024) {
+      kp = 2, chunks = (sub + 1) / 2;
+    } else {
+      int per = 128;
+      while ((entries + per - 1) / per > kMaxChunks || row_blocks * ((entries + per - 1) / per) > 1024) {
+        if (per >= entries) break;
+        per *= 2;
+      }
+      chunks = (entries + per - 1) / per;
+    }
+  } else {
+    while (chunks < 16 && row_blocks * chunks < 512 && entries / (chunks * 2) >= NT) chunks *= 2;
+  }
+  const int chunk_entries = fast ? (kp == 4 ? 32 : kp == 2 ? 64 : (entries + chunks - 1) / chunks)
+                                 : ((entries + chunks - 1) / chunks + NT - 1) / NT * NT;
+  const int ce = fast && kp == 1 ? (chunk_entries + 31) / 32 * 32 : chunk_entries;
 
   char* ws = static_cast<char*>(workspace);
   float* resid[2] = {reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws) + (size_t)rows * dim};
   ws += (size_t)2 * rows * dim * sizeof(float);
-  float* val[2] = {reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws) + (size_t)16 * rows};
-  ws += (size_t)2 * 16 * rows * sizeof(float);
-  int* idx[2] = {reinterpret_cast<int*>(ws), reinterpret_cast<int*>(ws) + (size_t)16 * rows};
+  float* val[2] = {reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws) + (size_t)kMaxChunks * rows};
+  ws += (size_t)2 * kMaxChunks * rows * sizeof(float);
+  int* idx[2] = {reinterpret_cast<int*>(ws), reinterpret_cast<int*>(ws) + (size_t)kMaxChunks * rows};
 
-  const size_t lds = step_lds_bytes(dim);
+  const size_t lds = fast ? ((size_t)RB * (dim + 4) + RB + 2 * 4 * RB + 3 * 32 * (RB + 1) + ce) * 4
+                          : step_lds_bytes(dim);
   if (lds > 64 * 1024) return FM_UNSUPPORTED;
   for (int j = 0; j < count; ++j) {
     StepArgs a{};
@@ -348,9 +554,19 @@ int fm_rvq_encode(const float* x, int ld_x, int rows, int rows_per_batch, int di
     a.norms = norms + (size_t)j * entries;
     a.val = val[cur];
     a.idx = idx[cur];
-    a.M = rows; a.dim = dim; a.entries = entries; a.chunk_entries = chunk_entries;
+    a.M = rows; a.dim = dim; a.entries = entries; a.chunk_entries = ce;
     a.chunks = chunks; a.rows_per_batch = rows_per_batch; a.batch_stride = batch_stride;
-    hipLaunchKernelGGL(rvq_step_kernel, dim3(row_blocks, chunks), dim3(256), lds, stream, a);
+    const float* embed = embeds + (size_t)j * entries * dim;
+    const dim3 grid(row_blocks, chunks);
+#define FM_RVQ(D, K) hipLaunchKernelGGL((rvq_step_mfma_kernel<D, K>), grid, dim3(256), lds, stream, a, embed)
+    if (!fast) hipLaunchKernelGGL(rvq_step_kernel, grid, dim3(256), lds, stream, a);
+    else if (dim == 256 && kp == 4) FM_RVQ(256, 4);
+    else if (dim == 256 && kp == 2) FM_RVQ(256, 2);
+    else if (dim == 256) FM_RVQ(256, 1);
+    else if (dim == 128 && kp == 2) FM_RVQ(128, 2);
+    else if (dim == 128) FM_RVQ(128, 1);
+    else FM_RVQ(64, 1);
+#undef FM_RVQ
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }

@@ -370,10 +370,18 @@ def rvq_encode_oracle(x, embeds, T):
     return codes.view(nq, M // T, T).transpose(0, 1)
 
 
-@pytest.mark.parametrize("B,T,nq", [(1, 125, 8), (4, 63, 7), (64, 125, 32), (1, 1, 3)])
-def test_rvq_encode_matches_reference_loop(B, T, nq):
-    g = torch.Generator().manual_seed(B * T + nq)
-    e, d = 2048, 256
+@pytest.mark.parametrize("B,T,nq,e,d", [
+    (1, 125, 8, 2048, 256),    # 32-entry chunks, 4 k-parts
+    (4, 63, 7, 2048, 256),
+    (8, 100, 4, 2048, 256),    # 64-entry chunks, 2 k-parts
+    (64, 125, 32, 2048, 256),  # 512-entry chunks, 1 k-part
+    (1, 1, 3, 2048, 256),
+    (3, 100, 3, 1000, 128),    # ragged last chunk
+    (2, 70, 3, 100, 64),
+    (2, 40, 3, 48, 8),         # general kernel (dim not in {64, 128, 256})
+])
+def test_rvq_encode_matches_reference_loop(B, T, nq, e, d):
+    g = torch.Generator().manual_seed(B * T + nq + e + d)
     embed_sum = torch.randn(nq, e, d, generator=g) / 16
     usage = torch.ones(nq, e)
     x = torch.randn(B * T, d, generator=g) * 0.3
