@@ -317,13 +317,13 @@ __global__ __launch_bounds__(NTHREADS) void gemm_fast_kernel(GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// Large-tile kernel: BM = 256 rows, BN in {64, 128}, BK = 32, 8 waves (two
-// per SIMD) of up to 64x64 outputs each.  A
-// k-tile carries far more MFMA work than the next tile's global-load latency,
-// so a single LDS stage refilled from a one-tile register prefetch keeps the
-// MFMA pipes busy; the second wave per SIMD overlaps one wave's load/store
-// code with the other's MFMAs.  Loads are branch-free (clamped address plus a
-// select) so the in-order instruction stream stays short.
+// Large-tile kernel: BM = 256 rows, BK = 32, 8 waves of (256/WM)x(BN/WN)
+// outputs (used as 256x64 with 64x32 per wave).  A k-tile carries far more
+// MFMA work than the next tile's global-load latency, so a single LDS stage
+// refilled from a one-tile register prefetch suffices; at ~100 VGPRs two
+// blocks share a CU, so one block's barrier/store phase overlaps the other's
+// MFMAs.  Loads are branch-free (clamped address plus a select) so the
+// in-order instruction stream stays short.
 template <int BN, int WM, int WN>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
   constexpr int NTH = 64 * WM * WN;
@@ -645,12 +645,15 @@ __global__ __launch_bounds__(256) void conv_cout1_kernel(const float* __restrict
 
 struct TileCfg {
   int BM, BN, WK, BK, id;
+  long fill;  // fewest tiles for which this candidate is taken
 };
-// Candidates, largest first: the first whose tile count covers the CUs wins.
-constexpr TileCfg kTiles[] = {{256, 128, 1, 32, 5}, {256, 64, 1, 32, 6},
-                              {128, 128, 1, 64, 0}, {128, 64, 1, 64, 1}, {128, 32, 1, 64, 2},
-                              {32, 64, 4, 32, 3}};
-constexpr long kFillBlocks = 224;  // ~0.9 blocks per CU
+// Candidates, largest first: the first whose tile count reaches its `fill`
+// wins.  The 256x64 tile (two 512-thread blocks per CU) measured faster than
+// every other shape down to ~190 tiles, so it is taken from half a tile per CU.
+constexpr TileCfg kTiles[] = {{256, 64, 1, 32, 6, 128},  {128, 128, 1, 64, 0, 224},
+                              {128, 64, 1, 64, 1, 224},  {128, 32, 1, 64, 2, 224},
+                              {32, 64, 4, 32, 3, 0}};
+constexpr TileCfg kSplitTile = kTiles[4];
 
 long tile_count(long M, int N, const TileCfg& t) {
   return ((M + t.BM - 1) / t.BM) * ((N + t.BN - 1) / t.BN);
@@ -668,10 +671,10 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
   if (p.L_in == 0 || M > INT_MAX / 2) return FM_BAD_ARGUMENT;
 
   const bool fast = (p.C_in % 4 == 0) && (p.K % 4 == 0);
-  TileCfg cfg = kTiles[3];
+  TileCfg cfg = kSplitTile;
   long tiles = 0;
   if (!fast) {
-    cfg = TileCfg{64, 64, 1, 16, -1};
+    cfg = TileCfg{64, 64, 1, 16, -1, 0};
     tiles = tile_count(M, p.N, cfg);
   } else {
     // Largest tile that still fills the GPU; tiles more than 2x wider than
@@ -680,7 +683,7 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
       if (t.WK == 1 && t.BN > 32 && t.BN / 2 >= p.N) continue;
       cfg = t;
       tiles = tile_count(M, p.N, t);
-      if (tiles >= kFillBlocks) break;
+      if (tiles >= t.fill) break;
     }
   }
   // Global K-split for long K when even the K-split tile leaves CUs idle.
@@ -705,7 +708,6 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     case 1: hipLaunchKernelGGL((gemm_fast_kernel<128, 64, 4, 1, 1, 64>), grid, dim3(NTHREADS), 0, s, p); break;
     case 2: hipLaunchKernelGGL((gemm_fast_kernel<128, 32, 4, 1, 1, 64>), grid, dim3(NTHREADS), 0, s, p); break;
     case 3: hipLaunchKernelGGL((gemm_fast_kernel<32, 64, 1, 1, 4, 32>), grid, dim3(NTHREADS), 0, s, p); break;
-    case 5: hipLaunchKernelGGL((gemm_big_kernel<128, 4, 2>), grid, dim3(512), 0, s, p); break;
     case 6: hipLaunchKernelGGL((gemm_big_kernel<64, 4, 2>), grid, dim3(512), 0, s, p); break;
     default: hipLaunchKernelGGL(gemm_generic_kernel, grid, dim3(256), 0, s, p); break;
   }
