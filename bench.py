@@ -12,7 +12,17 @@ over its mean launch time, timed with HIP events on the stream it runs on.
 ``cpu_baseline`` times the repository's CPU oracle (the reference's portable
 PyTorch path restated op for op) on the host cores, on the same 10 s input.
 
+``roofline.traffic`` is the dominant kernel's HBM bytes per launch as read by
+``rocprofv3 --pmc FETCH_SIZE`` and ``--pmc WRITE_SIZE`` on
+``bench.py --dominant-only`` (which also runs a plain device copy of known
+size to calibrate the counters); the figures live in
+``profiles/dec_up4_convt_c2_hbm_traffic.md`` and are read from there.
+
+The 100 s clip and the RVQ-heavy batch-64 / 32-codebook
+configuration are reported as extra sections.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+       python bench.py --dominant-only [--iters N]   (counter runs)
 """
 
 from __future__ import annotations
@@ -80,28 +90,82 @@ def dominant_kernel(model: MimiModel, name: str, batch: int, samples: int, nq: i
             "traffic": None}
 
 
+TRAFFIC_FILE = REPO / "profiles" / "dec_up4_convt_c2_hbm_traffic.md"
+COPY_BYTES = 256 << 20  # calibration copy: reads and writes this many bytes
+
+
+def recorded_traffic() -> dict | None:
+    """HBM bytes per launch of the dominant kernel from the committed counter summary.
+
+    The file holds ``key: value`` lines; ``traffic_bytes_per_launch`` is the
+    calibrated FETCH_SIZE + WRITE_SIZE per dispatch.
+    """
+    if not TRAFFIC_FILE.is_file():
+        return None
+    vals = {}
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if ":" in line and line.lstrip().startswith("- "):
+            k, v = line.lstrip()[2:].split(":", 1)
+            vals[k.strip().strip("`")] = v.strip().strip("`")
+    try:
+        return {"bytes": float(vals["traffic_bytes_per_launch"]),
+                "fetch": float(vals["fetch_bytes_per_launch"]),
+                "write": float(vals["write_bytes_per_launch"])}
+    except (KeyError, ValueError):
+        return None
+
+
+def dominant_only(iters: int) -> None:
+    """Launches of the dominant contraction plus a calibration copy (for --pmc runs)."""
+    dev = torch.device("cuda", 0)
+    model = MimiModel(MimiConfig(), device=dev, seed=0)
+    op = model.runtime().layer_op(DOMINANT, 1, 240_000)
+    src = torch.randn(COPY_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(iters):
+        op()
+    for _ in range(iters):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"dominant": DOMINANT, "iters": iters, "copy_bytes": COPY_BYTES}), flush=True)
+
+
 def cpu_baseline(audio: np.ndarray, mask: np.ndarray, nq: int, runs: int) -> dict:
     sys.path.insert(0, str(REPO))
     from oracle.mimi_oracle import MimiOracle
     from fast_mimi_amd.weights import seeded_state_dict
 
+    # The GPU box grants this job 16 host cores whatever os.cpu_count() reports.
     cores = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(cores)
     cfg = MimiConfig()
     oracle = MimiOracle(cfg, {k: torch.from_numpy(v) for k, v in seeded_state_dict(cfg, 0).items()})
     a, m = torch.from_numpy(audio), torch.from_numpy(mask)
-    oracle.forward(a, m, nq)  # warm-up
     times = []
-    for _ in range(runs):
-        t0 = time.perf_counter_ns()
-        oracle.forward(a, m, nq)
-        times.append((time.perf_counter_ns() - t0) / 1e6)
+    with torch.inference_mode():
+        for _ in range(2):  # warm-up
+            oracle.forward(a, m, nq)
+        for _ in range(runs):
+            t0 = time.perf_counter_ns()
+            oracle.forward(a, m, nq)
+            times.append((time.perf_counter_ns() - t0) / 1e6)
     med = statistics.median(times)
     seconds = audio.shape[0] * audio.shape[-1] / 24_000
     return {"value": round(seconds / (med / 1e3), 3), "unit": "audio-sec/sec", "cores": cores,
-            "kind": "port", "median_ms": round(med, 2),
-            "sample": f"B1 x 10 s, nq={nq}, CPU oracle (PyTorch eager, op order of model.py), "
-                      f"median of {runs} after 1 warm-up"}
+            "kind": "port", "median_ms": round(med, 2), "cpu": cpu_model(),
+            "sample": f"B1 x 10 s, nq={nq} (the bench workload itself), CPU oracle (PyTorch "
+                      f"eager restatement of the reference model.py path), median of {runs} "
+                      f"after 2 warm-ups, {cores} threads"}
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main() -> None:
@@ -109,7 +173,10 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cpu-runs", type=int, default=5)
+    ap.add_argument("--cpu-runs", type=int, default=10)
+    ap.add_argument("--no-extra", action="store_true", help="skip the 100 s and B64/nq32 sections")
+    ap.add_argument("--dominant-only", action="store_true")
+    ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batch16", action="store_true")
     args = ap.parse_args()
@@ -122,6 +189,9 @@ def main() -> None:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
     nat.library()
+    if args.dominant_only:
+        dominant_only(args.iters)
+        return
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     cfg = MimiConfig()
@@ -157,7 +227,24 @@ def main() -> None:
         result["batch16"] = {"audio_sec_per_sec": round(16 * 10 / (med16 / 1e3), 2),
                              "median_ms": round(med16, 3),
                              "pipeline_tflops": round(f16 / (med16 * 1e-3) / 1e12, 3)}
+    if not args.no_extra:
+        for key, cfg_name, steps in (("long100s", "c4", 10), ("rvq_b64_nq32", "c5", 5)):
+            ax, mx, nqx = synthetic.config_inputs(cfg_name)
+            axd, mxd = torch.from_numpy(ax).to(dev), torch.from_numpy(mx).to(dev)
+            tx = time_steps(lambda: model(axd, mxd, num_quantizers=nqx), steps, 2)
+            medx = statistics.median(tx)
+            fx = roundtrip_flops(cfg, ax.shape[0], ax.shape[-1], nqx)
+            result[key] = {"batch": int(ax.shape[0]), "samples": int(ax.shape[-1]),
+                           "num_quantizers": nqx, "median_ms": round(medx, 3),
+                           "audio_sec_per_sec": round(ax.shape[0] * ax.shape[-1] / 24_000 / (medx / 1e3), 2),
+                           "pipeline_tflops": round(fx / (medx * 1e-3) / 1e12, 3)}
+            del axd, mxd
+        model.release_graphs()
     result["roofline"] = dominant_kernel(model, DOMINANT, 1, audio.shape[-1], nq, 50)
+    tr = recorded_traffic()
+    if tr is not None:
+        result["roofline"]["traffic"] = tr["bytes"]
+        result["roofline"]["traffic_source"] = str(TRAFFIC_FILE.relative_to(REPO))
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(audio, mask, nq, args.cpu_runs)
         result["speedup_vs_cpu"] = round(result["value"] / result["cpu_baseline"]["value"], 2)

@@ -72,12 +72,15 @@ FM_DEVICE void store_out(float acc, long m, int n, const GemmArgs& p) {
   }
 }
 
-// Block -> tile, grouping a row band's tiles on one XCD.
+// Block -> tile.  Blocks are dispatched round-robin over the 8 XCDs (block b
+// to XCD b % 8), each with its own L2; XCD x is given one contiguous range of
+// tile indices (the first nb % 8 XCDs one tile more), so a row band's column
+// tiles, which re-read the same input rows, share an L2.
 FM_DEVICE int tile_index() {
   const int nb = gridDim.x;
   const int b = blockIdx.x;
-  if (nb % 8) return b;
-  return (b % 8) * (nb / 8) + b / 8;
+  const int x = b % 8, q = nb / 8, r = nb % 8;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + b / 8;
 }
 
 // ---------------------------------------------------------------------------

@@ -173,6 +173,12 @@ class MimiModel:
             if ".codebook." not in s.name:
                 yield self._state[s.name]
 
+    def release_graphs(self) -> None:
+        """Drop every captured hipGraph (and the device memory its pool holds)."""
+        self._graphs.clear()
+        if torch.cuda.is_available():
+            torch.cuda.empty_cache()
+
     def _invalidate(self) -> None:
         self._runtime = None
         self._graphs.clear()
