@@ -652,8 +652,9 @@ struct TileCfg {
 };
 // Candidates, largest first: the first whose tile count reaches its `fill`
 // wins.  The 256x64 tile (two 512-thread blocks per CU) measured faster than
-// every other shape down to ~190 tiles, so it is taken from half a tile per CU.
-constexpr TileCfg kTiles[] = {{256, 64, 1, 32, 6, 128},  {128, 128, 1, 64, 0, 224},
+// every other shape down to ~190 tiles (not at 128 with long K), so it is taken
+// from 160 tiles.
+constexpr TileCfg kTiles[] = {{256, 64, 1, 32, 6, 160},  {128, 128, 1, 64, 0, 224},
                               {128, 64, 1, 64, 1, 224},  {128, 32, 1, 64, 2, 224},
                               {32, 64, 4, 32, 3, 0}};
 constexpr TileCfg kSplitTile = kTiles[4];

@@ -284,6 +284,11 @@ __global__ __launch_bounds__(256) void window_attention_kernel(
 }
 
 
+// Grids of the row-block kernels put the column block in blockIdx.x: blocks
+// are dealt round-robin to the 8 XCDs, so each XCD's L2 holds a slice of the
+// weights (read once) plus the small activation block, instead of every XCD
+// streaming all of the weights.
+//
 // Row-block linear layer for the transformer projections (K = hidden = 512):
 //   y = epilogue( LN?(x) . W^T )
 // A block of NWV waves owns 32 rows x BN output columns.  Its 32 input rows
@@ -313,8 +318,8 @@ __global__ __launch_bounds__(64 * NWV) void row_linear_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, lcol = lane & 31;
-  const long m0 = (long)blockIdx.x * BM;
-  const int n0 = blockIdx.y * BN;
+  const long m0 = (long)blockIdx.y * BM;
+  const int n0 = blockIdx.x * BN;
   const int kw0 = wave * KW;
 
   // Weight fragments for this wave's k-slice.
@@ -432,6 +437,264 @@ __global__ __launch_bounds__(64 * NWV) void row_linear_kernel(
   for (int c = 0; c < OPT; c += 2) *reinterpret_cast<float2*>(dst + c) = float2{out[c], out[c + 1]};
 }
 
+
+// Row-block linear layer for long K (K a multiple of 8 * 64, no LayerNorm):
+// y = epilogue(x . W^T).  A block of 8 waves owns 32 rows x 32 columns; wave w
+// takes k-range [w*K/8, (w+1)*K/8) in 64-dim pieces whose A and B fragments
+// are loaded straight from global memory into registers one piece ahead of
+// their use (lane half h at step 4j+e carries dim 32h + 4j + e of the piece,
+// so every load is 16 bytes).  The 8 partial tiles are summed through LDS in
+// wave order; epilogue GELU or y = res + scale * acc.
+template <int K>
+__global__ __launch_bounds__(512) void row_stream_linear_kernel(
+    const float* __restrict__ x, int rows, const float* __restrict__ w, int N, int flags,
+    const float* res, const float* __restrict__ scale, float* y) {
+  constexpr int NWV = 8, KW = K / NWV, NP = KW / 64, PR = 33;
+  static_assert(KW % 64 == 0, "whole 64-dim pieces per wave");
+  __shared__ float red[NWV * 32 * PR];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, lcol = lane & 31;
+  const long m0 = (long)blockIdx.y * 32;
+  const int n0 = blockIdx.x * 32;
+  const float* xr = x + min(m0 + lcol, (long)rows - 1) * K + wave * KW + 32 * h;
+  const float* wr = w + (long)(n0 + lcol) * K + wave * KW + 32 * h;
+  floatx4 a[2][8], b[2][8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    a[0][j] = *reinterpret_cast<const floatx4*>(xr + 4 * j);
+    b[0][j] = *reinterpret_cast<const floatx4*>(wr + 4 * j);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  floatx16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int c = p & 1;
+    if (p + 1 < NP) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        a[c ^ 1][j] = *reinterpret_cast<const floatx4*>(xr + 64 * (p + 1) + 4 * j);
+        b[c ^ 1][j] = *reinterpret_cast<const floatx4*>(wr + 64 * (p + 1) + 4 * j);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the next piece's loads ahead of these MFMAs
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = fm_mfma32(a[c][j][e], b[c][j][e], acc);
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) red[(wave * 32 + fm_mfma32_row(r, lane)) * PR + lcol] = acc[r];
+  __syncthreads();
+  // 1024 outputs, 2 per thread (adjacent columns).
+  const int er = tid >> 4, ec = (tid & 15) * 2;
+  const long m = m0 + er;
+  if (m >= rows) return;
+  float out[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    float v = red[er * PR + ec + c];
+#pragma unroll
+    for (int g = 1; g < NWV; ++g) v = __fadd_rn(v, red[(g * 32 + er) * PR + ec + c]);
+    const int n = n0 + ec + c;
+    if (flags & FM_EPI_GELU) v = fm_gelu(v);
+    if (flags & FM_EPI_RES_SCALE) v = __fadd_rn(res[m * N + n], __fmul_rn(scale[n], v));
+    out[c] = v;
+  }
+  *reinterpret_cast<float2*>(y + m * N + n0 + ec) = float2{out[0], out[1]};
+}
+
+
+// ---------------------------------------------------------------------------
+// Packed row-block projections for few rows (the B x T <= ~512 transformer
+// and RVQ projections): 16 rows x BN columns per block on the 16x16x4 FP32
+// MFMA, 8 waves splitting K, so even 250 rows give hundreds of blocks.
+// Weights are pre-packed (fm_pack_row_weights) in fragment order: the float4
+// at index ((nt * (K/64) + kp) * 4 + t) * 64 + lane holds
+// W[16 nt + lane % 16][64 kp + 16 (lane / 16) + 4 t .. + 3], so each wave
+// load is 1 KB contiguous.  In a 64-dim piece the k-slot of lane group
+// g = lane / 16 at MFMA step 4t+e carries dim 16 g + 4 t + e, for A as for B.
+// K == 512: the 16 input rows are staged in LDS (and layer-normalised from
+// registers when gamma is given: 32 lanes per row, shuffle-reduced).
+// K == 2048: A fragments are streamed from global memory (no LayerNorm).
+// Both double-buffer the next 64-dim piece in registers.  The 8 partial tiles
+// are summed through LDS in wave order; epilogue as in row_linear_kernel.
+
+FM_DEVICE floatx4 fm_mfma16(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <int K, int BN>
+__global__ __launch_bounds__(512) void row16_linear_kernel(
+    const float* __restrict__ x, int rows, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float eps, const float* __restrict__ wp, int N, int flags,
+    const float* res, const float* __restrict__ scale, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, int rope_cols, int rows_per_seq, float* y) {
+  constexpr int NWV = 8, BM = 16, KW = K / NWV, NP = KW / 64, NT = BN / 16;
+  constexpr bool STAGE = (K == 512);
+  constexpr int PA = K + 4, PR = BN + 1, OPT = BM * BN / 512;
+  static_assert(KW % 64 == 0 && OPT >= 1, "tile shape");
+  constexpr int A_FLOATS = STAGE ? BM * PA : 0, R_FLOATS = NWV * BM * PR;
+  __shared__ __attribute__((aligned(16))) float sm[A_FLOATS > R_FLOATS ? A_FLOATS : R_FLOATS];
+  float* As = sm;
+  float* red = sm;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, li = lane & 15;
+  const long m0 = (long)blockIdx.y * BM;
+  const int n0 = blockIdx.x * BN;
+  const int kw0 = wave * KW;
+  const long tstride = (long)(K / 64) * 4 * 64 * 4;  // floats between 16-column tiles
+  const float* wb = wp + ((((long)(n0 / 16) * (K / 64) + kw0 / 64) * 4) * 64 + lane) * 4;
+  const float* xs = x + min(m0 + li, (long)rows - 1) * K + kw0 + 16 * g;
+
+  floatx4 a[2][4], b[2][NT][4];
+  auto load_b = [&](int buf, int piece) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        b[buf][j][t] = *reinterpret_cast<const floatx4*>(wb + j * tstride + piece * 1024 + t * 256);
+  };
+  auto load_a = [&](int buf, int piece) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      a[buf][t] = STAGE ? *reinterpret_cast<const floatx4*>(As + li * PA + kw0 + 64 * piece + 16 * g + 4 * t)
+                        : *reinterpret_cast<const floatx4*>(xs + 64 * piece + 4 * t);
+  };
+
+  load_b(0, 0);
+  if (STAGE) {
+    // 32 lanes per row, float4 chunks p, p + 32, ...
+    constexpr int TPR = 32, CH = K / 4 / TPR;
+    const int r = tid / TPR, p = tid % TPR;
+    const bool valid = m0 + r < rows;
+    const float* xr = x + min(m0 + r, (long)rows - 1) * K;
+    floatx4 v[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) v[u] = *reinterpret_cast<const floatx4*>(xr + 4 * (p + TPR * u));
+    if (gamma) {
+      floatx4 gv[CH], bv[CH];
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        gv[u] = *reinterpret_cast<const floatx4*>(gamma + 4 * (p + TPR * u));
+        bv[u] = *reinterpret_cast<const floatx4*>(beta + 4 * (p + TPR * u));
+      }
+      float s = 0.0f;
+#pragma unroll
+      for (int u = 0; u < CH; ++u) s += (v[u][0] + v[u][1]) + (v[u][2] + v[u][3]);
+#pragma unroll
+      for (int o = 1; o < TPR; o <<= 1) s += __shfl_xor(s, o, 64);
+      const float mean = s / (float)K;
+      float var = 0.0f;
+#pragma unroll
+      for (int u = 0; u < CH; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float d = v[u][e] - mean;
+          var = fmaf(d, d, var);
+        }
+#pragma unroll
+      for (int o = 1; o < TPR; o <<= 1) var += __shfl_xor(var, o, 64);
+      const float rstd = 1.0f / sqrtf(var / (float)K + eps);
+#pragma unroll
+      for (int u = 0; u < CH; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[u][e] = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(v[u][e], mean), rstd), gv[u][e]), bv[u][e]);
+    }
+#pragma unroll
+    for (int u = 0; u < CH; ++u)
+      *reinterpret_cast<floatx4*>(As + r * PA + 4 * (p + TPR * u)) =
+          valid ? v[u] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    __syncthreads();
+  }
+  load_a(0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  floatx4 acc[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) acc[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int pc = 0; pc < NP; ++pc) {
+    const int c = pc & 1;
+    if (pc + 1 < NP) {
+      load_b(c ^ 1, pc + 1);
+      load_a(c ^ 1, pc + 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[j] = fm_mfma16(a[c][t][e], b[c][j][t][e], acc[j]);
+  }
+  if (STAGE) __syncthreads();  // all waves are done with As before it becomes `red`
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[(wave * BM + 4 * g + r) * PR + 16 * j + li] = acc[j][r];
+  __syncthreads();
+  // OPT consecutive outputs per thread, BN / OPT threads per row.
+  const int er = tid / (BN / OPT), ec = (tid % (BN / OPT)) * OPT;
+  float out[OPT];
+#pragma unroll
+  for (int c = 0; c < OPT; ++c) {
+    float v = red[er * PR + ec + c];
+#pragma unroll
+    for (int q = 1; q < NWV; ++q) v = __fadd_rn(v, red[(q * BM + er) * PR + ec + c]);
+    out[c] = v;
+  }
+  const long m = m0 + er;
+  const bool rope = BN == 64 && cos_t && n0 < rope_cols;
+  if (rope) {
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < OPT; ++c) red[er * PR + ec + c] = out[c];
+    __syncthreads();
+  }
+  if (m >= rows) return;
+  const int tpos = (int)(m % rows_per_seq);
+#pragma unroll
+  for (int c = 0; c < OPT; ++c) {
+    const int n = n0 + ec + c;
+    float v = out[c];
+    if (rope) {
+      const int d = ec + c;
+      const float partner = red[er * PR + (d < 32 ? d + 32 : d - 32)];
+      const float rot = d < 32 ? -partner : partner;
+      v = __fadd_rn(__fmul_rn(v, cos_t[(long)tpos * 64 + d]), __fmul_rn(rot, sin_t[(long)tpos * 64 + d]));
+    }
+    if (flags & FM_EPI_GELU) v = fm_gelu(v);
+    if (flags & FM_EPI_RES_SCALE) v = __fadd_rn(res[m * N + n], __fmul_rn(scale[n], v));
+    out[c] = v;
+  }
+  float* dst = y + m * N + n0 + ec;
+  if constexpr (OPT == 2) {
+    *reinterpret_cast<float2*>(dst) = float2{out[0], out[1]};
+  } else {
+#pragma unroll
+    for (int c = 0; c < OPT; ++c) dst[c] = out[c];
+  }
+}
+
+// Packs W^T [N][K] (row-major) into the fragment order of row16_linear_kernel.
+__global__ __launch_bounds__(256) void pack_row_weights_kernel(const float* __restrict__ w, int N,
+                                                               int K, float* __restrict__ out) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;  // float4 index in the packed array
+  if (i >= (long)N * K / 4) return;
+  const int lane = (int)(i % 64);
+  const long q = i / 64;
+  const int t = (int)(q % 4);
+  const long q2 = q / 4;
+  const int kp = (int)(q2 % (K / 64));
+  const int nt = (int)(q2 / (K / 64));
+  const int n = 16 * nt + lane % 16, k = 64 * kp + 16 * (lane / 16) + 4 * t;
+  *reinterpret_cast<floatx4*>(out + 4 * i) = *reinterpret_cast<const floatx4*>(w + (long)n * K + k);
+}
+
 }  // namespace
 
 extern "C" {
@@ -441,7 +704,7 @@ extern "C" {
 // 64, tables [rows_per_seq][64]), GELU or LayerScale-residual epilogue.
 // in_features must be 512 (Mimi's hidden width); out_features a multiple of 64.
 int fm_row_linear_supported(int in_features, int out_features) {
-  return in_features == 512 && out_features % 64 == 0;
+  return (in_features == 512 || in_features == 2048) && out_features % 64 == 0;
 }
 
 int fm_row_linear(const float* x, int rows, int in_features, const float* ln_gamma,
@@ -455,6 +718,13 @@ int fm_row_linear(const float* x, int rows, int in_features, const float* ln_gam
   if ((flags & FM_EPI_RES_SCALE) && (!residual || !scale)) return FM_BAD_ARGUMENT;
   if (rope_cos && (!rope_sin || rope_cols % 64)) return FM_BAD_ARGUMENT;
   if (rows == 0) return FM_OK;
+  if ((rows + 31) / 32 > 65535) return FM_UNSUPPORTED;  // row blocks ride in grid y
+  if (in_features == 2048) {  // streamed A operand: no LayerNorm / RoPE on this path
+    if (ln_gamma || rope_cos) return FM_UNSUPPORTED;
+    hipLaunchKernelGGL(row_stream_linear_kernel<2048>, dim3(out_features / 32, (rows + 31) / 32),
+                       dim3(512), 0, stream, x, rows, weight, out_features, flags, residual, scale, y);
+    return (int)hipGetLastError();
+  }
   constexpr int K = 512;
   // 64-wide column tiles where RoPE needs whole heads, else 32-wide tiles (twice the blocks,
   // half the MFMA chain per wave); 8 waves split K.
@@ -462,7 +732,7 @@ int fm_row_linear(const float* x, int rows, int in_features, const float* ln_gam
 #define FM_ROWLIN(BN, NWV)                                                                       \
   {                                                                                              \
     const size_t lds = std::max<size_t>((size_t)32 * (K + 4), (size_t)NWV * 32 * (BN + 4)) * 4;  \
-    hipLaunchKernelGGL((row_linear_kernel<K, BN, NWV>), dim3((rows + 31) / 32, out_features / BN), \
+    hipLaunchKernelGGL((row_linear_kernel<K, BN, NWV>), dim3(out_features / BN, (rows + 31) / 32), \
                        dim3(64 * NWV), lds, stream, x, rows, ln_gamma, ln_beta, ln_eps, weight,   \
                        out_features, flags, residual, scale, rope_cos, rope_sin, rope_cols,      \
                        rows_per_seq, y);                                                         \
@@ -472,6 +742,47 @@ int fm_row_linear(const float* x, int rows, int in_features, const float* ln_gam
   else
     FM_ROWLIN(32, 8)
 #undef FM_ROWLIN
+  return (int)hipGetLastError();
+}
+
+// Few-row projections on fragment-packed weights (see row16_linear_kernel).
+// Same arguments and epilogues as fm_row_linear; weight_packed comes from
+// fm_pack_row_weights.  in_features 512 (LayerNorm / RoPE allowed) or 2048.
+int fm_row_linear_packed(const float* x, int rows, int in_features, const float* ln_gamma,
+                         const float* ln_beta, float ln_eps, const float* weight_packed,
+                         int out_features, int flags, const float* residual, const float* scale,
+                         const float* rope_cos, const float* rope_sin, int rope_cols,
+                         int rows_per_seq, float* y, hipStream_t stream) {
+  if (!x || !weight_packed || !y || rows < 0 || rows_per_seq <= 0 || (ln_gamma && !ln_beta))
+    return FM_BAD_ARGUMENT;
+  if (!fm_row_linear_supported(in_features, out_features)) return FM_UNSUPPORTED;
+  if ((flags & FM_EPI_RES_SCALE) && (!residual || !scale)) return FM_BAD_ARGUMENT;
+  if (rope_cos && (!rope_sin || rope_cols % 64)) return FM_BAD_ARGUMENT;
+  if (rows == 0) return FM_OK;
+  if ((rows + 15) / 16 > 65535) return FM_UNSUPPORTED;  // row blocks ride in grid y
+  if (in_features == 2048 && (ln_gamma || rope_cos)) return FM_UNSUPPORTED;
+  const dim3 g64(out_features / 64, (rows + 15) / 16), g32(out_features / 32, (rows + 15) / 16);
+#define FM_R16(KK, BN, G)                                                                       \
+  hipLaunchKernelGGL((row16_linear_kernel<KK, BN>), G, dim3(512), 0, stream, x, rows, ln_gamma, \
+                     ln_beta, ln_eps, weight_packed, out_features, flags, residual, scale,     \
+                     rope_cos, rope_sin, rope_cols, rows_per_seq, y)
+  if (in_features == 2048) FM_R16(2048, 32, g32);
+  else if (rope_cos) FM_R16(512, 64, g64);
+  else FM_R16(512, 32, g32);
+#undef FM_R16
+  return (int)hipGetLastError();
+}
+
+// Packs a [out_features][in_features] weight for fm_row_linear_packed
+// (out_features % 16 == 0, in_features % 64 == 0).  out must not alias weight.
+int fm_pack_row_weights(const float* weight, int out_features, int in_features, float* out,
+                        hipStream_t stream) {
+  if (!weight || !out || out_features <= 0 || in_features <= 0 || out_features % 16 ||
+      in_features % 64 || weight == out)
+    return FM_BAD_ARGUMENT;
+  const long n4 = (long)out_features * in_features / 4;
+  hipLaunchKernelGGL(pack_row_weights_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
+                     stream, weight, out_features, in_features, out);
   return (int)hipGetLastError();
 }
 

@@ -50,6 +50,8 @@ _SIGNATURES = {
     "fm_linear": ([_P, _I, _I, _P, _I, _I, _P, _P, _P, _P, _S, _P], _I),
     "fm_row_linear_supported": ([_I, _I], _I),
     "fm_row_linear": ([_P, _I, _I, _P, _P, _F, _P, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P], _I),
+    "fm_row_linear_packed": ([_P, _I, _I, _P, _P, _F, _P, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P], _I),
+    "fm_pack_row_weights": ([_P, _I, _I, _P, _P], _I),
     "fm_layer_norm": ([_P, _P, _P, _L, _I, _F, _P, _P], _I),
     "fm_window_attention": ([_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _I, _P], _I),
     "fm_rvq_prepare_codebook": ([_P, _P, _I, _I, _F, _P, _P, _P, _P], _I),

@@ -38,6 +38,8 @@ _WORKSPACE_BYTES = 64 << 20
 # Up to this many rows the transformer projections run as row-block kernels with
 # LayerNorm / RoPE fused; above it, tiled GEMMs amortise the weight reads better.
 _ROW_LINEAR_MAX_ROWS = 1024
+# Up to this many rows the 16-row kernels on fragment-packed weights are used.
+_ROW16_MAX_ROWS = 512
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -169,6 +171,17 @@ class MimiRuntime:
                      st[f"{p}.cluster_usage"].contiguous().data_ptr(), e, d, 1e-5,
                      self.embeds[j].data_ptr(), self.embeds_t[j].data_ptr(),
                      self.norms[j].data_ptr(), stream)
+        # Fragment-packed copies of the projection weights for the few-row kernels,
+        # keyed by the row-major weight's device address.
+        self._packed: dict[int, torch.Tensor] = {}
+        lib = nat.library()
+        for w in [m for lay in self.enc_tf + self.dec_tf for m in (lay.wqkv, lay.wo, lay.w1, lay.w2)] + \
+                [self.w_in, self.w_out]:
+            n, k = w.shape
+            if lib.fm_row_linear_supported(k, n):
+                pw = torch.empty_like(w)
+                nat.call("fm_pack_row_weights", w.data_ptr(), n, k, pw.data_ptr(), stream)
+                self._packed[w.data_ptr()] = pw
         self.workspace = torch.empty(_WORKSPACE_BYTES // 4, device=device)
         self._rope: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
         # Optional per-op timing: a list of (tag, start_event, end_event).
@@ -222,6 +235,13 @@ class MimiRuntime:
                  self._stream())
         return y
 
+    def _proj(self, x, rows, w, flags=0, residual=None, scale=None, out=None):
+        """Plain projection: row-block kernel for few rows, tiled GEMM otherwise."""
+        n, k = w.shape
+        if rows <= _ROW_LINEAR_MAX_ROWS and nat.library().fm_row_linear_supported(k, n):
+            return self._row_linear(x, rows, w, flags, residual, scale, out)
+        return self._linear(x, rows, w, flags, residual, scale, out)
+
     def _row_linear(self, x, rows, w, flags=0, residual=None, scale=None, out=None, ln=None,
                     rope=None):
         """Transformer projection with LayerNorm prologue / RoPE epilogue fused."""
@@ -229,8 +249,10 @@ class MimiRuntime:
         y = torch.empty((rows, n), device=self.device) if out is None else out
         g, b = (ln[0].data_ptr(), ln[1].data_ptr()) if ln is not None else (None, None)
         cos, sin, rope_cols, per_seq = rope if rope is not None else (None, None, 0, 1)
-        self._call("fm_row_linear", x.data_ptr(), rows, k, g, b, self.config.norm_eps,
-                   w.data_ptr(), n, flags, _ptr(residual), _ptr(scale), _ptr(cos), _ptr(sin),
+        packed = self._packed.get(w.data_ptr()) if rows <= _ROW16_MAX_ROWS else None
+        name, wp = ("fm_row_linear_packed", packed) if packed is not None else ("fm_row_linear", w)
+        self._call(name, x.data_ptr(), rows, k, g, b, self.config.norm_eps,
+                   wp.data_ptr(), n, flags, _ptr(residual), _ptr(scale), _ptr(cos), _ptr(sin),
                    rope_cols, per_seq, y.data_ptr(), self._stream())
         return y
 
@@ -308,7 +330,7 @@ class MimiRuntime:
                 self._tag = f"{tag}{li}.fc1"
                 ff = self._linear(xln, M, lay.w1, nat.EPI_GELU)
             self._tag = f"{tag}{li}.fc2"
-            self._linear(ff, M, lay.w2, nat.EPI_RES_SCALE, residual=h, scale=lay.ls2, out=h)
+            self._proj(ff, M, lay.w2, nat.EPI_RES_SCALE, residual=h, scale=lay.ls2, out=h)
         return h.reshape(B, T, C)
 
     # ------------------------------------------------------------- stages
@@ -337,7 +359,7 @@ class MimiRuntime:
         M = B * T
         vq = self.vq
         self._tag = "rvq.in"
-        proj = self._linear(h.reshape(M, cfg.hidden_size), M, self.w_in)
+        proj = self._proj(h.reshape(M, cfg.hidden_size), M, self.w_in)
         self._tag = "rvq.encode"
         codes = torch.empty((B, nq, T), dtype=torch.int64, device=self.device)
         ws_bytes = nat.library().fm_rvq_workspace_bytes(M, vq, cfg.codebook_size)
@@ -365,7 +387,7 @@ class MimiRuntime:
         self._call("fm_rvq_decode", codes.data_ptr(), B, nq, T, cfg.num_semantic_quantizers,
                  self.embeds.data_ptr(), cfg.codebook_size, vq, q.data_ptr(), self._stream())
         self._tag = "rvq.out"
-        h = self._linear(q, M, self.w_out).reshape(B, T, cfg.hidden_size)
+        h = self._proj(q, M, self.w_out).reshape(B, T, cfg.hidden_size)
         self._tag = "up"
         L = T
         if self.bottleneck:

@@ -108,11 +108,13 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
  *     row % rows_per_seq;
  *   - flags: FM_EPI_GELU, or FM_EPI_RES_SCALE (y = residual + scale[n] * acc,
  *     y may alias residual).
- * Supported shapes: fm_row_linear_supported(in, out) != 0 (in == 512, out a
- * multiple of 64).  Replaces the LayerNorm + q/k/v projection + _apply_rope
+ * Supported shapes: fm_row_linear_supported(in, out) != 0 (in 512 or 2048,
+ * out a multiple of 64; LayerNorm and RoPE only with in == 512).  Replaces the LayerNorm + q/k/v projection + _apply_rope
  * and LayerNorm + fc1 + GELU sequences of MimiTransformerLayer
  * (model.py:2028-2061, :1870-1961, :1551-1569, :1990-1999) and the Triton
- * _packed_qkv_rope_kernel (_packed_qkv.py:14-131).
+ * _packed_qkv_rope_kernel (_packed_qkv.py:14-131); with in == 2048 the fc2
+ * projection of MimiMLP (model.py:1990-1999); also fits the RVQ 1x1
+ * projections (model.py:2408-2444).
  */
 int fm_row_linear_supported(int in_features, int out_features);
 int fm_row_linear(const float* x, int rows, int in_features, const float* ln_gamma,
@@ -120,6 +122,26 @@ int fm_row_linear(const float* x, int rows, int in_features, const float* ln_gam
                   int flags, const float* residual, const float* scale, const float* rope_cos,
                   const float* rope_sin, int rope_cols, int rows_per_seq, float* y,
                   hipStream_t stream);
+
+/*
+ * fm_row_linear on fragment-packed weights, for few rows (16-row blocks on
+ * the 16x16x4 FP32 MFMA; the choice for rows <= ~512).  Same arguments,
+ * shapes and epilogues as fm_row_linear; weight_packed is produced by
+ * fm_pack_row_weights.  Packed layout: the float4 at index
+ * ((nt * (in/64) + kp) * 4 + t) * 64 + lane holds
+ * W[16 nt + lane % 16][64 kp + 16 (lane / 16) + 4 t .. 4 t + 3].
+ * Replaces the same reference computations as fm_row_linear.
+ */
+int fm_row_linear_packed(const float* x, int rows, int in_features, const float* ln_gamma,
+                         const float* ln_beta, float ln_eps, const float* weight_packed,
+                         int out_features, int flags, const float* residual, const float* scale,
+                         const float* rope_cos, const float* rope_sin, int rope_cols,
+                         int rows_per_seq, float* y, hipStream_t stream);
+/* Packs a [out_features][in_features] weight (out % 16 == 0, in % 64 == 0);
+ * out must not alias weight.  One-time preparation, like the reference's
+ * weight packing in _optimized_runtime.py / _packed_qkv.py. */
+int fm_pack_row_weights(const float* weight, int out_features, int in_features, float* out,
+                        hipStream_t stream);
 
 /*
  * LayerNorm over the last dimension (biased variance).

@@ -2,7 +2,7 @@
 
 This module is the checker, never the product: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
-import it.  The shipped path (``fast_mimi``) runs on the HIP library and fails
+import it.  The shipped path (``fast_mimi_amd``) runs on the HIP library and fails
 loudly without it.
 
 It restates, in PyTorch eager on the CPU and for any batch size, the portable

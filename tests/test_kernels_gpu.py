@@ -271,6 +271,9 @@ def test_window_attention_prerotated():
     close(out.cpu(), attention_reference(qkv, B, T, H, D, window, cos, sin), rel=5e-5)
 
 
+PACKED = {"packed": True}
+
+
 def run_row_linear(x, w, flags=0, ln=None, rope=None, res=None, scale=None, out=None):
     rows, k = x.shape
     n = w.shape[0]
@@ -278,14 +281,42 @@ def run_row_linear(x, w, flags=0, ln=None, rope=None, res=None, scale=None, out=
     g, b = ln if ln is not None else (None, None)
     cos, sin, rope_cols, per_seq = rope if rope is not None else (None, None, 0, 1)
     p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
-    nat.call("fm_row_linear", x.data_ptr(), rows, k, p(g), p(b), 1e-5, w.data_ptr(), n, flags,
+    name, wp = "fm_row_linear", w
+    if PACKED["packed"]:
+        wp = torch.empty_like(w)
+        nat.call("fm_pack_row_weights", w.data_ptr(), n, k, wp.data_ptr(), stream())
+        name = "fm_row_linear_packed"
+    nat.call(name, x.data_ptr(), rows, k, p(g), p(b), 1e-5, wp.data_ptr(), n, flags,
              p(res), p(scale), p(cos), p(sin), rope_cols, per_seq, y.data_ptr(), stream())
     torch.cuda.synchronize()
     return y
 
 
+@pytest.fixture(params=["rowmajor", "packed"])
+def weight_layout(request):
+    PACKED["packed"] = request.param == "packed"
+    yield request.param
+    PACKED["packed"] = False
+
+
+def test_pack_row_weights_layout():
+    n, k = 48, 128
+    w = torch.arange(n * k, dtype=torch.float32).view(n, k)
+    wd = w.to(DEV)
+    out = torch.empty_like(wd)
+    nat.call("fm_pack_row_weights", wd.data_ptr(), n, k, out.data_ptr(), stream())
+    torch.cuda.synchronize()
+    got = out.cpu().view(-1, 4)
+    for i in (0, 1, 63, 64, 255, 256, 777, got.shape[0] - 1):
+        lane, q = i % 64, i // 64
+        t, q2 = q % 4, q // 4
+        kp, nt = q2 % (k // 64), q2 // (k // 64)
+        row, col = 16 * nt + lane % 16, 64 * kp + 16 * (lane // 16) + 4 * t
+        assert torch.equal(got[i], w[row, col:col + 4]), i
+
+
 @pytest.mark.parametrize("rows", [250, 1, 33, 500, 4000])
-def test_row_linear(rows):
+def test_row_linear(rows, weight_layout):
     """LayerNorm prologue + RoPE / GELU / LayerScale-residual epilogues vs float64."""
     g = torch.Generator().manual_seed(rows)
     k, H, D = 512, 8, 64
@@ -321,13 +352,34 @@ def test_row_linear(rows):
     close(h.cpu(), res.double() + scale.double() * (x.double() @ wo.double().t()))
 
 
+@pytest.mark.parametrize("rows", [250, 1, 17, 1000])
+def test_row_linear_long_k(rows, weight_layout):
+    """K = 2048 streamed path (fc2): plain, GELU and in-place LayerScale residual."""
+    g = torch.Generator().manual_seed(rows + 7)
+    x = torch.randn(rows, 2048, generator=g)
+    w = torch.randn(512, 2048, generator=g) * 0.02
+    xd, wd = x.to(DEV), w.to(DEV)
+    want = x.double() @ w.double().t()
+    close(run_row_linear(xd, wd).cpu(), want)
+    close(run_row_linear(xd, wd, nat.EPI_GELU).cpu(), F.gelu(want))
+    res = torch.randn(rows, 512, generator=g)
+    scale = torch.rand(512, generator=g) * 0.1
+    h = res.to(DEV)
+    run_row_linear(xd, wd, nat.EPI_RES_SCALE, res=h, scale=scale.to(DEV), out=h)
+    close(h.cpu(), res.double() + scale.double() * want)
+
+
 def test_row_linear_rejects():
     lib = nat.library()
-    assert lib.fm_row_linear_supported(512, 1536) and not lib.fm_row_linear_supported(2048, 512)
-    x = torch.zeros(4, 2048, device=DEV)
-    w = torch.zeros(512, 2048, device=DEV)
+    assert lib.fm_row_linear_supported(512, 1536) and lib.fm_row_linear_supported(2048, 512)
+    assert not lib.fm_row_linear_supported(1024, 512) and not lib.fm_row_linear_supported(512, 100)
+    x = torch.zeros(4, 1024, device=DEV)
+    w = torch.zeros(512, 1024, device=DEV)
     with pytest.raises(nat.NativeError, match="unsupported"):
         run_row_linear(x, w)
+    x2, w2, gb = torch.zeros(4, 2048, device=DEV), torch.zeros(512, 2048, device=DEV), torch.ones(2048, device=DEV)
+    with pytest.raises(nat.NativeError, match="unsupported"):
+        run_row_linear(x2, w2, ln=(gb, gb))
 
 
 def prepare_codebooks(embed_sum, usage):
