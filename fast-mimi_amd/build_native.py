@@ -24,6 +24,9 @@ FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     # Packed FP32 ops are off: hipcc must not emit v_pk_{add,mul,fma}_f32.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # No implicit a*b+c -> fma contraction: the reference rounds each product
+    # and sum of its elementwise math separately (explicit fmaf stays fused).
+    "-ffp-contract=off",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
 ]
 

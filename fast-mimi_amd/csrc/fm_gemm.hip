@@ -764,6 +764,25 @@ int fm_conv1d(const float* x, int batch, int length, int in_channels, const floa
   return run_gemm(p, workspace, workspace_bytes, stream);
 }
 
+// Conv1d over exactly the given rows (no implicit padding): output row t
+// reads input rows t*stride .. t*stride + kernel - 1; output length
+// (length - kernel) / stride + 1 per batch item.  Streaming convolution,
+// where the caller prepends the layer's cached left context.
+int fm_conv1d_valid(const float* x, int batch, int length, int in_channels,
+                    const float* weight_packed, const float* bias, int out_channels, int kernel,
+                    int stride, int flags, const float* residual, float* y, float* workspace,
+                    size_t workspace_bytes, hipStream_t stream) {
+  if (kernel <= 0 || stride <= 0 || length < kernel || (flags & (FM_REPLICATE | FM_EPI_RES_SCALE)))
+    return FM_BAD_ARGUMENT;
+  GemmArgs p{};
+  p.x = x; p.w = weight_packed; p.bias = bias; p.res = residual; p.scale = nullptr; p.y = y;
+  p.batch = batch; p.L_in = length; p.C_in = in_channels;
+  p.rows = (length - kernel) / stride + 1;
+  p.rs = stride; p.padL = 0; p.K = kernel * in_channels; p.N = out_channels;
+  p.y_rows = p.rows; p.bias_len = out_channels; p.flags = flags;
+  return run_gemm(p, workspace, workspace_bytes, stream);
+}
+
 int fm_conv_transpose1d(const float* x, int batch, int length, int in_channels,
                         const float* weight_packed, const float* bias, int out_channels, int kernel,
                         int stride, int flags, const float* residual, float* y, float* workspace,

@@ -130,7 +130,9 @@ FM_DEVICE void wave_lds_fence() {
 }
 
 // Sliding-window causal attention on FP32 MFMA.
-// Grid: (ceil(T / QB), heads, batch), 256 threads.  Block = 32 queries of one
+// Grid: (ceil((T - q_start) / QB), heads, batch), 256 threads.  Queries are
+// rows q_start .. T-1 (earlier rows are cached keys/values only); query q
+// writes output row q - q_start.  Block = 32 queries of one
 // head; its key range [q0 - window + 1, q0 + 31] is cut into 32-key tiles that
 // the 4 waves take round-robin.  Waves run independently after the shared Q
 // stage: each keeps its next K/V tile in flight in registers while it
@@ -146,8 +148,8 @@ FM_DEVICE void wave_lds_fence() {
 template <int D, bool ROPE>
 __global__ __launch_bounds__(256) void window_attention_kernel(
     const float* __restrict__ qkv, int ld, int q_off, int k_off, int v_off,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int T, int heads,
-    int kv_heads, int window, float scale, float* __restrict__ out, int ld_out) {
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int T, int q_start,
+    int heads, int kv_heads, int window, float scale, float* __restrict__ out, int ld_out) {
   constexpr int DT = (D + 31) / 32;  // 32-row tiles of O^T
   constexpr int DP = DT * 32;        // padded head dim of V / O
   constexpr int PK = D + 4, PV = DP + 8, P = QB + 1;
@@ -163,7 +165,7 @@ __global__ __launch_bounds__(256) void window_attention_kernel(
   const int head = blockIdx.y;
   const int hk = head / (heads / kv_heads);
   const long b = blockIdx.z;
-  const int q0 = blockIdx.x * QB;
+  const int q0 = q_start + blockIdx.x * QB;
   const int q = q0 + col;
   const int k_lo = max(0, q0 - window + 1);
   const int k_hi = min(T, q0 + QB) - 1;
@@ -279,7 +281,7 @@ __global__ __launch_bounds__(256) void window_attention_kernel(
       num += stage[w][d * P + qi] * f;
       den += Lm[w][qi] * f;
     }
-    out[(b * (long)T + qg) * ld_out + head * D + d] = num / den;
+    out[(b * (long)(T - q_start) + qg - q_start) * ld_out + head * D + d] = num / den;
   }
 }
 
@@ -695,6 +697,29 @@ __global__ __launch_bounds__(256) void pack_row_weights_kernel(const float* __re
   *reinterpret_cast<floatx4*>(out + 4 * i) = *reinterpret_cast<const floatx4*>(w + (long)n * K + k);
 }
 
+
+// In-place RoPE on the first rope_cols columns of each row (heads of
+// head_dim, position = row % rows_per_seq into [*, head_dim] tables):
+// x_d' = x_d*cos_d + rotate_half(x)_d*sin_d, products and sum rounded
+// separately.  One thread per (row, head, d < head_dim / 2) pair.
+__global__ __launch_bounds__(256) void apply_rope_kernel(float* x, long rows, int ld, int rope_cols,
+                                                         int D, const float* __restrict__ cos_t,
+                                                         const float* __restrict__ sin_t,
+                                                         int rows_per_seq) {
+  const int half = D / 2;
+  const int pairs = rope_cols / 2;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * pairs) return;
+  const long m = i / pairs;
+  const int p = (int)(i % pairs);
+  const int head = p / half, d = p % half;
+  const long t = m % rows_per_seq;
+  float* row = x + m * ld + head * D;
+  const float lo = row[d], hi = row[d + half];
+  row[d] = __fadd_rn(__fmul_rn(lo, cos_t[t * D + d]), __fmul_rn(-hi, sin_t[t * D + d]));
+  row[d + half] = __fadd_rn(__fmul_rn(hi, cos_t[t * D + d + half]), __fmul_rn(lo, sin_t[t * D + d + half]));
+}
+
 }  // namespace
 
 extern "C" {
@@ -786,6 +811,19 @@ int fm_pack_row_weights(const float* weight, int out_features, int in_features, 
   return (int)hipGetLastError();
 }
 
+// In-place RoPE for projections made without the fused epilogue.
+int fm_apply_rope(float* x, long rows, int ld, int rope_cols, int head_dim, const float* cos_table,
+                  const float* sin_table, int rows_per_seq, hipStream_t stream) {
+  if (!x || !cos_table || !sin_table || rows < 0 || head_dim <= 0 || head_dim % 2 ||
+      rope_cols % head_dim || rope_cols > ld || rows_per_seq <= 0)
+    return FM_BAD_ARGUMENT;
+  const long total = rows * (rope_cols / 2);
+  if (total == 0) return FM_OK;
+  hipLaunchKernelGGL(apply_rope_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                     x, rows, ld, rope_cols, head_dim, cos_table, sin_table, rows_per_seq);
+  return (int)hipGetLastError();
+}
+
 int fm_layer_norm(const float* x, const float* gamma, const float* beta, long rows, int channels,
                   float eps, float* y, hipStream_t stream) {
   if (!x || !gamma || !beta || !y || rows < 0 || channels <= 0) return FM_BAD_ARGUMENT;
@@ -796,26 +834,46 @@ int fm_layer_norm(const float* x, const float* gamma, const float* beta, long ro
   return (int)hipGetLastError();
 }
 
+int fm_window_attention_rows(const float* qkv, int ld_qkv, int q_offset, int k_offset,
+                             int v_offset, const float* cos_table, const float* sin_table,
+                             int batch, int length, int query_start, int heads, int kv_heads,
+                             int head_dim, int window, float scale, float* out, int ld_out,
+                             hipStream_t stream);
+
 int fm_window_attention(const float* qkv, int ld_qkv, int q_offset, int k_offset, int v_offset,
                         const float* cos_table, const float* sin_table, int batch, int length,
                         int heads, int kv_heads, int head_dim, int window, float scale, float* out,
                         int ld_out, hipStream_t stream) {
+  return fm_window_attention_rows(qkv, ld_qkv, q_offset, k_offset, v_offset, cos_table, sin_table,
+                                  batch, length, 0, heads, kv_heads, head_dim, window, scale, out,
+                                  ld_out, stream);
+}
+
+// Attention for the queries at rows query_start .. length-1 of each sequence;
+// every row 0 .. length-1 is a key/value (rows before query_start hold a KV
+// cache).  out has length - query_start rows per sequence.
+int fm_window_attention_rows(const float* qkv, int ld_qkv, int q_offset, int k_offset,
+                             int v_offset, const float* cos_table, const float* sin_table,
+                             int batch, int length, int query_start, int heads, int kv_heads,
+                             int head_dim, int window, float scale, float* out, int ld_out,
+                             hipStream_t stream) {
   if (!qkv || !cos_table != !sin_table || !out || batch < 0 || length < 0 || heads <= 0 ||
       kv_heads <= 0 || heads % kv_heads || window <= 0)
     return FM_BAD_ARGUMENT;
   // Q/K/V rows are read as float4s.
   if ((ld_qkv | q_offset | k_offset | v_offset) % 4) return FM_BAD_ARGUMENT;
-  if (batch == 0 || length == 0) return FM_OK;
-  dim3 grid((length + QB - 1) / QB, heads, batch);
+  if (query_start < 0 || query_start > length) return FM_BAD_ARGUMENT;
+  if (batch == 0 || length == query_start) return FM_OK;
+  dim3 grid((length - query_start + QB - 1) / QB, heads, batch);
 #define FM_ATT(DV)                                                                         \
   if (cos_table)                                                                           \
     hipLaunchKernelGGL((window_attention_kernel<DV, true>), grid, dim3(256), 0, stream, qkv, \
                        ld_qkv, q_offset, k_offset, v_offset, cos_table, sin_table, length,  \
-                       heads, kv_heads, window, scale, out, ld_out);                        \
+                       query_start, heads, kv_heads, window, scale, out, ld_out);           \
   else                                                                                     \
     hipLaunchKernelGGL((window_attention_kernel<DV, false>), grid, dim3(256), 0, stream,   \
                        qkv, ld_qkv, q_offset, k_offset, v_offset, cos_table, sin_table,     \
-                       length, heads, kv_heads, window, scale, out, ld_out)
+                       length, query_start, heads, kv_heads, window, scale, out, ld_out)
   switch (head_dim) {
     case 8: FM_ATT(8); break;
     case 16: FM_ATT(16); break;

@@ -46,14 +46,17 @@ _S = ctypes.c_size_t
 _SIGNATURES = {
     "fm_abi_version": ([], _I),
     "fm_conv1d": ([_P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _S, _P], _I),
+    "fm_conv1d_valid": ([_P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _S, _P], _I),
     "fm_conv_transpose1d": ([_P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _S, _P], _I),
     "fm_linear": ([_P, _I, _I, _P, _I, _I, _P, _P, _P, _P, _S, _P], _I),
     "fm_row_linear_supported": ([_I, _I], _I),
     "fm_row_linear": ([_P, _I, _I, _P, _P, _F, _P, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P], _I),
     "fm_row_linear_packed": ([_P, _I, _I, _P, _P, _F, _P, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P], _I),
     "fm_pack_row_weights": ([_P, _I, _I, _P, _P], _I),
+    "fm_apply_rope": ([_P, _L, _I, _I, _I, _P, _P, _I, _P], _I),
     "fm_layer_norm": ([_P, _P, _P, _L, _I, _F, _P, _P], _I),
     "fm_window_attention": ([_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _I, _P], _I),
+    "fm_window_attention_rows": ([_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P, _I, _P], _I),
     "fm_rvq_prepare_codebook": ([_P, _P, _I, _I, _F, _P, _P, _P, _P], _I),
     "fm_rvq_workspace_bytes": ([_I, _I, _I], _S),
     "fm_rvq_encode": ([_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _S, _P], _I),

@@ -39,6 +39,7 @@ from .config import (
     KYUTAI_MIMI_WEIGHTS_SHA256,
     MimiConfig,
 )
+from .streaming import MimiConv1dPaddingCache, MimiKVCache
 from .weights import encoder_layer_indices, seeded_state_dict, state_dict_spec
 
 
@@ -91,12 +92,6 @@ def _file_sha256(path: Path) -> str:
         for block in iter(lambda: handle.read(1 << 20), b""):
             digest.update(block)
     return digest.hexdigest()
-
-
-def _no_streaming(**kwargs) -> None:
-    for name, value in kwargs.items():
-        if value not in (None, False):
-            raise NotImplementedError(f"{name}: streaming caches are not implemented by fast_mimi_amd")
 
 
 class _GraphRunner:
@@ -306,13 +301,23 @@ class MimiModel:
                return_dict: bool | None = None):
         """Encode ``[B, C, S]`` audio to int64 codes ``[B, nq, T]``.  The padding
         mask does not change encoding (``model.py:3123-3134``)."""
-        _no_streaming(encoder_past_key_values=encoder_past_key_values,
-                      padding_cache=padding_cache, use_streaming=use_streaming)
         return_dict = self.config.return_dict if return_dict is None else return_dict
+        use_streaming = self.config.use_streaming if use_streaming is None else use_streaming
         count = self._resolve_count(num_quantizers)
         self._check_audio(input_values)
         rt = self.runtime()
         audio = self._on_device(input_values, torch.float32)
+        if use_streaming and padding_cache is None:
+            padding_cache = self._new_padding_cache()
+        if use_streaming and encoder_past_key_values is None:
+            encoder_past_key_values = MimiKVCache(self.config.num_hidden_layers, self.config.sliding_window)
+        if padding_cache is not None or encoder_past_key_values is not None:
+            # Stateful calls run eagerly: cache lengths change from call to call.
+            with torch.cuda.device(self.device), torch.inference_mode():
+                codes = rt.encode(audio, count, padding_cache, encoder_past_key_values)
+            if not return_dict:
+                return codes, encoder_past_key_values, padding_cache
+            return MimiEncoderOutput(codes, encoder_past_key_values, padding_cache)
         self._prepare_lengths(audio.shape[-1])
         with torch.cuda.device(self.device), torch.inference_mode():
             if self.use_graphs:
@@ -328,7 +333,6 @@ class MimiModel:
                decoder_past_key_values=None, return_dict: bool | None = None):
         """Decode int64 codes ``[B, nq, T]`` to audio ``[B, C, T * frame_size]``,
         cropped to ``padding_mask.shape[-1]`` when that is shorter."""
-        _no_streaming(decoder_past_key_values=decoder_past_key_values)
         return_dict = self.config.return_dict if return_dict is None else return_dict
         if audio_codes.ndim != 3:
             raise ValueError("audio_codes must have shape [batch, codebooks, frames]")
@@ -340,16 +344,20 @@ class MimiModel:
             raise IndexError("audio code out of range of the codebook")
         out_len = None if padding_mask is None else padding_mask.shape[-1]
         frames = codes.shape[-1]
-        rt.prepare(frames * (2 if rt.bottleneck else 1))
+        kv = decoder_past_key_values
         with torch.cuda.device(self.device), torch.inference_mode():
-            if self.use_graphs:
+            if kv is not None:
+                audio = rt.decode(codes, out_len, kv)
+            elif self.use_graphs:
+                rt.prepare(frames * (2 if rt.bottleneck else 1))
                 audio = self._graph(("dec", tuple(codes.shape), out_len),
                                     lambda c: rt.decode(c, out_len), (codes,))
             else:
+                rt.prepare(frames * (2 if rt.bottleneck else 1))
                 audio = rt.decode(codes, out_len)
         if not return_dict:
-            return audio, None
-        return MimiDecoderOutput(audio, None)
+            return audio, kv
+        return MimiDecoderOutput(audio, kv)
 
     def forward(self, input_values: torch.Tensor, padding_mask: torch.Tensor | None = None,
                 num_quantizers: int | None = None, audio_codes: torch.Tensor | None = None,
@@ -357,13 +365,17 @@ class MimiModel:
                 return_dict: bool | None = None):
         """Encode→decode round trip (``model.py:3452-3538``); with ``audio_codes``
         given, decode only.  The mask crops the decoded audio to its length."""
-        _no_streaming(encoder_past_key_values=encoder_past_key_values,
-                      decoder_past_key_values=decoder_past_key_values)
         return_dict = self.config.return_dict if return_dict is None else return_dict
         mask = torch.ones_like(input_values, dtype=torch.bool) if padding_mask is None else padding_mask
-        if audio_codes is not None:
-            dec = self.decode(audio_codes, mask, return_dict=True)
+        if audio_codes is not None or encoder_past_key_values is not None or decoder_past_key_values is not None:
+            # Decode-only, or stateful: the encode/decode entry points, eagerly where a cache is given.
+            if audio_codes is None:
+                enc = self.encode(input_values, mask, num_quantizers, encoder_past_key_values,
+                                  return_dict=True)
+                audio_codes, encoder_past_key_values = enc.audio_codes, enc.encoder_past_key_values
+            dec = self.decode(audio_codes, mask, decoder_past_key_values, return_dict=True)
             codes, audio = audio_codes, dec.audio_values
+            decoder_past_key_values = dec.decoder_past_key_values
         else:
             count = self._resolve_count(num_quantizers)
             self._check_audio(input_values)
@@ -383,8 +395,16 @@ class MimiModel:
                 else:
                     codes, audio = roundtrip(audio_in)
         if not return_dict:
-            return codes, audio
-        return MimiOutput(codes, audio, None, None)
+            return codes, audio, encoder_past_key_values, decoder_past_key_values
+        return MimiOutput(codes, audio, encoder_past_key_values, decoder_past_key_values)
+
+    def _new_padding_cache(self) -> MimiConv1dPaddingCache:
+        """Empty streaming conv cache over the encoder convolutions and the
+        bottleneck downsample, in module order (``model.py:3047-3068``)."""
+        layers = self.runtime().stream_conv_layers()
+        return MimiConv1dPaddingCache(
+            len(layers), [c.k - c.stride for c, _ in layers], [m for _, m in layers],
+            [c.c_in for c, _ in layers])
 
     # -------------------------------------------------------- length helpers
     def get_encoded_length(self, input_length: torch.Tensor) -> torch.Tensor:

@@ -334,11 +334,32 @@ class MimiRuntime:
         return h.reshape(B, T, C)
 
     # ------------------------------------------------------------- stages
-    def encode(self, audio: torch.Tensor, num_quantizers: int) -> torch.Tensor:
-        """``[B, C, S]`` float32 audio -> ``[B, nq, T]`` int64 codes."""
-        cfg = self.config
+    def encode(self, audio: torch.Tensor, num_quantizers: int, padding_cache=None,
+               kv_cache=None) -> torch.Tensor:
+        """``[B, C, S]`` float32 audio -> ``[B, nq, T]`` int64 codes.
+
+        With ``padding_cache`` the convolutions run on cached left context with
+        no right padding (streaming); with ``kv_cache`` the transformer
+        continues from cached keys/values (``model.py:2964-3005``)."""
         B, C, S = audio.shape
         x = audio if C == 1 else audio.transpose(1, 2).contiguous()
+        if padding_cache is None:
+            h, L = self._encoder_seanet(x, B, S)
+        else:
+            h, L = self._encoder_seanet_stream(x.view(B, S, C), B, padding_cache)
+        if kv_cache is None:
+            h = self.transformer(h, B, L, self.enc_tf, "enc.tf")
+        else:
+            h = self.transformer_cached(h, B, L, self.enc_tf, kv_cache)
+        if self.bottleneck:
+            self._tag = "down"
+            if padding_cache is None:
+                h, L = self._conv(h, B, L, self.down)
+            else:
+                h, L = self._stream_conv(h, self.down, padding_cache, len(padding_cache.padding_cache) - 1)
+        return self.quantize(h, B, L, num_quantizers)
+
+    def _encoder_seanet(self, x, B, S):
         self._tag = "enc.first"
         h, L = self._conv(x, B, S, self.enc_first)
         n = len(self.enc_stages)
@@ -348,11 +369,105 @@ class MimiRuntime:
             h, L = self._conv(h, B, L, down, nat.EPI_ELU if i == n - 1 else 0)
         self._tag = "enc.last"
         h, L = self._conv(h, B, L, self.enc_last)
-        h = self.transformer(h, B, L, self.enc_tf, "enc.tf")
+        return h, L
+
+    # ------------------------------------------------------------ streaming
+    def stream_conv_layers(self) -> list[tuple[_Conv, str]]:
+        """The convolutions a streaming encode caches, in the reference's
+        order (encoder modules, then the bottleneck downsample;
+        ``model.py:3047-3068``), with their padding modes."""
+        convs = [(self.enc_first, "constant")]
+        for (c1, c2), down in self.enc_stages:
+            convs += [(c1, "constant"), (c2, "constant"), (down, "constant")]
+        convs.append((self.enc_last, "constant"))
         if self.bottleneck:
-            self._tag = "down"
-            h, L = self._conv(h, B, L, self.down)
-        return self.quantize(h, B, L, num_quantizers)
+            convs.append((self.down, "replicate"))
+        return convs
+
+    def _stream_conv(self, x, layer: _Conv, cache, idx: int, flags: int = 0, residual=None):
+        """One cached causal conv: the layer runs on (context ++ chunk) with no
+        padding; the cache keeps the newest ``k - stride`` input rows."""
+        B, L, _ = x.shape
+        ctx = cache.update(x, idx)
+        buf = torch.cat((ctx, x), dim=1) if ctx.shape[1] else x
+        total = buf.shape[1]
+        if total < layer.k:
+            raise RuntimeError(f"streaming chunk too short: {total} rows for a kernel of {layer.k}")
+        rows = (total - layer.k) // layer.stride + 1
+        y = torch.empty((B, rows, layer.c_out), device=self.device)
+        self._call("fm_conv1d_valid", buf.data_ptr(), B, total, layer.c_in, layer.w.data_ptr(),
+                   _ptr(layer.b), layer.c_out, layer.k, layer.stride, flags, _ptr(residual),
+                   y.data_ptr(), self.workspace.data_ptr(), _WORKSPACE_BYTES, self._stream())
+        return y, rows
+
+    def _encoder_seanet_stream(self, x, B, cache):
+        i = 0
+        self._tag = "enc.first"
+        h, L = self._stream_conv(x, self.enc_first, cache, i)
+        i += 1
+        n = len(self.enc_stages)
+        for s, ((c1, c2), down) in enumerate(self.enc_stages):
+            self._tag = f"enc.res{down.c_in}"
+            hid, _ = self._stream_conv(h, c1, cache, i, nat.ELU_IN | nat.EPI_ELU)
+            h, L = self._stream_conv(hid, c2, cache, i + 1, nat.EPI_RES_ADD | nat.EPI_ELU, residual=h)
+            self._tag = f"enc.down{down.stride}"
+            h, L = self._stream_conv(h, down, cache, i + 2, nat.EPI_ELU if s == n - 1 else 0)
+            i += 3
+        self._tag = "enc.last"
+        return self._stream_conv(h, self.enc_last, cache, i)
+
+    def transformer_cached(self, h, B, T, layers, kv):
+        """Transformer continuing from a ``MimiKVCache``: positions start at
+        the cache length; each layer attends to its retained ``window - 1``
+        rotated keys/values plus this chunk's (``model.py:2129-2232``)."""
+        cfg = self.config
+        M = B * T
+        C = cfg.hidden_size
+        nh, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        lib = nat.library()
+        fused = (M <= _ROW_LINEAR_MAX_ROWS and hd == 64
+                 and lib.fm_row_linear_supported(C, layers[0].wqkv.shape[0])
+                 and lib.fm_row_linear_supported(C, layers[0].w1.shape[0])
+                 and lib.fm_row_linear_supported(nh * hd, C))
+        kv.configure_sliding_window(cfg.sliding_window)
+        past = kv.get_seq_length()
+        cos, sin = self._rope_tables(past + T)
+        cos, sin = cos[past:], sin[past:]
+        h = h.reshape(M, C)
+        att = torch.empty((M, nh * hd), device=self.device)
+        qd, kd = nh * hd, nkv * hd
+        s = self._stream()
+        xln = None if fused else torch.empty((M, C), device=self.device)
+        for li, lay in enumerate(layers):
+            if fused:
+                qkv = self._row_linear(h, M, lay.wqkv, ln=lay.ln1, rope=(cos, sin, qd + kd, T))
+            else:
+                self._call("fm_layer_norm", h.data_ptr(), lay.ln1[0].data_ptr(), lay.ln1[1].data_ptr(),
+                           M, C, cfg.norm_eps, xln.data_ptr(), s)
+                qkv = self._linear(xln, M, lay.wqkv)
+                self._call("fm_apply_rope", qkv.data_ptr(), M, qkv.shape[1], qd + kd, hd,
+                           cos.data_ptr(), sin.data_ptr(), T, s)
+            ld = qkv.shape[1]
+            q3 = qkv.view(B, T, ld)
+            keys, values = kv.update(q3[:, :, qd:qd + kd], q3[:, :, qd + kd:], li)
+            n = keys.shape[1] - T
+            comb = torch.empty((B, n + T, ld), device=self.device)
+            comb[:, :, qd:qd + kd] = keys
+            comb[:, :, qd + kd:] = values
+            comb[:, n:, :qd] = q3[:, :, :qd]
+            self._call("fm_window_attention_rows", comb.data_ptr(), ld, 0, qd, qd + kd, None, None,
+                       B, n + T, n, nh, nkv, hd, cfg.sliding_window, 1.0 / (hd ** 0.5),
+                       att.data_ptr(), qd, s)
+            if fused:
+                self._row_linear(att, M, lay.wo, nat.EPI_RES_SCALE, residual=h, scale=lay.ls1, out=h)
+                ff = self._row_linear(h, M, lay.w1, nat.EPI_GELU, ln=lay.ln2)
+            else:
+                self._linear(att, M, lay.wo, nat.EPI_RES_SCALE, residual=h, scale=lay.ls1, out=h)
+                self._call("fm_layer_norm", h.data_ptr(), lay.ln2[0].data_ptr(), lay.ln2[1].data_ptr(),
+                           M, C, cfg.norm_eps, xln.data_ptr(), s)
+                ff = self._linear(xln, M, lay.w1, nat.EPI_GELU)
+            self._proj(ff, M, lay.w2, nat.EPI_RES_SCALE, residual=h, scale=lay.ls2, out=h)
+        return h.reshape(B, T, C)
 
     def quantize(self, h, B, T, nq):
         cfg = self.config
@@ -376,8 +491,10 @@ class MimiRuntime:
                      codes.data_ptr() + first * T * 8, nq * T, ws.data_ptr(), ws_bytes, s)
         return codes
 
-    def decode(self, codes: torch.Tensor, out_length: int | None = None) -> torch.Tensor:
-        """``[B, nq, T]`` int64 codes -> ``[B, 1, out_length]`` float32 audio."""
+    def decode(self, codes: torch.Tensor, out_length: int | None = None, kv_cache=None) -> torch.Tensor:
+        """``[B, nq, T]`` int64 codes -> ``[B, 1, out_length]`` float32 audio.
+        With ``kv_cache`` the decoder transformer continues from it; everything
+        else decodes the chunk alone (``model.py:3139-3170``)."""
         cfg = self.config
         B, nq, T = codes.shape
         M = B * T
@@ -395,7 +512,10 @@ class MimiRuntime:
             self._call("fm_upsample_depthwise", h.data_ptr(), B, L, cfg.hidden_size,
                      self.up_w.data_ptr(), self.up_k, 2, up.data_ptr(), self._stream())
             h, L = up, 2 * L
-        h = self.transformer(h, B, L, self.dec_tf, "dec.tf")
+        if kv_cache is None:
+            h = self.transformer(h, B, L, self.dec_tf, "dec.tf")
+        else:
+            h = self.transformer_cached(h, B, L, self.dec_tf, kv_cache)
         self._tag = "dec.first"
         h, L = self._conv(h, B, L, self.dec_first, nat.EPI_ELU)
         n = len(self.dec_stages)

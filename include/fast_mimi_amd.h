@@ -64,6 +64,18 @@ int fm_conv1d(const float* x, int batch, int length, int in_channels, const floa
               size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * Conv1d over exactly the given rows, no padding: output row t reads input
+ * rows t*stride .. t*stride + kernel - 1; y is [batch][(length - kernel) /
+ * stride + 1][out_channels].  Streaming convolution: the caller prepends the
+ * layer's cached left context.  Replaces MimiConv1d.forward with a padding
+ * cache (model.py:764-797, MimiConv1dPaddingCache.update :536-620).
+ */
+int fm_conv1d_valid(const float* x, int batch, int length, int in_channels,
+                    const float* weight_packed, const float* bias, int out_channels, int kernel,
+                    int stride, int flags, const float* residual, float* y, float* workspace,
+                    size_t workspace_bytes, hipStream_t stream);
+
+/*
  * Causal ConvTranspose1d with the full right trim (trim ratio 1): output
  * [batch][length * stride][out_channels].  kernel must be a multiple of stride.
  * Replaces MimiConvTranspose1d.forward (model.py:886-897),
@@ -144,6 +156,15 @@ int fm_pack_row_weights(const float* weight, int out_features, int in_features, 
                         hipStream_t stream);
 
 /*
+ * In-place RoPE on columns 0 .. rope_cols-1 of each row (heads of head_dim;
+ * position row % rows_per_seq into the [*, head_dim] cos/sin tables), for
+ * projections computed without fm_row_linear's fused epilogue (e.g. cached
+ * transformer steps at other widths).  Replaces _apply_rope (model.py:1551-1569).
+ */
+int fm_apply_rope(float* x, long rows, int ld, int rope_cols, int head_dim, const float* cos_table,
+                  const float* sin_table, int rows_per_seq, hipStream_t stream);
+
+/*
  * LayerNorm over the last dimension (biased variance).
  * Replaces nn.LayerNorm in MimiTransformerLayer (model.py:2028-2061).
  */
@@ -168,6 +189,19 @@ int fm_window_attention(const float* qkv, int ld_qkv, int q_offset, int k_offset
                         const float* cos_table, const float* sin_table, int batch, int length,
                         int heads, int kv_heads, int head_dim, int window, float scale, float* out,
                         int ld_out, hipStream_t stream);
+
+/*
+ * fm_window_attention for the queries at rows query_start .. length-1 of each
+ * sequence; every row 0 .. length-1 is a key/value, so rows before
+ * query_start act as a KV cache.  out holds length - query_start rows per
+ * sequence.  Replaces the cached path of MimiAttention.forward with a
+ * MimiKVCache (model.py:1912-1914, :363-518, mask :1627-1688).
+ */
+int fm_window_attention_rows(const float* qkv, int ld_qkv, int q_offset, int k_offset,
+                             int v_offset, const float* cos_table, const float* sin_table,
+                             int batch, int length, int query_start, int heads, int kv_heads,
+                             int head_dim, int window, float scale, float* out, int ld_out,
+                             hipStream_t stream);
 
 /*
  * Codebook preparation: embed = embed_sum / max(cluster_usage, eps), its

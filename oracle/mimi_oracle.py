@@ -15,7 +15,9 @@ Pins (see ``tests/test_oracle.py``):
     ``tests/golden/make_golden.py`` from the reference itself): codes and
     waveforms, tiny and full-size configs — bit-exact;
   * Hugging Face ``transformers.MimiModel`` at the reference's tiny test config
-    (the reference's own test oracle, ``tests/conftest.py:31-55``) — bit-exact;
+    (the reference's own test oracle, ``tests/conftest.py:31-55``) — bit-exact,
+    offline and streaming (padding-cache encode, KV-cache decode; also the
+    full config's streaming encode);
   * float64 brute force of every primitive on tiny inputs (conv padding and
     stride alignment, transposed-conv trim, replicate padding, RoPE, windowed
     causal softmax attention, LayerNorm, exact-erf GELU, ELU, the cdist
@@ -93,6 +95,24 @@ class Trace:
     rvq_inputs: list = field(default_factory=list)  # per codebook: [N, D] query rows
     quantized: torch.Tensor | None = None
     decoder_in: torch.Tensor | None = None
+
+
+class KVState:
+    """Per-layer retained rotated keys/values ``[B, H, n, D]`` plus the
+    cumulative position count (``MimiKVCache``, model.py:363-518)."""
+
+    def __init__(self, layers):
+        self.keys = [None] * layers
+        self.values = [None] * layers
+        self.length = 0
+
+
+@dataclass
+class StreamState:
+    """Encoder streaming state: per-conv left contexts (keyed by module
+    prefix) and the encoder transformer's KV cache."""
+    encoder_kv: KVState
+    conv: dict = field(default_factory=dict)
 
 
 class MimiOracle:
@@ -173,12 +193,14 @@ class MimiOracle:
         return self._conv(h, f"decoder.layers.{self.dec_last}")
 
     # ---------------- transformer (model.py:1454-2232) ----------------
-    def rope_tables(self, batch, length):
-        """``MimiRotaryEmbedding`` (model.py:1484-1535) for positions 0..T-1."""
+    def rope_tables(self, batch, length, offset=0):
+        """``MimiRotaryEmbedding`` (model.py:1484-1535) for positions
+        offset .. offset+T-1 (a streaming chunk starts at the cache length,
+        model.py:2179-2186)."""
         cfg = self.config
         inv_freq = 1.0 / (cfg.rope_theta ** (
             torch.arange(0, cfg.head_dim, 2, dtype=torch.int64).float() / cfg.head_dim))
-        positions = torch.arange(length).unsqueeze(0).expand(batch, -1)
+        positions = torch.arange(offset, offset + length).unsqueeze(0).expand(batch, -1)
         inv = inv_freq[None, :, None].float().expand(batch, -1, 1)
         freqs = (inv.float() @ positions[:, None, :].float()).transpose(1, 2)
         emb = torch.cat((freqs, freqs), dim=-1)
@@ -235,6 +257,131 @@ class MimiOracle:
             m = F.linear(F.gelu(F.linear(x, self._w(f"{p}.mlp.fc1.weight"))), self._w(f"{p}.mlp.fc2.weight"))
             hidden = hidden + self._w(f"{p}.mlp_layer_scale.scale") * m
         return hidden
+
+    # ---------------- streaming (model.py:363-621, :697-797, :2129-2232, :2964-3202) ----------------
+    def _conv_stream(self, x, prefix, state, stride=1, dilation=1, pad_mode="constant"):
+        """``MimiConv1d.forward`` with a padding cache (model.py:764-797) and
+        ``MimiConv1dPaddingCache.update`` (model.py:536-620): the layer sees
+        its cached left context followed by the chunk, with no right padding;
+        the cache keeps the last ``k_eff - stride`` samples of that input.
+        The first chunk's context is zeros, or its first sample repeated for
+        replicate padding."""
+        w = self._w(f"{prefix}.conv.weight")
+        pad = (w.shape[-1] - 1) * dilation + 1 - stride
+        ctx = state.conv.get(prefix)
+        if ctx is None:
+            if pad_mode == "constant":
+                ctx = x.new_zeros((x.shape[0], x.shape[1], pad))
+            elif pad_mode == "replicate":
+                ctx = x[..., :1].expand(x.shape[0], x.shape[1], pad).clone()
+            else:
+                raise NotImplementedError(f"padding mode {pad_mode!r} is not supported for streaming")
+        xx = torch.cat((ctx, x), dim=-1)
+        state.conv[prefix] = xx[..., xx.shape[-1] - pad:] if pad > 0 else x.new_empty((x.shape[0], x.shape[1], 0))
+        return F.conv1d(xx, w, self.state.get(f"{prefix}.conv.bias"), stride, 0, dilation)
+
+    def _resblock_stream(self, x, prefix, dilation, state):
+        h = self._conv_stream(elu(x), f"{prefix}.block.1", state, dilation=dilation)
+        h = self._conv_stream(elu(h), f"{prefix}.block.3", state)
+        residual = x
+        if self.config.use_conv_shortcut:
+            residual = self._conv_stream(x, f"{prefix}.shortcut", state)
+        return residual + h
+
+    def encoder_stream(self, x, state):
+        """``MimiEncoder._forward_eager`` with a padding cache (model.py:1067-1084)."""
+        cfg = self.config
+        h = self._conv_stream(x, "encoder.layers.0", state)
+        for stage, ratio in enumerate(reversed(cfg.upsampling_ratios)):
+            for r, li in enumerate(self.enc_res[stage]):
+                h = self._resblock_stream(h, f"encoder.layers.{li}", cfg.dilation_growth_rate ** r, state)
+            h = elu(h)
+            h = self._conv_stream(h, f"encoder.layers.{self.enc_down[stage]}", state, stride=ratio)
+        h = elu(h)
+        return self._conv_stream(h, f"encoder.layers.{self.enc_last}", state)
+
+    def transformer_cached(self, hidden, prefix, kv):
+        """``MimiTransformerModel.forward`` with a ``MimiKVCache``
+        (model.py:2129-2232, :363-518): positions continue from the cache
+        length; each layer attends to its retained ``window - 1`` rotated
+        keys/values plus the chunk; the explicit window mask is skipped in
+        exactly the cases ``_attention_mask`` skips it (model.py:1627-1688),
+        SDPA then being causal for more than one query (model.py:1846-1866)."""
+        cfg = self.config
+        b, t, _ = hidden.shape
+        window = cfg.sliding_window
+        past = kv.length
+        cos, sin = self.rope_tables(b, t, offset=past)
+        cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
+        key_offset = max(past - window + 1, 0)
+        key_length = (window - 1 + t) if past >= window else past + t
+        if key_length < window and (t == 1 or key_length == t or past == 0):
+            mask = None
+        else:
+            qp = torch.arange(t)[:, None] + past
+            kp = torch.arange(key_length)[None, :] + key_offset
+            mask = ((kp <= qp) & (kp > qp - window))[None, None].expand(b, 1, t, key_length)
+        nh, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        for i in range(cfg.num_hidden_layers):
+            p = f"{prefix}.layers.{i}"
+            x = F.layer_norm(hidden, (cfg.hidden_size,), self._w(f"{p}.input_layernorm.weight"),
+                             self._w(f"{p}.input_layernorm.bias"), cfg.norm_eps)
+            q = F.linear(x, self._w(f"{p}.self_attn.q_proj.weight")).view(b, t, nh, hd).transpose(1, 2)
+            k = F.linear(x, self._w(f"{p}.self_attn.k_proj.weight")).view(b, t, nkv, hd).transpose(1, 2)
+            v = F.linear(x, self._w(f"{p}.self_attn.v_proj.weight")).view(b, t, nkv, hd).transpose(1, 2)
+            q, k = q * cos + self._rotate_half(q) * sin, k * cos + self._rotate_half(k) * sin
+            if kv.keys[i] is not None:
+                k = torch.cat((kv.keys[i], k), dim=-2)
+                v = torch.cat((kv.values[i], v), dim=-2)
+            keep = window - 1
+            kv.keys[i] = k[..., -keep:, :] if keep > 0 else k[..., :0, :]
+            kv.values[i] = v[..., -keep:, :] if keep > 0 else v[..., :0, :]
+            n = k.shape[-2]
+            if nh != nkv:
+                rep = nh // nkv
+                k = k[:, :, None].expand(b, nkv, rep, n, hd).reshape(b, nh, n, hd)
+                v = v[:, :, None].expand(b, nkv, rep, n, hd).reshape(b, nh, n, hd)
+            o = F.scaled_dot_product_attention(
+                q, k, v, attn_mask=mask, dropout_p=0.0, scale=1.0 / math.sqrt(hd),
+                is_causal=(t > 1 and mask is None))
+            o = o.transpose(1, 2).contiguous()
+            o = F.linear(o.reshape(b, t, -1).contiguous(), self._w(f"{p}.self_attn.o_proj.weight"))
+            hidden = hidden + self._w(f"{p}.self_attn_layer_scale.scale") * o
+            x = F.layer_norm(hidden, (cfg.hidden_size,), self._w(f"{p}.post_attention_layernorm.weight"),
+                             self._w(f"{p}.post_attention_layernorm.bias"), cfg.norm_eps)
+            m = F.linear(F.gelu(F.linear(x, self._w(f"{p}.mlp.fc1.weight"))), self._w(f"{p}.mlp.fc2.weight"))
+            hidden = hidden + self._w(f"{p}.mlp_layer_scale.scale") * m
+        kv.length += t
+        return hidden
+
+    @torch.inference_mode()
+    def encode_stream(self, chunk, num_quantizers, state, trace=None):
+        """One ``encode(..., use_streaming=True)`` call (model.py:3070-3137,
+        :2964-3005): SEANet encoder and downsample on padding caches, encoder
+        transformer on its KV cache, then the (stateless) split RVQ."""
+        emb = self.encoder_stream(chunk, state)
+        h = self.transformer_cached(emb.transpose(1, 2), "encoder_transformer", state.encoder_kv)
+        emb = h.transpose(1, 2)
+        if self._bottleneck_ratio() is not None:
+            emb = self._conv_stream(emb, "downsample", state, stride=2, pad_mode="replicate")
+        return self.quantizer_encode(emb, num_quantizers, trace)
+
+    @torch.inference_mode()
+    def decode_cached(self, codes, kv):
+        """``decode(codes, decoder_past_key_values=kv)`` (model.py:3139-3202):
+        only the decoder transformer carries state; RVQ decode, upsample and
+        the SEANet decoder run on the chunk alone."""
+        emb = self.quantizer_decode(codes)
+        if self._bottleneck_ratio() is not None:
+            emb = self._convt(emb, "upsample", stride=2, groups=self.config.upsample_groups)
+        h = self.transformer_cached(emb.transpose(1, 2), "decoder_transformer", kv)
+        return self.decoder(h.transpose(1, 2))
+
+    def new_stream(self):
+        return StreamState(encoder_kv=KVState(self.config.num_hidden_layers))
+
+    def new_kv(self):
+        return KVState(self.config.num_hidden_layers)
 
     # ---------------- quantizer (model.py:2238-2696) ----------------
     def embed(self, codebook_prefix):

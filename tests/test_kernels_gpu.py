@@ -382,6 +382,69 @@ def test_row_linear_rejects():
         run_row_linear(x2, w2, ln=(gb, gb))
 
 
+@pytest.mark.parametrize("B,L,ci,co,k,s,flags", [
+    (1, 13, 1, 64, 7, 1, 0), (2, 40, 64, 32, 3, 1, nat.ELU_IN | nat.EPI_ELU),
+    (1, 22, 128, 256, 10, 5, 0), (3, 9, 512, 512, 4, 2, 0), (1, 18, 32, 64, 1, 1, 0)])
+def test_conv1d_valid(B, L, ci, co, k, s, flags, ws):
+    """No-padding conv (streaming): output t reads rows t*s .. t*s + k - 1."""
+    g = torch.Generator().manual_seed(L * k + ci)
+    x = torch.randn(B, ci, L, generator=g)
+    w = torch.randn(co, ci, k, generator=g) * 0.1
+    b = torch.randn(co, generator=g)
+    layer = _Conv(w.to(DEV), b.to(DEV), s)
+    xd = x.transpose(1, 2).contiguous().to(DEV)
+    rows = (L - k) // s + 1
+    y = torch.empty(B, rows, co, device=DEV)
+    nat.call("fm_conv1d_valid", xd.data_ptr(), B, L, ci, layer.w.data_ptr(), layer.b.data_ptr(),
+             co, k, s, flags, None, y.data_ptr(), ws.data_ptr(), WS_BYTES, stream())
+    torch.cuda.synchronize()
+    xin = F.elu(x.double()) if flags & nat.ELU_IN else x.double()
+    want = F.conv1d(xin, w.double(), b.double(), s)
+    if flags & nat.EPI_ELU:
+        want = F.elu(want)
+    close(y.cpu().transpose(1, 2), want)
+    with pytest.raises(nat.NativeError, match="bad argument"):
+        nat.call("fm_conv1d_valid", xd.data_ptr(), B, k - 1, ci, layer.w.data_ptr(), None, co, k, s,
+                 0, None, y.data_ptr(), ws.data_ptr(), WS_BYTES, stream())
+
+
+@pytest.mark.parametrize("B,T,q_start,window", [(1, 260, 249, 250), (2, 300, 249, 250),
+                                                (1, 10, 9, 250), (3, 12, 4, 8), (1, 64, 0, 250)])
+def test_window_attention_rows_with_cached_keys(B, T, q_start, window):
+    """Queries at rows q_start.. over all rows as keys (a KV cache in front)."""
+    H, D = 8, 64
+    g = torch.Generator().manual_seed(T + q_start)
+    qkv = torch.randn(B * T, 3 * H * D, generator=g)
+    out = torch.empty(B * (T - q_start), H * D, device=DEV)
+    qd = qkv.to(DEV)
+    nat.call("fm_window_attention_rows", qd.data_ptr(), 3 * H * D, 0, H * D, 2 * H * D, None, None,
+             B, T, q_start, H, H, D, window, 1.0 / math.sqrt(D), out.data_ptr(), H * D, stream())
+    torch.cuda.synchronize()
+    zeros = torch.zeros(T, D)
+    cos1 = torch.ones(T, D)  # identity rotation: q, k taken as given
+    want = attention_reference(qkv, B, T, H, D, window, cos1, zeros)
+    want = want.view(B, T, H * D)[:, q_start:].reshape(-1, H * D)
+    close(out.cpu(), want, rel=5e-5)
+
+
+@pytest.mark.parametrize("rows,T,H,D", [(250, 250, 8, 64), (7, 7, 2, 8), (40, 20, 2, 16)])
+def test_apply_rope_in_place(rows, T, H, D):
+    g = torch.Generator().manual_seed(rows + D)
+    x = torch.randn(rows, 3 * H * D, generator=g)
+    cfg = MimiConfig(head_dim=D, hidden_size=H * D, num_attention_heads=H, num_key_value_heads=H)
+    cos, sin = rope_tables(cfg, T)
+    xd, cd, sd = x.to(DEV), cos.to(DEV), sin.to(DEV)
+    nat.call("fm_apply_rope", xd.data_ptr(), rows, 3 * H * D, 2 * H * D, D, cd.data_ptr(),
+             sd.data_ptr(), T, stream())
+    torch.cuda.synchronize()
+    t = torch.arange(rows) % T
+    qk = x[:, : 2 * H * D].reshape(rows, 2 * H, D)
+    c, s_ = cos[t][:, None], sin[t][:, None]
+    want = x.clone()
+    want[:, : 2 * H * D] = (qk * c + MimiOracle._rotate_half(qk) * s_).reshape(rows, -1)
+    assert torch.equal(xd.cpu(), want)  # same rounding steps as the reference's _apply_rope
+
+
 def prepare_codebooks(embed_sum, usage):
     n, e, d = embed_sum.shape
     emb = torch.empty(n, e, d, device=DEV)

@@ -26,8 +26,6 @@ def test_validation_errors_precede_execution():
         model.encode(torch.zeros(1, 64))
     with pytest.raises(ValueError, match="channels"):
         model.encode(torch.zeros(1, 3, 64))
-    with pytest.raises(NotImplementedError, match="streaming"):
-        model.encode(torch.zeros(1, 1, 64), use_streaming=True)
     with pytest.raises(ValueError, match="attention_backend"):
         MimiModel(MimiConfig(**TINY), attention_backend="flash")
 
@@ -45,3 +43,55 @@ def test_output_container_behaves_like_model_output():
 def test_fp32_only():
     with pytest.raises(ValueError, match="float32"):
         MimiModel(MimiConfig(**TINY)).to(dtype=torch.float16)
+
+
+def test_kv_cache_window_and_positions():
+    """MimiKVCache semantics (model.py:363-518): window - 1 frames retained,
+    cumulative positions unbounded, mask sizes as _attention_mask needs them."""
+    from fast_mimi_amd import MimiKVCache
+
+    kv = MimiKVCache(2, sliding_window=4)
+    assert kv.get_seq_length() == 0 and kv.get_mask_sizes(2) == (2, 0)
+    for step in range(1, 6):
+        k = torch.full((1, 2, 3), float(step))
+        keys, values = kv.update(k, -k, 0)
+        assert kv.get_seq_length(0) == 2 * step
+        assert keys.shape[1] == min(2 * step - 2, 3) + 2        # stored + new frames
+        assert kv.key_cache[0].shape[1] == min(2 * step, 3)      # window - 1 kept
+        assert torch.equal(kv.value_cache[0], -kv.key_cache[0])
+    # 10 frames seen: keys visible to 2 more queries are the last 3 stored + 2 new.
+    assert kv.get_mask_sizes(2) == (5, 7)
+    assert kv.get_seq_length(1) == 0 and kv.get_seq_length(9) == 0
+    kv.update(torch.zeros(1, 1, 3), torch.zeros(1, 1, 3), 5)      # grows lazily
+    assert len(kv.key_cache) == 6
+    with pytest.raises(ValueError):
+        MimiKVCache(1, sliding_window=0)
+    with pytest.raises(ValueError, match="match"):
+        kv.configure_sliding_window(8)
+    late = MimiKVCache(1)
+    late.update(torch.arange(12.0).view(1, 6, 2), torch.zeros(1, 6, 2), 0)
+    late.configure_sliding_window(3)
+    assert late.key_cache[0].shape[1] == 2 and late.get_seq_length() == 6
+    assert torch.equal(late.key_cache[0], torch.arange(8.0, 12.0).view(1, 2, 2))
+
+
+def test_padding_cache_context_rules():
+    """MimiConv1dPaddingCache.update (model.py:536-620): zero or replicated
+    first context; the newest `padding` rows (of context + chunk) are kept."""
+    from fast_mimi_amd import MimiConv1dPaddingCache
+
+    pc = MimiConv1dPaddingCache(3, [3, 2, 0], ["constant", "replicate", "constant"], [1, 2, 4])
+    x = torch.arange(1.0, 3.0).view(1, 2, 1)                        # 2 rows < padding 3
+    assert torch.equal(pc.update(x, 0), torch.zeros(1, 3, 1))
+    assert torch.equal(pc.padding_cache[0].flatten(), torch.tensor([0.0, 1.0, 2.0]))
+    x2 = torch.arange(3.0, 8.0).view(1, 5, 1)
+    assert torch.equal(pc.update(x2, 0).flatten(), torch.tensor([0.0, 1.0, 2.0]))
+    assert torch.equal(pc.padding_cache[0].flatten(), torch.tensor([5.0, 6.0, 7.0]))
+    y = torch.tensor([[[4.0, 5.0], [6.0, 7.0], [8.0, 9.0]]])
+    assert torch.equal(pc.update(y, 1), torch.tensor([[[4.0, 5.0], [4.0, 5.0]]]))
+    assert torch.equal(pc.padding_cache[1], y[:, 1:])
+    assert pc.update(torch.ones(1, 3, 4), 2).shape == (1, 0, 4)
+    with pytest.raises(ValueError):
+        MimiConv1dPaddingCache(2, [1], ["constant"], [1])
+    with pytest.raises(NotImplementedError):
+        MimiConv1dPaddingCache(1, [1], ["reflect"], [1])

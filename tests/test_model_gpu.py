@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from conftest import TINY, torch_state, tiny_config
-from fast_mimi_amd import MimiConfig, MimiModel, synthetic
+from fast_mimi_amd import MimiConfig, MimiKVCache, MimiModel, synthetic
 from oracle.mimi_oracle import MimiOracle, Trace
 from rvq_check import certify
 
@@ -135,6 +135,83 @@ def test_large_configs_match_oracle_per_clip(full, name, clips):
             print(f"{name} clip {c}: {n} certified near-tie code rows (worst gap {worst:.2e})")
             ref_audio = oracle.decode(got, m[c:c + 1])
         assert_audio(values[c:c + 1], ref_audio)
+
+
+def _codes_match_or_near_tie(oracle, trace, got, want, what):
+    if torch.equal(got, want):
+        return
+    rows = [r for _, r in trace.rvq_inputs]
+    embeds = [oracle.embed(f"{p}.codebook") for p, _ in trace.rvq_inputs]
+    n, worst = certify(rows, embeds, got, want)
+    print(f"{what}: {n} certified near-tie code rows (worst gap {worst:.2e})")
+
+
+@pytest.mark.parametrize("batch,samples,chunk", [(1, 40, 8), (2, 96, 16), (1, 200, 24), (1, 72, 12)])
+def test_streaming_encode_tiny(tiny, batch, samples, chunk):
+    """encode(use_streaming=True) chunk by chunk, caches carried over
+    (the reference's test_parity.py:56-80 scenario) against the oracle."""
+    model, oracle = tiny
+    g = torch.Generator().manual_seed(samples)
+    audio = torch.randn(batch, 1, samples, generator=g) * 0.05
+    state = oracle.new_stream()
+    kv = pc = None
+    for piece in audio.split(chunk, dim=-1):
+        out = model.encode(piece.to(DEV), num_quantizers=4, encoder_past_key_values=kv,
+                           padding_cache=pc, use_streaming=True)
+        kv, pc = out.encoder_past_key_values, out.padding_cache
+        trace = Trace()
+        want = oracle.encode_stream(piece, 4, state, trace)
+        _codes_match_or_near_tie(oracle, trace, out.audio_codes.cpu(), want, "tiny stream")
+        assert kv.get_seq_length() == state.encoder_kv.length
+
+
+def test_streaming_encode_full_config(full):
+    """Full architecture, 80 ms (1920-sample) chunks, 0.64 s."""
+    model, oracle = full
+    audio, _ = synthetic.batch(1, 15_360, base_seed=3)
+    a = torch.from_numpy(audio)
+    state = oracle.new_stream()
+    kv = pc = None
+    for piece in a.split(1920, dim=-1):
+        out = model.encode(piece.to(DEV), num_quantizers=8, encoder_past_key_values=kv,
+                           padding_cache=pc, use_streaming=True)
+        kv, pc = out.encoder_past_key_values, out.padding_cache
+        trace = Trace()
+        want = oracle.encode_stream(piece, 8, state, trace)
+        _codes_match_or_near_tie(oracle, trace, out.audio_codes.cpu(), want, "full stream")
+    assert kv.get_seq_length() == state.encoder_kv.length == 15_360 // 960
+
+
+@pytest.mark.parametrize("which", ["tiny", "full"])
+def test_cached_decode_frame_by_frame(tiny, full, which):
+    """decode(codes, decoder_past_key_values=cache) one frame at a time past
+    the attention window (test_parity.py:83-110 scenario)."""
+    model, oracle = tiny if which == "tiny" else full
+    cfg = model.config
+    steps = 12 if which == "tiny" else 6
+    g = torch.Generator().manual_seed(99)
+    cache = MimiKVCache(cfg.num_hidden_layers)
+    kv = oracle.new_kv()
+    for _ in range(steps):
+        codes = torch.randint(0, cfg.codebook_size, (1, min(cfg.num_quantizers, 8), 1), generator=g)
+        out = model.decode(codes.to(DEV), decoder_past_key_values=cache)
+        want = oracle.decode_cached(codes, kv)
+        assert out.decoder_past_key_values is cache
+        assert_audio(out.audio_values.cpu(), want)
+        assert cache.get_seq_length() == kv.length
+        assert all(k is None or k.shape[1] <= cfg.sliding_window - 1 for k in cache.key_cache)
+
+
+def test_forward_with_caches_returns_them(tiny):
+    model, oracle = tiny
+    audio = torch.linspace(-0.1, 0.1, 32).view(1, 1, -1)
+    enc_kv, dec_kv = MimiKVCache(2), MimiKVCache(2)
+    out = model(audio.to(DEV), num_quantizers=4, encoder_past_key_values=enc_kv,
+                decoder_past_key_values=dec_kv)
+    assert out.encoder_past_key_values is enc_kv and out.decoder_past_key_values is dec_kv
+    assert enc_kv.get_seq_length() == 8 and dec_kv.get_seq_length() == 8
+    codes, values, e, d = model(audio.to(DEV), num_quantizers=4, return_dict=False)
+    assert e is None and d is None and values.shape == (1, 1, 32)
 
 
 def test_decode_only_and_encode_only(full):

@@ -4,7 +4,8 @@ GPU parity reference.
 * Reference golden vectors (tests/golden/reference_golden.npz, written by
   tests/golden/make_golden.py from kadirnar/fast-mimi itself): bit-exact.
 * Hugging Face transformers.MimiModel at the reference's tiny test config —
-  the oracle of the reference's own tests (tests/conftest.py:31-55): bit-exact.
+  the oracle of the reference's own tests (tests/conftest.py:31-55): bit-exact,
+  offline and streaming (padding-cache encode, KV-cache decode).
 * Float64 brute force / closed forms for every primitive, each written from the
   definition (loops, explicit sums), so a dropped term, wrong sign, index shift
   or transposed operand in the oracle fails one of them.
@@ -125,6 +126,67 @@ def test_tiny_matches_transformers_mimi(tiny_oracle):
         codes, values = tiny_oracle.forward(a, None, 4)
         assert torch.equal(codes, ref.audio_codes)
         assert torch.equal(values, ref.audio_values)
+
+
+def _hf_model(cfg, seed):
+    transformers = pytest.importorskip("transformers")
+    hf_cfg = transformers.MimiConfig(**cfg.to_dict())
+    hf_cfg._attn_implementation = "sdpa"
+    hf = transformers.MimiModel(hf_cfg).eval()
+    hf.load_state_dict(torch_state(cfg, seed), strict=True)
+    return hf
+
+
+@pytest.mark.parametrize("batch,samples,chunk", [(1, 40, 8), (2, 96, 16), (1, 200, 24), (1, 72, 12)])
+def test_streaming_encode_matches_transformers_mimi(tiny_oracle, batch, samples, chunk):
+    """Chunked encode with padding + KV caches (the reference's
+    test_parity.py:56-80 scenario), bit-exact codes and cache lengths."""
+    hf = _hf_model(tiny_config(), 1234)
+    g = torch.Generator().manual_seed(samples)
+    audio = torch.randn(batch, 1, samples, generator=g) * 0.05
+    state = tiny_oracle.new_stream()
+    kv = pc = None
+    for piece in audio.split(chunk, dim=-1):
+        codes = tiny_oracle.encode_stream(piece, 4, state)
+        with torch.inference_mode():
+            ref = hf.encode(piece, encoder_past_key_values=kv, padding_cache=pc, use_streaming=True)
+        kv, pc = ref.encoder_past_key_values, ref.padding_cache
+        assert torch.equal(codes, ref.audio_codes)
+        assert state.encoder_kv.length == kv.get_seq_length()
+
+
+def test_cached_decode_matches_transformers_mimi(tiny_oracle):
+    """Frame-by-frame decode through the decoder KV cache, past the window
+    (the reference's test_parity.py:83-110 scenario)."""
+    from transformers import DynamicCache
+
+    hf = _hf_model(tiny_config(), 1234)
+    g = torch.Generator().manual_seed(99)
+    kv, hc = tiny_oracle.new_kv(), DynamicCache(config=hf.config)
+    for _ in range(12):
+        codes = torch.randint(0, tiny_oracle.config.codebook_size, (1, 4, 1), generator=g)
+        audio = tiny_oracle.decode_cached(codes, kv)
+        with torch.inference_mode():
+            ref = hf.decode(codes, decoder_past_key_values=hc)
+        assert torch.equal(audio, ref.audio_values)
+        assert kv.length == hc.get_seq_length()
+        assert all(k is None or k.shape[-2] <= tiny_oracle.config.sliding_window - 1 for k in kv.keys)
+
+
+def test_full_config_streaming_matches_transformers_mimi(full_oracle):
+    """Full architecture: 0.4 s in 80 ms frames (1920 samples) through the streaming encoder."""
+    hf = _hf_model(MimiConfig(), 0)
+    audio, _ = synthetic.batch(1, 9600, base_seed=3)
+    a = torch.from_numpy(audio)
+    state = full_oracle.new_stream()
+    kv = pc = None
+    for piece in a.split(1920, dim=-1):
+        codes = full_oracle.encode_stream(piece, 8, state)
+        with torch.inference_mode():
+            ref = hf.encode(piece, num_quantizers=8, encoder_past_key_values=kv, padding_cache=pc,
+                            use_streaming=True)
+        kv, pc = ref.encoder_past_key_values, ref.padding_cache
+        assert torch.equal(codes, ref.audio_codes)
 
 
 # -------------------------------------------------- float64 brute force
