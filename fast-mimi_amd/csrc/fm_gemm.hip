@@ -337,8 +337,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
   constexpr int APT = BM / RPP, BPT = BN / RPP;
   static_assert(FM >= 1 && FN >= 1 && BPT >= 1 && APT * RPP == BM && BPT * RPP == BN, "tiling");
 
-  __shared__ __attribute__((aligned(16))) float As[BM * P];
-  __shared__ __attribute__((aligned(16))) float Bs[BN * P];
+  // The operand stage and, after the k-loop, the finished output tile share one array.
+  constexpr int PC = BN + 4;
+  constexpr int STAGE_F = (BM + BN) * P, TILE_F = BM * PC;
+  __shared__ __attribute__((aligned(16))) float smem[STAGE_F > TILE_F ? STAGE_F : TILE_F];
+  float* As = smem;
+  float* Bs = smem + BM * P;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
@@ -371,26 +375,31 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
 #pragma unroll
   for (int i = 0; i < BPT; ++i) b_n[i] = n0 + rrow + i * RPP;
 
+  // Prefetched rows stay raw in registers, with a validity mask; the zeroing
+  // select happens at the LDS store, so nothing waits on the loads until the
+  // next k-tile (a select right after the load would expose their latency).
   floatx4 ra[APT], rb[BPT];
+  unsigned amask = 0, bmask = 0;
   auto load = [&](int k0) {
     const int kg = k0 + ck;
     const bool kok = kg < k_end;
     const int kc = min(kg, p.K - 4);
     const int tap = tap_uniform ? k0 / p.C_in : kc / p.C_in;
     const int cin = kc - tap * p.C_in;  // channel within the position
+    amask = bmask = 0;
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
       const int pos = a_p0[i] + tap;
       const bool ok = kok && (replicate ? a_p0[i] > INT_MIN / 2 : (pos >= 0 && pos < p.L_in));
       const int pc = min(max(pos, 0), p.L_in - 1);
-      const floatx4 v = *reinterpret_cast<const floatx4*>(p.x + a_org[i] + (long)pc * p.C_in + cin);
-      ra[i] = ok ? v : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      ra[i] = *reinterpret_cast<const floatx4*>(p.x + a_org[i] + (long)pc * p.C_in + cin);
+      amask |= (unsigned)ok << i;
     }
 #pragma unroll
     for (int i = 0; i < BPT; ++i) {
       const bool ok = kok && b_n[i] < p.N;
-      const floatx4 v = *reinterpret_cast<const floatx4*>(p.w + (long)min(b_n[i], p.N - 1) * p.K + kc);
-      rb[i] = ok ? v : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      rb[i] = *reinterpret_cast<const floatx4*>(p.w + (long)min(b_n[i], p.N - 1) * p.K + kc);
+      bmask |= (unsigned)ok << i;
     }
   };
 
@@ -409,13 +418,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
-      floatx4 v = ra[i];
+      floatx4 v = ((amask >> i) & 1) ? ra[i] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
       if (elu_in) v = floatx4{fm_elu(v.x), fm_elu(v.y), fm_elu(v.z), fm_elu(v.w)};
       *reinterpret_cast<floatx4*>(As + (rrow + i * RPP) * P + ck) = v;
     }
 #pragma unroll
     for (int i = 0; i < BPT; ++i)
-      *reinterpret_cast<floatx4*>(Bs + (rrow + i * RPP) * P + ck) = rb[i];
+      *reinterpret_cast<floatx4*>(Bs + (rrow + i * RPP) * P + ck) =
+          ((bmask >> i) & 1) ? rb[i] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     __syncthreads();
     if (k0 + BK < k_end) load(k0 + BK);
 #pragma unroll
@@ -436,42 +446,49 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
     }
   }
 
+  // Epilogue through LDS: the waves drop their accumulators into the tile,
+  // then each thread finishes float4 runs of a row (bias, residual, ELU) with
+  // one bounds check per run and 16-byte loads and stores.
+  __syncthreads();  // every wave is done reading the operand stage
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        smem[(wm0 + i * 32 + fm_mfma32_row(r, lane)) * PC + wn0 + j * 32 + lcol] = acc[i][j][r];
+  __syncthreads();
   const bool crop = p.y_rows != p.rows;
   const bool has_res = p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE);
   float* part = p.partial ? p.partial + (long)blockIdx.y * M * p.N : nullptr;
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int n = n0 + wn0 + j * 32 + lcol;
-    const int nc = min(n, p.N - 1);
-    const float bias = p.bias ? p.bias[nc % p.bias_len] : 0.0f;
-    const float scale = (p.flags & FM_EPI_RES_SCALE) ? p.scale[nc] : 0.0f;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      // Residual loads of this 32-row block first, then its 16 stores.
-      float rv[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const long m = min(m0 + wm0 + i * 32 + fm_mfma32_row(r, lane), M - 1);
-        rv[r] = (has_res && !part) ? p.res[m * p.N + nc] : 0.0f;
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const long m = m0 + wm0 + i * 32 + fm_mfma32_row(r, lane);
-        if (m >= M || n >= p.N) continue;
-        if (part) {
-          part[m * p.N + n] = acc[i][j][r];
-          continue;
-        }
-        const float v = epilogue_v(acc[i][j][r], bias, rv[r], scale, p.flags);
-        if (!crop) {
-          p.y[m * p.N + n] = v;
-        } else {
-          const int b = (int)(m / p.rows);
-          const int t = (int)(m - (long)b * p.rows);
-          if (t < p.y_rows) p.y[((long)b * p.y_rows + t) * p.N + n] = v;
-        }
-      }
+  constexpr int RUNS = BM * BN / 4;
+#pragma unroll 2
+  for (int u = tid; u < RUNS; u += NTH) {
+    const int r = u / (BN / 4), c = (u % (BN / 4)) * 4;
+    const long m = m0 + r;
+    const int n = n0 + c;
+    if (m >= M || n >= p.N) continue;
+    floatx4 v = *reinterpret_cast<const floatx4*>(smem + r * PC + c);
+    if (part) {
+      *reinterpret_cast<floatx4*>(part + m * p.N + n) = v;
+      continue;
     }
+    const floatx4 bias = p.bias ? *reinterpret_cast<const floatx4*>(p.bias + n % p.bias_len)
+                                : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    const floatx4 res = has_res ? *reinterpret_cast<const floatx4*>(p.res + m * p.N + n)
+                                : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    const floatx4 scale = (p.flags & FM_EPI_RES_SCALE) ? *reinterpret_cast<const floatx4*>(p.scale + n)
+                                                       : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = epilogue_v(v[e], bias[e], res[e], scale[e], p.flags);
+    long dst = m * p.N + n;
+    if (crop) {
+      const int b = (int)(m / p.rows);
+      const int t = (int)(m - (long)b * p.rows);
+      if (t >= p.y_rows) continue;
+      dst = ((long)b * p.y_rows + t) * p.N + n;
+    }
+    *reinterpret_cast<floatx4*>(p.y + dst) = v;
   }
 }
 
@@ -685,6 +702,8 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     // the output are skipped (the narrowest fallback is always eligible).
     for (const TileCfg& t : kTiles) {
       if (t.WK == 1 && t.BN > 32 && t.BN / 2 >= p.N) continue;
+      // The 256-row tile's float4 epilogue needs 4-aligned rows and bias periods.
+      if (t.id == 6 && (p.N % 4 || (p.bias && p.bias_len % 4))) continue;
       cfg = t;
       tiles = tile_count(M, p.N, t);
       if (tiles >= t.fill) break;

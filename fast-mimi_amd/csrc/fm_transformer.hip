@@ -62,15 +62,17 @@ struct RowTile {
   static constexpr int HALF = D / 2, PAIRS = QB * D / 8;
   static constexpr int N = (PAIRS + NTH - 1) / NTH;
   floatx4 lo[N], hi[N], c[N], s[N];
+  unsigned okm;  // rows inside the sequence; zeroing waits for the store (see VTile)
 
   FM_DEVICE void load(int tid, const float* __restrict__ src, long ld, int t0, int t_last,
                       const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+    okm = 0;
 #pragma unroll
     for (int u = 0; u < N; ++u) {
       const int e = tid + u * NTH;
       const int r = e / (D / 8), d = (e % (D / 8)) * 4;
       const int t = min(t0 + r, t_last);
-      const bool ok = e < PAIRS && t0 + r <= t_last;
+      okm |= (unsigned)(e < PAIRS && t0 + r <= t_last) << u;
       const float* row = src + (long)t * ld;
       lo[u] = *reinterpret_cast<const floatx4*>(row + d);
       hi[u] = *reinterpret_cast<const floatx4*>(row + d + HALF);
@@ -78,7 +80,6 @@ struct RowTile {
         c[u] = *reinterpret_cast<const floatx4*>(cos_t + (long)t * D + d);
         s[u] = *reinterpret_cast<const floatx4*>(sin_t + (long)t * D + d);
       }
-      if (!ok) lo[u] = hi[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
   }
   // Writes the tile to dst[row * pitch + dim], rotated when ROPE.
@@ -88,7 +89,9 @@ struct RowTile {
       const int e = tid + u * NTH;
       if (PAIRS % NTH && e >= PAIRS) continue;
       const int r = e / (D / 8), d = (e % (D / 8)) * 4;
-      floatx4 l = lo[u], h = hi[u];
+      const bool ok = (okm >> u) & 1;
+      floatx4 l = ok ? lo[u] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      floatx4 h = ok ? hi[u] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
       if (ROPE) rope_pair(l, h, c[u], s[u]);
       *reinterpret_cast<floatx4*>(dst + r * pitch + d) = l;
       *reinterpret_cast<floatx4*>(dst + r * pitch + d + HALF) = h;
@@ -101,14 +104,18 @@ template <int D, int DP>
 struct VTile {
   static constexpr int CHUNKS = QB * DP / 4, N = (CHUNKS + 63) / 64;
   floatx4 v[N];
+  // Validity bits; the zeroing select is applied at the store, so a prefetch
+  // does not wait for its loads where it is issued.
+  unsigned okm;
   FM_DEVICE void load(int lane, const float* __restrict__ src, long ld, int t0, int t_last) {
+    okm = 0;
 #pragma unroll
     for (int u = 0; u < N; ++u) {
       const int e = lane + u * 64;
       const int r = e / (DP / 4), d = (e % (DP / 4)) * 4;
       const int t = min(t0 + r, t_last);
       v[u] = *reinterpret_cast<const floatx4*>(src + (long)t * ld + min(d, D - 4));
-      if (!(e < CHUNKS && t0 + r <= t_last && d < D)) v[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      okm |= (unsigned)(e < CHUNKS && t0 + r <= t_last && d < D) << u;
     }
   }
   FM_DEVICE void store(int lane, float* dst, int pitch) {
@@ -117,7 +124,8 @@ struct VTile {
       const int e = lane + u * 64;
       if (CHUNKS % 64 && e >= CHUNKS) continue;
       const int r = e / (DP / 4), d = (e % (DP / 4)) * 4;
-      *reinterpret_cast<floatx4*>(dst + r * pitch + d) = v[u];
+      *reinterpret_cast<floatx4*>(dst + r * pitch + d) =
+          ((okm >> u) & 1) ? v[u] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
   }
 };
