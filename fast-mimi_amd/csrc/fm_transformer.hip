@@ -320,7 +320,8 @@ __global__ __launch_bounds__(64 * NWV) void row_linear_kernel(
     const float* res, const float* __restrict__ scale, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, int rope_cols, int rows_per_seq, float* y) {
   constexpr int BM = 32, NTH = 64 * NWV, PA = K + 4, KW = K / NWV, KT = KW / 32, NJ = BN / 32;
-  constexpr int PR = BN + 4, TPR = NTH / BM, CH = K / 4 / TPR, OPT = BM * BN / NTH;
+  // PR = 8 mod 16: the two lane halves (4 rows apart) store 32 banks apart.
+  constexpr int PR = BN + 8, TPR = NTH / BM, CH = K / 4 / TPR, OPT = BM * BN / NTH;
   static_assert(KW % 32 == 0 && CH >= 1 && OPT % 2 == 0, "tile shape");
   extern __shared__ __attribute__((aligned(16))) float sm[];
   float* As = sm;   // [BM][PA]
@@ -459,7 +460,8 @@ template <int K>
 __global__ __launch_bounds__(512) void row_stream_linear_kernel(
     const float* __restrict__ x, int rows, const float* __restrict__ w, int N, int flags,
     const float* res, const float* __restrict__ scale, float* y) {
-  constexpr int NWV = 8, KW = K / NWV, NP = KW / 64, PR = 33;
+  // PR = 8 mod 16: the two lane halves (4 rows apart) store 32 banks apart.
+  constexpr int NWV = 8, KW = K / NWV, NP = KW / 64, PR = 40;
   static_assert(KW % 64 == 0, "whole 64-dim pieces per wave");
   __shared__ float red[NWV * 32 * PR];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -543,7 +545,8 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
     const float* __restrict__ sin_t, int rope_cols, int rows_per_seq, float* y) {
   constexpr int NWV = 8, BM = 16, KW = K / NWV, NP = KW / 64, NT = BN / 16;
   constexpr bool STAGE = (K == 512);
-  constexpr int PA = K + 4, PR = BN + 1, OPT = BM * BN / 512;
+  // PR = 4 mod 16: the four 16-lane groups of a partial-tile store hit disjoint banks.
+  constexpr int PA = K + 4, PR = BN + 4, OPT = BM * BN / 512;
   static_assert(KW % 64 == 0 && OPT >= 1, "tile shape");
   constexpr int A_FLOATS = STAGE ? BM * PA : 0, R_FLOATS = NWV * BM * PR;
   __shared__ __attribute__((aligned(16))) float sm[A_FLOATS > R_FLOATS ? A_FLOATS : R_FLOATS];
@@ -574,7 +577,9 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
                         : *reinterpret_cast<const floatx4*>(xs + 64 * piece + 4 * t);
   };
 
-  load_b(0, 0);
+  // The input rows are the critical path (LayerNorm, then the A operand):
+  // their loads go out first, the weight fragments right after.
+  if (!STAGE) load_b(0, 0);
   if (STAGE) {
     // 32 lanes per row, float4 chunks p, p + 32, ...
     constexpr int TPR = 32, CH = K / 4 / TPR;
@@ -584,6 +589,7 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
     floatx4 v[CH];
 #pragma unroll
     for (int u = 0; u < CH; ++u) v[u] = *reinterpret_cast<const floatx4*>(xr + 4 * (p + TPR * u));
+    load_b(0, 0);
     if (gamma) {
       floatx4 gv[CH], bv[CH];
 #pragma unroll
@@ -764,7 +770,7 @@ int fm_row_linear(const float* x, int rows, int in_features, const float* ln_gam
   const bool wide = rope_cos != nullptr;
 #define FM_ROWLIN(BN, NWV)                                                                       \
   {                                                                                              \
-    const size_t lds = std::max<size_t>((size_t)32 * (K + 4), (size_t)NWV * 32 * (BN + 4)) * 4;  \
+    const size_t lds = std::max<size_t>((size_t)32 * (K + 4), (size_t)NWV * 32 * (BN + 8)) * 4;  \
     hipLaunchKernelGGL((row_linear_kernel<K, BN, NWV>), dim3(out_features / BN, (rows + 31) / 32), \
                        dim3(64 * NWV), lds, stream, x, rows, ln_gamma, ln_beta, ln_eps, weight,   \
                        out_features, flags, residual, scale, rope_cos, rope_sin, rope_cols,      \
@@ -799,8 +805,11 @@ int fm_row_linear_packed(const float* x, int rows, int in_features, const float*
   hipLaunchKernelGGL((row16_linear_kernel<KK, BN>), G, dim3(512), 0, stream, x, rows, ln_gamma, \
                      ln_beta, ln_eps, weight_packed, out_features, flags, residual, scale,     \
                      rope_cos, rope_sin, rope_cols, rows_per_seq, y)
+  // 64-column blocks where RoPE needs whole heads, or where 32-column blocks
+  // would not all be resident at once (two 8-wave blocks per CU).
+  const bool wide = rope_cos || (long)(out_features / 32) * ((rows + 15) / 16) > 512;
   if (in_features == 2048) FM_R16(2048, 32, g32);
-  else if (rope_cos) FM_R16(512, 64, g64);
+  else if (wide) FM_R16(512, 64, g64);
   else FM_R16(512, 32, g32);
 #undef FM_R16
   return (int)hipGetLastError();
