@@ -40,7 +40,6 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float* __restrict
 
 constexpr int QB = 32;  // queries per block (one MFMA column tile)
 constexpr int KB = 32;  // keys per MFMA row tile
-constexpr int NW = 4;   // waves per block; they split the key range
 
 // RoPE as the reference writes it: x*cos + rotate_half(x)*sin, each product
 // and the sum rounded separately.  For the pair (x_d, x_{d+half}) with the
@@ -138,11 +137,11 @@ FM_DEVICE void wave_lds_fence() {
 }
 
 // Sliding-window causal attention on FP32 MFMA.
-// Grid: (ceil((T - q_start) / QB), heads, batch), 256 threads.  Queries are
+// Grid: (ceil((T - q_start) / QB), heads, batch), 64 * NW threads.  Queries are
 // rows q_start .. T-1 (earlier rows are cached keys/values only); query q
 // writes output row q - q_start.  Block = 32 queries of one
 // head; its key range [q0 - window + 1, q0 + 31] is cut into 32-key tiles that
-// the 4 waves take round-robin.  Waves run independently after the shared Q
+// the NW waves take round-robin.  Waves run independently after the shared Q
 // stage: each keeps its next K/V tile in flight in registers while it
 // computes on the current one from its own LDS slot (rows contiguous, K pitch
 // D+4, V pitch DP+8).  Per tile a wave computes S^T = K Q^T (keys on MFMA
@@ -153,11 +152,12 @@ FM_DEVICE void wave_lds_fence() {
 // registers: MFMA step s takes keys 8*(s/4) + 4*h + s%4, exactly the rows
 // that lane holds in accumulator slot s.  The waves' (max, sum, O) are merged
 // through LDS.  ROPE: rotate Q and K while staging (else they arrive rotated).
-template <int D, bool ROPE>
-__global__ __launch_bounds__(256) void window_attention_kernel(
+template <int D, bool ROPE, int NW>
+__global__ __launch_bounds__(64 * NW) void window_attention_kernel(
     const float* __restrict__ qkv, int ld, int q_off, int k_off, int v_off,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, int T, int q_start,
     int heads, int kv_heads, int window, float scale, float* __restrict__ out, int ld_out) {
+  constexpr int NTH = 64 * NW;
   constexpr int DT = (D + 31) / 32;  // 32-row tiles of O^T
   constexpr int DP = DT * 32;        // padded head dim of V / O
   constexpr int PK = D + 4, PV = DP + 8, P = QB + 1;
@@ -189,7 +189,7 @@ __global__ __launch_bounds__(256) void window_attention_kernel(
     vr.load(lane, vcol, ld, k_lo + wave * KB, k_hi);
   }
   {
-    RowTile<D, 256, ROPE> qr;
+    RowTile<D, NTH, ROPE> qr;
     qr.load(tid, seq + q_off + head * D, ld, q0, T - 1, cos_t, sin_t);
     qr.store(tid, Qs, PK);
   }
@@ -274,7 +274,7 @@ __global__ __launch_bounds__(256) void window_attention_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) Om[(t * 32 + fm_mfma32_row(r, lane)) * P + col] = o[t][r];
   __syncthreads();
-  for (int e = tid; e < QB * D; e += 256) {
+  for (int e = tid; e < QB * D; e += NTH) {
     const int qi = e / D, d = e % D;
     const int qg = q0 + qi;
     if (qg >= T) continue;
@@ -882,15 +882,21 @@ int fm_window_attention_rows(const float* qkv, int ld_qkv, int q_offset, int k_o
   if (query_start < 0 || query_start > length) return FM_BAD_ARGUMENT;
   if (batch == 0 || length == query_start) return FM_OK;
   dim3 grid((length - query_start + QB - 1) / QB, heads, batch);
-#define FM_ATT(DV)                                                                         \
-  if (cos_table)                                                                           \
-    hipLaunchKernelGGL((window_attention_kernel<DV, true>), grid, dim3(256), 0, stream, qkv, \
-                       ld_qkv, q_offset, k_offset, v_offset, cos_table, sin_table, length,  \
-                       query_start, heads, kv_heads, window, scale, out, ld_out);           \
-  else                                                                                     \
-    hipLaunchKernelGGL((window_attention_kernel<DV, false>), grid, dim3(256), 0, stream,   \
-                       qkv, ld_qkv, q_offset, k_offset, v_offset, cos_table, sin_table,     \
-                       length, query_start, heads, kv_heads, window, scale, out, ld_out)
+  // Eight waves per block (fewer key tiles per wave) while the grid is too
+  // small to fill the GPU; four once blocks are plentiful.
+  const bool eight = (long)grid.x * grid.y * grid.z < 512;
+#define FM_ATT_NW(DV, R, W)                                                                  \
+  hipLaunchKernelGGL((window_attention_kernel<DV, R, W>), grid, dim3(64 * W), 0, stream, qkv, \
+                     ld_qkv, q_offset, k_offset, v_offset, cos_table, sin_table, length,      \
+                     query_start, heads, kv_heads, window, scale, out, ld_out)
+#define FM_ATT(DV)                                  \
+  if (cos_table) {                                  \
+    if (eight) FM_ATT_NW(DV, true, 8);              \
+    else FM_ATT_NW(DV, true, 4);                    \
+  } else {                                          \
+    if (eight) FM_ATT_NW(DV, false, 8);             \
+    else FM_ATT_NW(DV, false, 4);                   \
+  }
   switch (head_dim) {
     case 8: FM_ATT(8); break;
     case 16: FM_ATT(16); break;
@@ -899,6 +905,7 @@ int fm_window_attention_rows(const float* qkv, int ld_qkv, int q_offset, int k_o
     default: return FM_UNSUPPORTED;
   }
 #undef FM_ATT
+#undef FM_ATT_NW
   return (int)hipGetLastError();
 }
 
