@@ -29,8 +29,26 @@ enum FmGemmFlags {
   FM_EPI_RES_SCALE = 32 // y = res + scale[n] * acc
 };
 
-// ELU with alpha = 1 (torch.nn.ELU).
-FM_DEVICE float fm_elu(float x) { return x > 0.0f ? x : expm1f(x); }
+// e^x - 1 for x <= 0, branch-free.  Near zero (x > -1/4) the Taylor series
+// of e^x - 1 through x^8 (truncation < 1e-11, below half an ulp of the
+// result), in Horner form with FMAs; further out e^x - 1 from the hardware
+// exponential, where the result is at least 0.22 in magnitude so the
+// subtraction loses nothing.  Within a few ulp of expm1 over x <= 0.
+FM_DEVICE float fm_expm1_neg(float x) {
+  float p = fmaf(x, 1.0f / 40320.0f, 1.0f / 5040.0f);
+  p = fmaf(x, p, 1.0f / 720.0f);
+  p = fmaf(x, p, 1.0f / 120.0f);
+  p = fmaf(x, p, 1.0f / 24.0f);
+  p = fmaf(x, p, 1.0f / 6.0f);
+  p = fmaf(x, p, 0.5f);
+  p = fmaf(x, p, 1.0f);
+  const float small = x * p;
+  const float large = __expf(x) - 1.0f;
+  return x > -0.25f ? small : large;
+}
+
+// ELU with alpha = 1 (torch.nn.ELU): x for x > 0, e^x - 1 otherwise.
+FM_DEVICE float fm_elu(float x) { return x > 0.0f ? x : fm_expm1_neg(fminf(x, 0.0f)); }
 
 // Exact-erf GELU (torch.nn.functional.gelu, approximate='none').
 FM_DEVICE float fm_gelu(float x) {
@@ -47,3 +65,10 @@ FM_DEVICE floatx16 fm_mfma32(float a, float b, floatx16 c) {
 FM_DEVICE int fm_mfma32_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
 static inline int fm_ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
+
+// Orders this wave's LDS accesses: everything before completes before
+// anything after is issued (the compiler may not move memory ops across).
+FM_DEVICE void wave_lds_fence() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+}

@@ -214,6 +214,143 @@ __global__ __launch_bounds__(NT) void resblock_kernel(const float* __restrict__ 
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// C = 64 residual block as a persistent kernel.  The whole block's weights fit
+// in registers as MFMA B fragments (W1^T [32][192]: 96 per lane; W2^T [64][32]:
+// 32 per lane), loaded once per wave.  Each of the 8 waves then takes 32-row
+// tiles in a grid-stride loop, with no block-level barrier: stage ELU(x) rows
+// t0-2 .. t0+31 in its own LDS slot, k3 conv (96 MFMAs, taps as row-shifted
+// views), hidden = ELU(acc + b1) into LDS, 1x1 conv (32 MFMAs), then the
+// output tile goes back through LDS so the epilogue (bias, raw residual, ELU)
+// runs on float4 runs.  Two waves per SIMD overlap one tile's loads and
+// ELUs with the other's MFMAs.  MFMA k-slots: lane half h at step 4q+e carries
+// k = 96h + 4q + e (k3 conv, k = tap*64 + c_in) or 16h + 4q + e (1x1 conv).
+constexpr int R64_WAVES = 8;
+constexpr int R64_PE = 68;   // pitch of the ELU(x) / output tile rows
+constexpr int R64_PH = 36;   // pitch of the hidden tile rows
+constexpr int R64_SLOT = 34 * R64_PE + 32 * R64_PH;
+
+__global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
+    const float* __restrict__ x, int batch, int L, const float* __restrict__ w1,
+    const float* __restrict__ b1, const float* __restrict__ w2, const float* __restrict__ b2,
+    int elu_out, float* __restrict__ y) {
+  constexpr int C = 64, HC = 32;
+  __shared__ __attribute__((aligned(16))) float smem[R64_WAVES * R64_SLOT];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = lane >> 5, lcol = lane & 31;
+  float* E = smem + wave * R64_SLOT;   // [34][68] ELU(x); later the [32][68] output tile
+  float* H = E + 34 * R64_PE;          // [32][36] hidden
+
+  floatx4 wa[24], wb[2][4];
+#pragma unroll
+  for (int q = 0; q < 24; ++q) wa[q] = *reinterpret_cast<const floatx4*>(w1 + lcol * 192 + 96 * h + 4 * q);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      wb[j][q] = *reinterpret_cast<const floatx4*>(w2 + (j * 32 + lcol) * HC + 16 * h + 4 * q);
+  const float bias1 = b1[lcol];
+
+  const int tpb = (L + 31) / 32;
+  const long tiles = (long)batch * tpb;
+  const long stride = (long)gridDim.x * R64_WAVES;
+  long tile = (long)blockIdx.x * R64_WAVES + wave;
+
+  // x rows t0-2 .. t0+31 of a tile: 544 float4 chunks, 9 per lane (chunk c = lane + 64u).
+  floatx4 xv[9];
+  unsigned xok = 0;
+  auto load_x = [&](long tl) {
+    const int b = (int)(tl / tpb), t0 = (int)(tl % tpb) * 32;
+    const float* xb = x + (long)b * L * C;
+    xok = 0;
+#pragma unroll
+    for (int u = 0; u < 9; ++u) {
+      const int c = lane + 64 * u;
+      const int t = t0 - 2 + c / 16;
+      const bool ok = c < 544 && t >= 0 && t < L;
+      xv[u] = *reinterpret_cast<const floatx4*>(xb + (long)min(max(t, 0), L - 1) * C + (c % 16) * 4);
+      xok |= (unsigned)ok << u;
+    }
+  };
+  for (; tile < tiles; tile += stride) {
+    const int b = (int)(tile / tpb), t0 = (int)(tile % tpb) * 32;
+    load_x(tile);
+    // ELU(x) into the slot (zero outside the sequence: the causal zero padding).
+#pragma unroll
+    for (int u = 0; u < 9; ++u) {
+      const int c = lane + 64 * u;
+      if (c >= 544) continue;
+      floatx4 v = ((xok >> u) & 1) ? xv[u] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      *reinterpret_cast<floatx4*>(E + (c / 16) * R64_PE + (c % 16) * 4) =
+          floatx4{fm_elu(v[0]), fm_elu(v[1]), fm_elu(v[2]), fm_elu(v[3])};
+    }
+    wave_lds_fence();
+
+    // k3 conv: rows = positions, columns = hidden channels.
+    floatx16 acc1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc1[r] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 24; ++q) {
+      const int k0 = 96 * h + 4 * q;
+      const floatx4 a = *reinterpret_cast<const floatx4*>(E + (lcol + k0 / 64) * R64_PE + k0 % 64);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc1 = fm_mfma32(a[e], wa[q][e], acc1);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      H[fm_mfma32_row(r, lane) * R64_PH + lcol] = fm_elu(__fadd_rn(acc1[r], bias1));
+    wave_lds_fence();
+
+    // 1x1 conv: columns = output channels (two 32-wide tiles).
+    floatx16 acc2[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc2[j][r] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const floatx4 a = *reinterpret_cast<const floatx4*>(H + lcol * R64_PH + 16 * h + 4 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc2[j] = fm_mfma32(a[e], wb[j][q][e], acc2[j]);
+    }
+    // Output tile through LDS (the ELU(x) rows are no longer read).
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) E[fm_mfma32_row(r, lane) * R64_PE + j * 32 + lcol] = acc2[j][r];
+    // Raw residual rows t0 .. t0+31 (chunk c = lane + 64u, 8 per lane); the
+    // other wave on this SIMD covers their latency.
+    const float* xb = x + (long)b * L * C;
+    floatx4 rv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int c = lane + 64 * u;
+      rv[u] = *reinterpret_cast<const floatx4*>(xb + (long)min(t0 + c / 16, L - 1) * C + (c % 16) * 4);
+    }
+    wave_lds_fence();
+    float* yb = y + (long)b * L * C;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int c = lane + 64 * u;
+      const int r = c / 16, c4 = (c % 16) * 4;
+      const floatx4 acc = *reinterpret_cast<const floatx4*>(E + r * R64_PE + c4);
+      const floatx4 bb = *reinterpret_cast<const floatx4*>(b2 + c4);
+      floatx4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = __fadd_rn(rv[u][e], __fadd_rn(acc[e], bb[e]));
+        if (elu_out) v[e] = fm_elu(v[e]);
+      }
+      if (t0 + r < L) *reinterpret_cast<floatx4*>(yb + (long)(t0 + r) * C + c4) = v;
+    }
+    wave_lds_fence();  // the slot is rewritten by the next tile
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -234,6 +371,14 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
 #define FM_RB(C, BM, A, B_, C2, D)                                                              \
   hipLaunchKernelGGL((resblock_kernel<C, BM, A, B_, C2, D>), dim3((length + BM - 1) / BM, batch), \
                      dim3(NT), 0, stream, x, length, w1_packed, b1, w2_packed, b2, elu_out, y)
+  if (channels == 64) {
+    // Persistent: one 8-wave block per CU (LDS-bound), waves stride over 32-row tiles.
+    const long tiles = (long)batch * ((length + 31) / 32);
+    const int blocks = (int)std::min<long>((tiles + R64_WAVES - 1) / R64_WAVES, 256);
+    hipLaunchKernelGGL(resblock64_kernel, dim3(blocks), dim3(64 * R64_WAVES), 0, stream, x, batch,
+                       length, w1_packed, b1, w2_packed, b2, elu_out, y);
+    return (int)hipGetLastError();
+  }
   switch (channels) {
     case 64: FM_RB(64, 128, 4, 1, 4, 1); break;
     case 128: FM_RB(128, 64, 2, 2, 2, 2); break;

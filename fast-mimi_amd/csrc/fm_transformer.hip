@@ -129,13 +129,6 @@ struct VTile {
   }
 };
 
-// Orders this wave's LDS accesses: everything before completes before
-// anything after is issued (the compiler may not move memory ops across).
-FM_DEVICE void wave_lds_fence() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_wave_barrier();
-}
-
 // Sliding-window causal attention on FP32 MFMA.
 // Grid: (ceil((T - q_start) / QB), heads, batch), 64 * NW threads.  Queries are
 // rows q_start .. T-1 (earlier rows are cached keys/values only); query q

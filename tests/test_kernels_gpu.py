@@ -445,6 +445,23 @@ def test_apply_rope_in_place(rows, T, H, D):
     assert torch.equal(xd.cpu(), want)  # same rounding steps as the reference's _apply_rope
 
 
+def test_elu_accuracy_dense(ws):
+    """ELU through an identity 1x1 conv (EPI_ELU) against float64 expm1 over
+    a dense grid of x <= 0, plus x > 0 passthrough: within 4 ulp."""
+    x = torch.cat([-torch.logspace(-8, 2, 200_000, dtype=torch.float64),
+                   torch.linspace(-1, 0, 100_001, dtype=torch.float64),
+                   torch.logspace(-8, 2, 1000, dtype=torch.float64)]).float()
+    n = x.numel() // 4 * 4
+    x = x[:n]
+    w = torch.eye(4).view(4, 4, 1)
+    y = run_conv(x.view(1, n // 4, 4).transpose(1, 2), w, None, 1, 0, nat.EPI_ELU, ws)
+    got = y.transpose(1, 2).reshape(-1).double()
+    want = torch.where(x > 0, x.double(), torch.expm1(x.double()))
+    ulp = torch.nextafter(want.float().abs(), torch.tensor(float("inf"))).double() - want.abs().float().double()
+    err = ((got - want).abs() / ulp.clamp(min=1e-45)).max().item()
+    assert err <= 4.0, f"max error {err:.2f} ulp"
+
+
 def prepare_codebooks(embed_sum, usage):
     n, e, d = embed_sum.shape
     emb = torch.empty(n, e, d, device=DEV)
