@@ -52,6 +52,37 @@ FM_DEVICE void resolve(const float* val, const int* idx, int chunks, long M, lon
   }
 }
 
+// Argmin over the chunk partials of row m, spread over the 8 lanes pt = 0..7
+// of an aligned lane group: lane pt takes chunks pt, pt + 8, ... (at most
+// kMaxChunks / 8), all loads issued before the first compare, then the 8
+// lanes are shuffle-reduced.  ``better`` is a total order, so the result is
+// the lowest-index minimum whatever the reduction order.
+FM_DEVICE void resolve8(const float* val, const int* idx, int chunks, long M, long m, int pt,
+                        float& bv, int& bi) {
+  constexpr int PER = kMaxChunks / 8;
+  float v[PER];
+  int ix[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int c = pt + 8 * u;
+    const int cc = min(c, chunks - 1);
+    v[u] = val[(long)cc * M + m];
+    ix[u] = idx[(long)cc * M + m];
+    if (c >= chunks) v[u] = INFINITY, ix[u] = 0x7fffffff;
+  }
+  bv = v[0];
+  bi = ix[0];
+#pragma unroll
+  for (int u = 1; u < PER; ++u)
+    if (better(v[u], ix[u], bv, bi)) bv = v[u], bi = ix[u];
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (better(ov, oi, bv, bi)) bv = ov, bi = oi;
+  }
+}
+
 constexpr int NT = 128;  // entries per sub-tile (4 waves x 32)
 constexpr int KSL = 32;  // codebook dims per staged slice
 constexpr int PB = NT + 4;
@@ -250,6 +281,24 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a, const fl
   const int e_begin = chunk * a.chunk_entries;
   const int e_end = min(a.entries, e_begin + a.chunk_entries);
 
+  // The first codebook piece does not depend on the previous step: its
+  // loads go out before the prologue's dependent chain.
+  const int nsub = (e_end - e_begin + 31) / 32;
+  const int my_sub = (nsub - g + EG - 1) / EG;  // sub-tiles g, g+EG, ...
+  const int items = (KP == 1) ? my_sub * NPC : NPC;
+  const int kbase = p * KW;
+  floatx4 cur[8], nxt[8];
+  auto load_piece = [&](floatx4* dst, int item) {
+    const int st = g + EG * ((KP == 1) ? item / NPC : 0);
+    const int pc = item % NPC;
+    const int entry = min(e_begin + 32 * st + col, a.entries - 1);
+    const float* src = embed + (long)entry * DIM + kbase + 64 * pc + 32 * h;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dst[j] = *reinterpret_cast<const floatx4*>(src + 4 * j);
+  };
+  const bool has_work = KP == 1 ? items > 0 : g < nsub;
+  if (has_work) load_piece(cur, 0);
+
   // ---- prologue: row r = tid / 8, lane part pt = tid % 8.
   {
     const int r = tid >> 3, pt = tid & 7;
@@ -258,19 +307,9 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a, const fl
     const bool valid = m < a.M;
     int code = 0;
     if (a.prev_embed) {
-      float bv = INFINITY;
-      int bi = 0x7fffffff;
-      for (int c = pt; c < a.chunks; c += 8) {
-        const float v = a.prev_val[(long)c * a.M + mc];
-        const int i = a.prev_idx[(long)c * a.M + mc];
-        if (better(v, i, bv, bi)) bv = v, bi = i;
-      }
-#pragma unroll
-      for (int o = 1; o < 8; o <<= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (better(ov, oi, bv, bi)) bv = ov, bi = oi;
-      }
+      float bv;
+      int bi;
+      resolve8(a.prev_val, a.prev_idx, a.chunks, a.M, mc, pt, bv, bi);
       code = bi;
       if (chunk == 0 && pt == 0 && valid) {
         const long b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
@@ -310,24 +349,9 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a, const fl
   const float xq = xnS[col];
   float best_v = INFINITY;
   int best_i = 0x7fffffff;
-  const int nsub = (e_end - e_begin + 31) / 32;
-  const int my_sub = (nsub - g + EG - 1) / EG;  // sub-tiles g, g+EG, ...
-  const int items = (KP == 1) ? my_sub * NPC : NPC;
-  const int kbase = p * KW;
-  floatx4 cur[8], nxt[8];
-  auto load_piece = [&](floatx4* dst, int item) {
-    const int st = g + EG * ((KP == 1) ? item / NPC : 0);
-    const int pc = item % NPC;
-    const int entry = min(e_begin + 32 * st + col, a.entries - 1);
-    const float* src = embed + (long)entry * DIM + kbase + 64 * pc + 32 * h;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) dst[j] = *reinterpret_cast<const floatx4*>(src + 4 * j);
-  };
   floatx16 acc;
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-  const bool has_work = KP == 1 ? items > 0 : g < nsub;
-  if (has_work) load_piece(cur, 0);
   for (int it = 0; it < (has_work ? items : 0); ++it) {
     if (it + 1 < items) load_piece(nxt, it + 1);
     const int pc = it % NPC;
@@ -399,14 +423,16 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a, const fl
   }
 }
 
+// Resolves the last step: 8 lanes per row (32 rows per block).
 __global__ __launch_bounds__(256) void rvq_finalize_kernel(const float* val, const int* idx,
                                                            int chunks, int M, int64_t* codes,
                                                            int rows_per_batch, int batch_stride) {
-  const long m = (long)blockIdx.x * 256 + threadIdx.x;
-  if (m >= M) return;
+  const long m = (long)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int pt = threadIdx.x & 7;
   float bv;
   int bi;
-  resolve(val, idx, chunks, M, m, bv, bi);
+  resolve8(val, idx, chunks, M, min(m, (long)M - 1), pt, bv, bi);
+  if (m >= M || pt != 0) return;
   const long b = m / rows_per_batch, t = m - b * rows_per_batch;
   codes[b * batch_stride + t] = bi;
 }
@@ -571,7 +597,7 @@ int fm_rvq_encode(const float* x, int ld_x, int rows, int rows_per_batch, int di
     if (e != hipSuccess) return (int)e;
   }
   const int last = (count - 1) & 1;
-  hipLaunchKernelGGL(rvq_finalize_kernel, dim3((rows + 255) / 256), dim3(256), 0, stream,
+  hipLaunchKernelGGL(rvq_finalize_kernel, dim3((rows + 31) / 32), dim3(256), 0, stream,
                      val[last], idx[last], chunks, rows,
                      codes + (size_t)(count - 1) * rows_per_batch, rows_per_batch, batch_stride);
   return (int)hipGetLastError();

@@ -366,9 +366,11 @@ class MimiModel:
         """Encode→decode round trip (``model.py:3452-3538``); with ``audio_codes``
         given, decode only.  The mask crops the decoded audio to its length."""
         return_dict = self.config.return_dict if return_dict is None else return_dict
-        mask = torch.ones_like(input_values, dtype=torch.bool) if padding_mask is None else padding_mask
+        mask = padding_mask
         if audio_codes is not None or encoder_past_key_values is not None or decoder_past_key_values is not None:
             # Decode-only, or stateful: the encode/decode entry points, eagerly where a cache is given.
+            if mask is None:
+                mask = torch.ones_like(input_values, dtype=torch.bool)
             if audio_codes is None:
                 enc = self.encode(input_values, mask, num_quantizers, encoder_past_key_values,
                                   return_dict=True)
@@ -381,7 +383,7 @@ class MimiModel:
             self._check_audio(input_values)
             rt = self.runtime()
             audio_in = self._on_device(input_values, torch.float32)
-            out_len = mask.shape[-1]
+            out_len = input_values.shape[-1] if mask is None else mask.shape[-1]
             self._prepare_lengths(audio_in.shape[-1])
 
             def roundtrip(a):
