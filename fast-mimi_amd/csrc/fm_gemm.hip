@@ -22,8 +22,11 @@
 //   128x32 (4x1 of 32x32);
 //   32x64 with the four waves splitting K (summed through LDS in wave order)
 //   when the large tiles cannot fill the GPU, plus global K-splits summed in
-//   split order by a second kernel for very long K.  All sums are in a fixed
-//   order, so results are deterministic.
+//   split order by a second kernel for very long K.
+// Long-K contractions with few rows (the 12.5-25 Hz end of the SEANet stacks)
+// take 64x64 / 32x32 tiles of 16x16x4 MFMA chains with BK = 128 (gemm_mid),
+// or 256x64 tiles, split along K to a few hundred blocks.  All sums are in a
+// fixed order, so results are deterministic.
 // Blocks are renumbered so consecutive tiles of one row band land on one XCD
 // (dispatch assigns block i to XCD i % 8), keeping the band's A rows in that
 // XCD's L2.
@@ -493,6 +496,185 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Mid-size kernel for few-row / long-K contractions: BM x BN in {32, 64}^2,
+// 4 waves, each owning a 32x32 output tile as 2x2 independent 16x16x4 FP32
+// MFMA chains; the waves form (BM/32) x (BN/32) x WK groups, and with WK > 1
+// the groups split every k-tile and their tiles are summed through LDS in
+// group order.  k-tile BK = 128 staged in one LDS stage (row pitch BK + 4),
+// refilled from a one-k-tile register prefetch, so each barrier pair
+// brackets 128 / WK MFMAs per wave.  Lane (g = l/16, i = l%16) carries k =
+// 32g + 4t + e of the k-tile at MFMA step 4t+e: 16-byte LDS reads.
+FM_DEVICE floatx4 fm_mfma16x4(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <int BM, int BN, int WK>
+__global__ __launch_bounds__(256) void gemm_mid_kernel(GemmArgs p) {
+  constexpr int NTH = 256, BK = 128, P = BK + 4, CPR = BK / 4;
+  constexpr int WMN = BN / 32;                   // waves along N within a k-group
+  static_assert((BM / 32) * (BN / 32) * WK == 4, "4 waves");
+  constexpr int RPP = NTH / CPR;                 // rows per load pass (8)
+  constexpr int APT = BM / RPP, BPT = BN / RPP;
+  constexpr int KSL = BK / WK;                   // k per group per k-tile
+  constexpr int TSTEPS = KSL / 16;               // float4 steps of the group's slice per lane group
+  constexpr int STAGE = (BM + BN) * P;
+  constexpr int RED = (WK - 1) * BM * (BN + 4);
+  __shared__ __attribute__((aligned(16))) float msm[STAGE > RED ? STAGE : RED];
+  float* As = msm;
+  float* Bs = msm + BM * P;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int grp = wave / ((BM / 32) * WMN);
+  const int wv = wave % ((BM / 32) * WMN);
+  const int wm0 = (wv / WMN) * 32, wn0 = (wv % WMN) * 32;
+  const int g = lane >> 4, li = lane & 15;
+  const long M = (long)p.batch * p.rows;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int tile = tile_index();
+  const long m0 = (long)(tile / tiles_n) * BM;
+  const int n0 = (tile % tiles_n) * BN;
+  const int k_begin = blockIdx.y * p.k_split;
+  const int k_end = min(p.K, k_begin + p.k_split);
+  const bool replicate = p.flags & FM_REPLICATE;
+  const int ck = (tid % CPR) * 4;
+  const int rrow = tid / CPR;
+
+  long a_org[APT];
+  int a_p0[APT];
+#pragma unroll
+  for (int i = 0; i < APT; ++i) {
+    const long m = min(m0 + rrow + i * RPP, M - 1);
+    const int b = (int)(m / p.rows);
+    const int t = (int)(m - (long)b * p.rows);
+    a_p0[i] = (m0 + rrow + i * RPP < M) ? t * p.rs - p.padL : INT_MIN / 2;
+    a_org[i] = (long)b * p.L_in * p.C_in;
+  }
+  floatx4 ra[APT], rb[BPT];
+  unsigned amask = 0, bmask = 0;
+  auto load = [&](int k0) {
+    const int kg = k0 + ck;
+    const bool kok = kg < k_end;
+    const int kc = min(kg, p.K - 4);
+    const int tap = kc / p.C_in;
+    const int cin = kc - tap * p.C_in;
+    amask = bmask = 0;
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+      const int pos = a_p0[i] + tap;
+      const bool ok = kok && (replicate ? a_p0[i] > INT_MIN / 2 : (pos >= 0 && pos < p.L_in));
+      const int pc = min(max(pos, 0), p.L_in - 1);
+      ra[i] = *reinterpret_cast<const floatx4*>(p.x + a_org[i] + (long)pc * p.C_in + cin);
+      amask |= (unsigned)ok << i;
+    }
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      const int n = n0 + rrow + i * RPP;
+      const bool ok = kok && n < p.N;
+      rb[i] = *reinterpret_cast<const floatx4*>(p.w + (long)min(n, p.N - 1) * p.K + kc);
+      bmask |= (unsigned)ok << i;
+    }
+  };
+  const bool elu_in = p.flags & FM_ELU_IN;
+
+  floatx4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int kbase = grp * KSL;  // this group's k offset within a k-tile
+  if (k_begin < k_end) load(k_begin);
+  for (int k0 = k_begin; k0 < k_end; k0 += BK) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+      floatx4 v = ((amask >> i) & 1) ? ra[i] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (elu_in) v = floatx4{fm_elu(v.x), fm_elu(v.y), fm_elu(v.z), fm_elu(v.w)};
+      *reinterpret_cast<floatx4*>(As + (rrow + i * RPP) * P + ck) = v;
+    }
+#pragma unroll
+    for (int i = 0; i < BPT; ++i)
+      *reinterpret_cast<floatx4*>(Bs + (rrow + i * RPP) * P + ck) =
+          ((bmask >> i) & 1) ? rb[i] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    __syncthreads();
+    if (k0 + BK < k_end) load(k0 + BK);
+#pragma unroll
+    for (int t = 0; t < TSTEPS; ++t) {
+      const int kk = kbase + (KSL / 4) * g + 4 * t;
+      floatx4 a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const floatx4*>(As + (wm0 + 16 * i + li) * P + kk);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const floatx4*>(Bs + (wn0 + 16 * j + li) * P + kk);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[i][j] = fm_mfma16x4(a[i][e], b[j][e], acc[i][j]);
+    }
+  }
+
+  if constexpr (WK > 1) {
+    constexpr int PRD = BN + 4;
+    __syncthreads();
+    if (grp > 0) {
+      float* red = msm + (grp - 1) * BM * PRD;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) red[(wm0 + 16 * i + 4 * g + r) * PRD + wn0 + 16 * j + li] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (grp > 0) return;
+#pragma unroll
+    for (int q = 1; q < WK; ++q) {
+      const float* red = msm + (q - 1) * BM * PRD;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[i][j][r] = __fadd_rn(acc[i][j][r], red[(wm0 + 16 * i + 4 * g + r) * PRD + wn0 + 16 * j + li]);
+    }
+  }
+
+  const bool crop = p.y_rows != p.rows;
+  const bool has_res = p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE);
+  float* part = p.partial ? p.partial + (long)blockIdx.y * M * p.N : nullptr;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + wn0 + 16 * j + li;
+    const int nc = min(n, p.N - 1);
+    const float bias = p.bias ? p.bias[nc % p.bias_len] : 0.0f;
+    const float scale = (p.flags & FM_EPI_RES_SCALE) ? p.scale[nc] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const long m = m0 + wm0 + 16 * i + 4 * g + r;
+        if (m >= M || n >= p.N) continue;
+        if (part) {
+          part[m * p.N + n] = acc[i][j][r];
+          continue;
+        }
+        const float res = has_res ? p.res[m * p.N + n] : 0.0f;
+        const float v = epilogue_v(acc[i][j][r], bias, res, scale, p.flags);
+        if (!crop) {
+          p.y[m * p.N + n] = v;
+        } else {
+          const int b = (int)(m / p.rows);
+          const int t = (int)(m - (long)b * p.rows);
+          if (t < p.y_rows) p.y[((long)b * p.y_rows + t) * p.N + n] = v;
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Generic kernel: 64x64 tiles, one output element pair per thread per step,
 // scalar loads.  Used only when C_in or K is not a multiple of 4.
 __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
@@ -669,15 +851,26 @@ struct TileCfg {
 };
 // Candidates, largest first: the first whose tile count reaches its `fill`
 // wins.  The 256x64 tile (two 512-thread blocks per CU) measured faster than
-// every other shape down to ~190 tiles (not at 128 with long K), so it is taken
+// every other shape from ~190 tiles (not at 128 with long K), so it is taken
 // from 160 tiles.
 constexpr TileCfg kTiles[] = {{256, 64, 1, 32, 6, 160},  {128, 128, 1, 64, 0, 224},
                               {128, 64, 1, 64, 1, 224},  {128, 32, 1, 64, 2, 224},
                               {32, 64, 4, 32, 3, 0}};
 constexpr TileCfg kSplitTile = kTiles[4];
+constexpr TileCfg kBigTile = kTiles[0];
+constexpr TileCfg kMid64 = {64, 64, 1, 128, 7, 0};
+constexpr TileCfg kMid32 = {32, 32, 4, 128, 8, 0};
 
 long tile_count(long M, int N, const TileCfg& t) {
   return ((M + t.BM - 1) / t.BM) * ((N + t.BN - 1) / t.BN);
+}
+
+// Smallest power-of-two K-split (<= cap) that brings tiles * splits to
+// `blocks`, keeping at least `min_k` reduction elements per split.
+int pick_splits(long tiles, int K, long blocks, int cap, int min_k) {
+  int s = 1;
+  while (s < cap && tiles * s < blocks && K / (2 * s) >= min_k) s *= 2;
+  return s;
 }
 
 int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s) {
@@ -694,26 +887,41 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
   const bool fast = (p.C_in % 4 == 0) && (p.K % 4 == 0);
   TileCfg cfg = kSplitTile;
   long tiles = 0;
+  int splits = 1;
+  const bool big_ok = p.N % 4 == 0 && !(p.bias && p.bias_len % 4);
+  const long big_tiles = tile_count(M, p.N, kBigTile);
   if (!fast) {
     cfg = TileCfg{64, 64, 1, 16, -1, 0};
     tiles = tile_count(M, p.N, cfg);
+  } else if (p.K >= 1024 && big_tiles < 384 && M >= 1024 && big_ok && workspace) {
+    // Long K, a few hundred rows-bands of work: 256x64 tiles split along K
+    // to ~512 blocks (two per CU).
+    cfg = kBigTile;
+    tiles = big_tiles;
+    splits = pick_splits(tiles, p.K, 512, 8, 128);
+  } else if (p.K >= 1024 && M < 1024 && workspace) {
+    // Few rows, long K: 64x64 (or, up to 128 rows, 32x32 with the K split
+    // inside the block) 16x16-MFMA tiles split along K to ~384 blocks.
+    cfg = M <= 128 ? kMid32 : kMid64;
+    tiles = tile_count(M, p.N, cfg);
+    splits = pick_splits(tiles, p.K, 384, 16, 384);
   } else {
     // Largest tile that still fills the GPU; tiles more than 2x wider than
     // the output are skipped (the narrowest fallback is always eligible).
     for (const TileCfg& t : kTiles) {
       if (t.WK == 1 && t.BN > 32 && t.BN / 2 >= p.N) continue;
       // The 256-row tile's float4 epilogue needs 4-aligned rows and bias periods.
-      if (t.id == 6 && (p.N % 4 || (p.bias && p.bias_len % 4))) continue;
+      if (t.id == 6 && !big_ok) continue;
       cfg = t;
       tiles = tile_count(M, p.N, t);
       if (tiles >= t.fill) break;
     }
+    // Global K-split for long K when even the K-split tile leaves CUs idle.
+    const int kchunks = (p.K + KT - 1) / KT;
+    if (cfg.WK > 1 && tiles < 384 && kchunks >= 32 && workspace)
+      splits = (int)std::min<long>((512 + tiles - 1) / tiles, kchunks / 16);
   }
-  // Global K-split for long K when even the K-split tile leaves CUs idle.
-  const int kchunks = (p.K + KT - 1) / KT;
-  int splits = 1;
-  if (cfg.WK > 1 && tiles < 384 && kchunks >= 32 && workspace) {
-    splits = (int)std::min<long>((512 + tiles - 1) / tiles, kchunks / 16);
+  if (splits > 1) {
     const size_t per = (size_t)M * p.N * sizeof(float);
     while (splits > 1 && per * splits > workspace_bytes) --splits;
     splits = std::max(splits, 1);
@@ -732,6 +940,8 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     case 2: hipLaunchKernelGGL((gemm_fast_kernel<128, 32, 4, 1, 1, 64>), grid, dim3(NTHREADS), 0, s, p); break;
     case 3: hipLaunchKernelGGL((gemm_fast_kernel<32, 64, 1, 1, 4, 32>), grid, dim3(NTHREADS), 0, s, p); break;
     case 6: hipLaunchKernelGGL((gemm_big_kernel<64, 4, 2>), grid, dim3(512), 0, s, p); break;
+    case 7: hipLaunchKernelGGL((gemm_mid_kernel<64, 64, 1>), grid, dim3(NTHREADS), 0, s, p); break;
+    case 8: hipLaunchKernelGGL((gemm_mid_kernel<32, 32, 4>), grid, dim3(NTHREADS), 0, s, p); break;
     default: hipLaunchKernelGGL(gemm_generic_kernel, grid, dim3(256), 0, s, p); break;
   }
   hipError_t e = hipGetLastError();

@@ -187,18 +187,11 @@ class MimiRuntime:
         # Optional per-op timing: a list of (tag, start_event, end_event).
         self.profile: list | None = None
         self._tag = ""
-        self._side: torch.cuda.Stream | None = None
         torch.cuda.synchronize(device)
 
     # ------------------------------------------------------------------ ops
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
-
-    def _side_stream(self) -> torch.cuda.Stream:
-        """A second stream (default priority) for independent work."""
-        if self._side is None:
-            self._side = torch.cuda.Stream(self.device)
-        return self._side
 
     def _call(self, name: str, *args) -> None:
         if self.profile is None:
@@ -488,22 +481,16 @@ class MimiRuntime:
         n_sem = cfg.num_semantic_quantizers
         branches = [(0, 0, n_sem), (vq, n_sem, nq - n_sem)]
         branches = [b for b in branches if b[2] > 0]
-        # The semantic and acoustic branches are independent chains: the
-        # first runs on a side stream (its own workspace) beside the second.
-        main = torch.cuda.current_stream(self.device)
-        side = self._side_stream()
-        side.wait_stream(main)
-        for bi, (col, first, count) in enumerate(branches):
-            stream = side if bi == 0 and len(branches) > 1 else main
-            ws = torch.empty((ws_bytes + 3) // 4, device=self.device)
-            with torch.cuda.stream(stream):
-                self._call("fm_rvq_encode", proj.data_ptr() + col * 4, 2 * vq, M, T, vq,
-                           cfg.codebook_size, count, self.embeds[first].data_ptr(),
-                           self.embeds_t[first].data_ptr(), self.norms[first].data_ptr(),
-                           codes.data_ptr() + first * T * 8, nq * T, ws.data_ptr(), ws_bytes,
-                           stream.cuda_stream)
-            ws.record_stream(stream)
-        main.wait_stream(side)
+        # The two branches run back to back on one stream: forking the
+        # semantic chain onto a second stream measured slower in the captured
+        # graph (cross-queue waits cost more than the overlap gains).
+        ws = torch.empty((ws_bytes + 3) // 4, device=self.device)
+        s = self._stream()
+        for col, first, count in branches:
+            self._call("fm_rvq_encode", proj.data_ptr() + col * 4, 2 * vq, M, T, vq,
+                       cfg.codebook_size, count, self.embeds[first].data_ptr(),
+                       self.embeds_t[first].data_ptr(), self.norms[first].data_ptr(),
+                       codes.data_ptr() + first * T * 8, nq * T, ws.data_ptr(), ws_bytes, s)
         return codes
 
     def decode(self, codes: torch.Tensor, out_length: int | None = None, kv_cache=None) -> torch.Tensor:

@@ -80,6 +80,11 @@ CONV_CASES = [
     (1, 64, 128, 8, 4, 240000),    # 256x128 tiles
     (1, 64, 64, 3, 1, 60000),      # 256x64 tiles
     (2, 128, 256, 10, 5, 300000),  # 256x256 tiles, batch seam inside a tile
+    (1, 256, 512, 12, 6, 12000),   # 256x64 tiles split along K (M = 2000, K = 3072)
+    (1, 512, 1024, 16, 8, 2000),   # 64x64 16x16-MFMA tiles split along K (M = 250)
+    (2, 512, 256, 3, 1, 300),      # 64x64 16x16-MFMA tiles, batch seam inside a tile
+    (1, 512, 512, 4, 2, 250),      # 32x32 tiles, K split inside the block and across blocks
+    (3, 1024, 96, 2, 1, 70),       # 32x32 tiles, partial column tile
 ]
 
 
@@ -120,6 +125,28 @@ def test_conv1d_fused_resblock_epilogues(ws):
     y = run_conv(h.contiguous(), w2, b2, 1, "constant", nat.EPI_RES_ADD | nat.EPI_ELU, ws, residual_ncl=x)
     want = F.elu(xd + causal_conv1d(want_h, w2.double(), b2.double()))
     close(y, want, rel=5e-5)
+
+
+@pytest.mark.parametrize("B,C,L", [(1, 512, 2000), (1, 512, 250), (2, 512, 61)])
+def test_long_k_epilogues(B, C, L, ws):
+    """ELU-on-load / ELU / residual epilogues and replicate padding on the
+    long-K paths (split 256x64 tiles at 2000 rows, 16x16-MFMA tiles below)."""
+    g = torch.Generator().manual_seed(B * C + L)
+    x = torch.randn(B, C, L, generator=g)
+    w1 = torch.randn(C // 2, C, 3, generator=g) / math.sqrt(3 * C)
+    b1 = torch.randn(C // 2, generator=g) * 0.1
+    w2 = torch.randn(C, C // 2, 3, generator=g) / math.sqrt(1.5 * C)
+    b2 = torch.randn(C, generator=g) * 0.1
+    xd = x.double()
+    h = run_conv(x, w1, b1, 1, "constant", nat.ELU_IN | nat.EPI_ELU, ws)
+    want_h = F.elu(causal_conv1d(F.elu(xd), w1.double(), b1.double()))
+    close(h, want_h)
+    y = run_conv(h.contiguous(), w2, b2, 1, "constant", nat.EPI_RES_ADD | nat.EPI_ELU, ws,
+                 residual_ncl=x)
+    close(y, F.elu(xd + causal_conv1d(want_h, w2.double(), b2.double())), rel=5e-5)
+    wr = torch.randn(C, C, 4, generator=g) / math.sqrt(4 * C)
+    got = run_conv(x, wr, None, 2, "replicate", 0, ws)
+    close(got, causal_conv1d(xd, wr.double(), None, 2, pad_mode="replicate"))
 
 
 @pytest.mark.parametrize("B,C,L", [(1, 64, 1000), (2, 64, 129), (1, 128, 777), (3, 128, 1),
