@@ -461,29 +461,43 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
       for (int r = 0; r < 16; ++r)
         smem[(wm0 + i * 32 + fm_mfma32_row(r, lane)) * PC + wn0 + j * 32 + lcol] = acc[i][j][r];
   __syncthreads();
+  // A thread's runs share one column group (NTH is a multiple of BN / 4), so
+  // bias and scale load once; the LDS reads and residual loads of all runs
+  // are issued before the first store.
   const bool crop = p.y_rows != p.rows;
   const bool has_res = p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE);
   float* part = p.partial ? p.partial + (long)blockIdx.y * M * p.N : nullptr;
-  constexpr int RUNS = BM * BN / 4;
-#pragma unroll 2
-  for (int u = tid; u < RUNS; u += NTH) {
-    const int r = u / (BN / 4), c = (u % (BN / 4)) * 4;
-    const long m = m0 + r;
-    const int n = n0 + c;
-    if (m >= M || n >= p.N) continue;
-    floatx4 v = *reinterpret_cast<const floatx4*>(smem + r * PC + c);
+  constexpr int CG = BN / 4, RSTEP = NTH / CG, NRUN = BM / RSTEP;
+  static_assert(NTH % CG == 0 && BM % RSTEP == 0, "epilogue runs");
+  const int c = (tid % CG) * 4, r0 = tid / CG;
+  const int n = n0 + c;
+  const bool n_ok = n < p.N;
+  const int ncl = n_ok ? n : 0;
+  const floatx4 bias = (p.bias && !part) ? *reinterpret_cast<const floatx4*>(p.bias + ncl % p.bias_len)
+                                         : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  const floatx4 scale = ((p.flags & FM_EPI_RES_SCALE) && !part)
+                            ? *reinterpret_cast<const floatx4*>(p.scale + ncl)
+                            : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  floatx4 v[NRUN], res[NRUN];
+#pragma unroll
+  for (int u = 0; u < NRUN; ++u) {
+    const int r = r0 + u * RSTEP;
+    const long m = min(m0 + r, M - 1);
+    v[u] = *reinterpret_cast<const floatx4*>(smem + r * PC + c);
+    res[u] = (has_res && !part) ? *reinterpret_cast<const floatx4*>(p.res + m * p.N + ncl)
+                                : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+#pragma unroll
+  for (int u = 0; u < NRUN; ++u) {
+    const long m = m0 + r0 + u * RSTEP;
+    if (m >= M || !n_ok) continue;
     if (part) {
-      *reinterpret_cast<floatx4*>(part + m * p.N + n) = v;
+      *reinterpret_cast<floatx4*>(part + m * p.N + n) = v[u];
       continue;
     }
-    const floatx4 bias = p.bias ? *reinterpret_cast<const floatx4*>(p.bias + n % p.bias_len)
-                                : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    const floatx4 res = has_res ? *reinterpret_cast<const floatx4*>(p.res + m * p.N + n)
-                                : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    const floatx4 scale = (p.flags & FM_EPI_RES_SCALE) ? *reinterpret_cast<const floatx4*>(p.scale + n)
-                                                       : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    floatx4 o = v[u];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = epilogue_v(v[e], bias[e], res[e], scale[e], p.flags);
+    for (int e = 0; e < 4; ++e) o[e] = epilogue_v(o[e], bias[e], res[u][e], scale[e], p.flags);
     long dst = m * p.N + n;
     if (crop) {
       const int b = (int)(m / p.rows);
@@ -491,7 +505,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
       if (t >= p.y_rows) continue;
       dst = ((long)b * p.y_rows + t) * p.N + n;
     }
-    *reinterpret_cast<floatx4*>(p.y + dst) = v;
+    *reinterpret_cast<floatx4*>(p.y + dst) = o;
   }
 }
 

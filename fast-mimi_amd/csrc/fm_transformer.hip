@@ -38,6 +38,10 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float* __restrict
     yr[c] = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(xr[c], mean), rstd), gamma[c]), beta[c]);
 }
 
+FM_DEVICE floatx4 fm_mfma16(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 constexpr int QB = 32;  // queries per block (one MFMA column tile)
 constexpr int KB = 32;  // keys per MFMA row tile
 
@@ -56,9 +60,9 @@ FM_DEVICE void rope_pair(floatx4& lo, floatx4& hi, const floatx4& c, const float
 // Rows t0 .. t0+31 of one head of Q or K (D dims, row pitch ld), held as
 // float4 pairs (dims 4c.. and 4c + D/2..) so that RoPE's partners sit in the
 // same lane; rows past t_last read as zero.  NTH threads share the tile.
-template <int D, int NTH, bool ROPE>
+template <int D, int NTH, bool ROPE, int ROWS = QB>
 struct RowTile {
-  static constexpr int HALF = D / 2, PAIRS = QB * D / 8;
+  static constexpr int HALF = D / 2, PAIRS = ROWS * D / 8;
   static constexpr int N = (PAIRS + NTH - 1) / NTH;
   floatx4 lo[N], hi[N], c[N], s[N];
   unsigned okm;  // rows inside the sequence; zeroing waits for the store (see VTile)
@@ -160,6 +164,8 @@ __global__ __launch_bounds__(64 * NW) void window_attention_kernel(
   __shared__ __attribute__((aligned(16))) float Qs[QB * PK];
   __shared__ float Mm[NW][QB];
   __shared__ float Lm[NW][QB];
+  __shared__ float Fm[NW][QB];
+  __shared__ float Dm[QB];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, col = lane & 31;
@@ -214,15 +220,21 @@ __global__ __launch_bounds__(64 * NW) void window_attention_kernel(
       vr.load(lane, vcol, ld, k0 + NW * KB, k_hi);
     }
 
-    floatx16 s;
+    // Two interleaved MFMA chains (even / odd 4-dim groups), summed after.
+    floatx16 s, s2;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+    for (int r = 0; r < 16; ++r) s[r] = 0.0f, s2[r] = 0.0f;
 #pragma unroll
     for (int j = 0; j < D / 8; ++j) {
       const floatx4 a4 = *reinterpret_cast<const floatx4*>(Ks + col * PK + (D / 2) * h + 4 * j);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) s = fm_mfma32(a4[e], qv[4 * j + e], s);
+      for (int e = 0; e < 4; ++e) {
+        if (j & 1) s2 = fm_mfma32(a4[e], qv[4 * j + e], s2);
+        else s = fm_mfma32(a4[e], qv[4 * j + e], s);
+      }
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] += s2[r];
 
     float cmax = -INFINITY;
 #pragma unroll
@@ -267,22 +279,207 @@ __global__ __launch_bounds__(64 * NW) void window_attention_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) Om[(t * 32 + fm_mfma32_row(r, lane)) * P + col] = o[t][r];
   __syncthreads();
+  // Per query: M = max_w m_w, the factors f_w = exp(m_w - M) (0 for a wave
+  // that saw no key) and den = sum_w l_w f_w, once; then each output element
+  // is sum_w O_w f_w / den.
+  if (tid < QB) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, Mm[w][tid]);
+    float den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float f = (Mm[w][tid] == -INFINITY) ? 0.0f : expf(Mm[w][tid] - M);
+      Fm[w][tid] = f;
+      if (Mm[w][tid] != -INFINITY) den += Lm[w][tid] * f;
+    }
+    Dm[tid] = den;
+  }
+  __syncthreads();
   for (int e = tid; e < QB * D; e += NTH) {
     const int qi = e / D, d = e % D;
     const int qg = q0 + qi;
     if (qg >= T) continue;
+    float num = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+      if (Mm[w][qi] != -INFINITY) num += stage[w][d * P + qi] * Fm[w][qi];
+    out[(b * (long)(T - q_start) + qg - q_start) * ld_out + head * D + d] = num / Dm[qi];
+  }
+}
+
+
+// Sliding-window causal attention for head_dim 64 on 16x16x4 FP32 MFMA.
+// Block = 16 queries of one head (twice the blocks of the 32-query kernel, so
+// short sequences spread over more CUs; the per-block MFMA work is what bounds
+// this kernel at a few hundred frames).  The key range is cut into 32-key
+// tiles taken round-robin by the NW waves, each with its own LDS slot and the
+// next tile's K/V prefetched in registers.  Per tile a wave forms S^T = K Q^T
+// as two 16-key row tiles (lane (g, i) = (l / 16, l % 16) owns query i and
+// keys 4g..4g+3 of each; k-slot g at step 4t+e carries dim 16g + 4t + e, so K
+// comes from 16-byte LDS reads and Q^T from registers), four MFMA chains
+// (row tile x even/odd t).  After the window mask and an online softmax per
+// query, O^T += V^T P^T runs with P^T straight from the S^T registers: step r
+// of row tile kt uses key 16kt + 4g + r in k-slot g, exactly the key that
+// lane holds in accumulator slot r.  O^T is four 16-dim row tiles (four
+// chains).  The waves' (max, sum, O) are merged through LDS with the factors
+// exp(m_w - M) computed once per query.  ROPE: Q and K rotate while staging.
+template <bool ROPE, int NW>
+__global__ __launch_bounds__(64 * NW) void window_attention16_kernel(
+    const float* __restrict__ qkv, int ld, int q_off, int k_off, int v_off,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int T, int q_start,
+    int heads, int kv_heads, int window, float scale, float* __restrict__ out, int ld_out) {
+  constexpr int D = 64, QT = 16, NTH = 64 * NW;
+  constexpr int PK = D + 4, PVV = D + 4, P = QT + 1;
+  constexpr int SLOT = KB * PK + KB * PVV;
+  static_assert(D * P <= SLOT, "merge tile fits the slot");
+  __shared__ __attribute__((aligned(16))) float stage[NW][SLOT];
+  __shared__ __attribute__((aligned(16))) float Qs[QT * PK];
+  __shared__ float Mm[NW][QT];
+  __shared__ float Lm[NW][QT];
+  __shared__ float Fm[NW][QT];
+  __shared__ float Dm[QT];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, i = lane & 15;
+  const int head = blockIdx.y;
+  const int hk = head / (heads / kv_heads);
+  const long b = blockIdx.z;
+  const int q0 = q_start + blockIdx.x * QT;
+  const int q = q0 + i;
+  const int k_lo = max(0, q0 - window + 1);
+  const int k_hi = min(T, q0 + QT) - 1;
+  const float* seq = qkv + b * (long)T * ld;
+  const float* kcol = seq + k_off + hk * D;
+  const float* vcol = seq + v_off + hk * D;
+
+  const int ntiles = (k_hi - k_lo + KB) / KB;
+  RowTile<D, 64, ROPE> kr;
+  VTile<D, D> vr;
+  if (wave < ntiles) {
+    kr.load(lane, kcol, ld, k_lo + wave * KB, k_hi, cos_t, sin_t);
+    vr.load(lane, vcol, ld, k_lo + wave * KB, k_hi);
+  }
+  {
+    RowTile<D, NTH, ROPE, QT> qr;
+    qr.load(tid, seq + q_off + head * D, ld, q0, T - 1, cos_t, sin_t);
+    qr.store(tid, Qs, PK);
+  }
+  __syncthreads();
+  float qv[16];  // query i, dims 16g .. 16g+15
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const floatx4 t4 = *reinterpret_cast<const floatx4*>(Qs + i * PK + 16 * g + 4 * t);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qv[4 * t + e] = t4[e];
+  }
+
+  float m_run = -INFINITY, l_run = 0.0f;
+  floatx4 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  float* Ks = stage[wave];
+  float* Vs = Ks + KB * PK;
+  for (int tile = wave; tile < ntiles; tile += NW) {
+    const int k0 = k_lo + tile * KB;
+    kr.store(lane, Ks, PK);
+    vr.store(lane, Vs, PVV);
+    wave_lds_fence();
+    if (tile + NW < ntiles) {  // next tile's loads overlap this tile's math
+      kr.load(lane, kcol, ld, k0 + NW * KB, k_hi, cos_t, sin_t);
+      vr.load(lane, vcol, ld, k0 + NW * KB, k_hi);
+    }
+
+    floatx4 sc[2][2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int par = 0; par < 2; ++par) sc[kt][par] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const floatx4 a4 = *reinterpret_cast<const floatx4*>(Ks + (16 * kt + i) * PK + 16 * g + 4 * t);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[kt][t & 1] = fm_mfma16(a4[e], qv[4 * t + e], sc[kt][t & 1]);
+      }
+    float sv[2][4];
+    float cmax = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = k0 + 16 * kt + 4 * g + r;
+        const bool ok = q < T && key <= k_hi && key <= q && key > q - window;
+        const float v = sc[kt][0][r] + sc[kt][1][r];
+        sv[kt][r] = ok ? v * scale : -INFINITY;
+        cmax = fmaxf(cmax, sv[kt][r]);
+      }
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+    const float m_new = fmaxf(m_run, cmax);
+    float psum = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = (sv[kt][r] == -INFINITY) ? 0.0f : expf(sv[kt][r] - m_new);
+        sv[kt][r] = pv;
+        psum += pv;
+      }
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);
+    const float corr = (m_run == -INFINITY) ? 0.0f : expf(m_run - m_new);
+    l_run = l_run * corr + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[dt][r] *= corr;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float* vrow = Vs + (16 * kt + 4 * g + r) * PVV + i;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt] = fm_mfma16(vrow[16 * dt], sv[kt][r], o[dt]);
+      }
+    wave_lds_fence();  // this tile's LDS reads are done before the slot is rewritten
+  }
+
+  // Merge the waves: O = sum_w O_w f_w / sum_w l_w f_w, f_w = exp(m_w - M).
+  __syncthreads();
+  float* Om = stage[wave];
+  if (g == 0) Mm[wave][i] = m_run, Lm[wave][i] = l_run;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Om[(16 * dt + 4 * g + r) * P + i] = o[dt][r];
+  __syncthreads();
+  if (tid < QT) {
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, Mm[w][qi]);
-    float num = 0.0f, den = 0.0f;
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, Mm[w][tid]);
+    float den = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      if (Mm[w][qi] == -INFINITY) continue;
-      const float f = expf(Mm[w][qi] - M);
-      num += stage[w][d * P + qi] * f;
-      den += Lm[w][qi] * f;
+      const float f = (Mm[w][tid] == -INFINITY) ? 0.0f : expf(Mm[w][tid] - M);
+      Fm[w][tid] = f;
+      if (Mm[w][tid] != -INFINITY) den += Lm[w][tid] * f;
     }
-    out[(b * (long)(T - q_start) + qg - q_start) * ld_out + head * D + d] = num / den;
+    Dm[tid] = den;
+  }
+  __syncthreads();
+  for (int e = tid; e < QT * D; e += NTH) {
+    const int qi = e / D, d = e % D;
+    const int qg = q0 + qi;
+    if (qg >= T) continue;
+    float num = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+      if (Mm[w][qi] != -INFINITY) num += stage[w][d * P + qi] * Fm[w][qi];
+    out[(b * (long)(T - q_start) + qg - q_start) * ld_out + head * D + d] = num / Dm[qi];
   }
 }
 
@@ -526,9 +723,6 @@ __global__ __launch_bounds__(512) void row_stream_linear_kernel(
 // Both double-buffer the next 64-dim piece in registers.  The 8 partial tiles
 // are summed through LDS in wave order; epilogue as in row_linear_kernel.
 
-FM_DEVICE floatx4 fm_mfma16(float a, float b, floatx4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
 
 template <int K, int BN>
 __global__ __launch_bounds__(512) void row16_linear_kernel(
@@ -874,6 +1068,22 @@ int fm_window_attention_rows(const float* qkv, int ld_qkv, int q_offset, int k_o
   if ((ld_qkv | q_offset | k_offset | v_offset) % 4) return FM_BAD_ARGUMENT;
   if (query_start < 0 || query_start > length) return FM_BAD_ARGUMENT;
   if (batch == 0 || length == query_start) return FM_OK;
+  if (head_dim == 64) {
+    // 16-query blocks; eight waves per block (fewer key tiles per wave) while
+    // the grid is too small to fill the GPU, four once blocks are plentiful.
+    const dim3 g16((length - query_start + 15) / 16, heads, batch);
+    const bool eight16 = (long)g16.x * g16.y * g16.z < 1024;
+#define FM_ATT16(R, W)                                                                             hipLaunchKernelGGL((window_attention16_kernel<R, W>), g16, dim3(64 * W), 0, stream, qkv, ld_qkv,                      q_offset, k_offset, v_offset, cos_table, sin_table, length, query_start,                           heads, kv_heads, window, scale, out, ld_out)
+    if (cos_table) {
+      if (eight16) FM_ATT16(true, 8);
+      else FM_ATT16(true, 4);
+    } else {
+      if (eight16) FM_ATT16(false, 8);
+      else FM_ATT16(false, 4);
+    }
+#undef FM_ATT16
+    return (int)hipGetLastError();
+  }
   dim3 grid((length - query_start + QB - 1) / QB, heads, batch);
   // Eight waves per block (fewer key tiles per wave) while the grid is too
   // small to fill the GPU; four once blocks are plentiful.
@@ -894,7 +1104,6 @@ int fm_window_attention_rows(const float* qkv, int ld_qkv, int q_offset, int k_o
     case 8: FM_ATT(8); break;
     case 16: FM_ATT(16); break;
     case 32: FM_ATT(32); break;
-    case 64: FM_ATT(64); break;
     default: return FM_UNSUPPORTED;
   }
 #undef FM_ATT
