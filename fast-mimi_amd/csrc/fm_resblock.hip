@@ -20,16 +20,18 @@
 namespace {
 
 constexpr int NT = 256;
-constexpr int WBK = 32;           // weight k-tile
-constexpr int PW = WBK + 4;       // weight tile pitch
 
-template <int C, int BM, int WM1, int WN1, int WM2, int WN2>
+// WBK: weight k-tile (16 keeps the LDS footprint low enough for two blocks
+// per CU at C = 128, so a second block's MFMAs cover one block's barriers).
+template <int C, int BM, int WM1, int WN1, int WM2, int WN2, int WBK>
 __global__ __launch_bounds__(NT) void resblock_kernel(const float* __restrict__ x, int L,
                                                       const float* __restrict__ w1,
                                                       const float* __restrict__ b1,
                                                       const float* __restrict__ w2,
                                                       const float* __restrict__ b2, int elu_out,
                                                       float* __restrict__ y) {
+  constexpr int PW = WBK + 4;       // weight tile pitch
+  constexpr int HK = WBK / 2;       // k per MFMA lane half within a weight tile
   constexpr int HC = C / 2;
   constexpr int K1 = 3 * C;
   constexpr int T1 = K1 / WBK, T2 = HC / WBK, T = T1 + T2;
@@ -134,14 +136,14 @@ __global__ __launch_bounds__(NT) void resblock_kernel(const float* __restrict__ 
       const int kk0 = w * WBK;
       const int tap = kk0 / C, ci0 = kk0 % C;
 #pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
+      for (int s4 = 0; s4 < WBK / 8; ++s4) {
         floatx4 a[FM1], bb[FN1];
 #pragma unroll
         for (int i = 0; i < FM1; ++i)
-          a[i] = *reinterpret_cast<const floatx4*>(&Xe[(wm1 + i * 32 + lcol + tap) * PX + ci0 + h * 16 + s4 * 4]);
+          a[i] = *reinterpret_cast<const floatx4*>(&Xe[(wm1 + i * 32 + lcol + tap) * PX + ci0 + h * HK + s4 * 4]);
 #pragma unroll
         for (int j = 0; j < FN1; ++j)
-          bb[j] = *reinterpret_cast<const floatx4*>(&Wc[(wn1 + j * 32 + lcol) * PW + h * 16 + s4 * 4]);
+          bb[j] = *reinterpret_cast<const floatx4*>(&Wc[(wn1 + j * 32 + lcol) * PW + h * HK + s4 * 4]);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -165,14 +167,14 @@ __global__ __launch_bounds__(NT) void resblock_kernel(const float* __restrict__ 
     } else {
       const int kk0 = (w - T1) * WBK;
 #pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
+      for (int s4 = 0; s4 < WBK / 8; ++s4) {
         floatx4 a[FM2], bb[FN2];
 #pragma unroll
         for (int i = 0; i < FM2; ++i)
-          a[i] = *reinterpret_cast<const floatx4*>(&Hs[(wm2 + i * 32 + lcol) * PH + kk0 + h * 16 + s4 * 4]);
+          a[i] = *reinterpret_cast<const floatx4*>(&Hs[(wm2 + i * 32 + lcol) * PH + kk0 + h * HK + s4 * 4]);
 #pragma unroll
         for (int j = 0; j < FN2; ++j)
-          bb[j] = *reinterpret_cast<const floatx4*>(&Wc[(wn2 + j * 32 + lcol) * PW + h * 16 + s4 * 4]);
+          bb[j] = *reinterpret_cast<const floatx4*>(&Wc[(wn2 + j * 32 + lcol) * PW + h * HK + s4 * 4]);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -368,8 +370,8 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
   if (!fm_resblock_supported(channels)) return FM_UNSUPPORTED;
   if (x == y) return FM_BAD_ARGUMENT;  // the halo rows of other blocks must stay intact
   if (batch == 0 || length == 0) return FM_OK;
-#define FM_RB(C, BM, A, B_, C2, D)                                                              \
-  hipLaunchKernelGGL((resblock_kernel<C, BM, A, B_, C2, D>), dim3((length + BM - 1) / BM, batch), \
+#define FM_RB(C, BM, A, B_, C2, D, KB)                                                              \
+  hipLaunchKernelGGL((resblock_kernel<C, BM, A, B_, C2, D, KB>), dim3((length + BM - 1) / BM, batch), \
                      dim3(NT), 0, stream, x, length, w1_packed, b1, w2_packed, b2, elu_out, y)
   if (channels == 64) {
     // Persistent: one 8-wave block per CU (LDS-bound), waves stride over 32-row tiles.
@@ -380,9 +382,9 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
     return (int)hipGetLastError();
   }
   switch (channels) {
-    case 64: FM_RB(64, 128, 4, 1, 4, 1); break;
-    case 128: FM_RB(128, 64, 2, 2, 2, 2); break;
-    default: FM_RB(256, 32, 1, 4, 1, 4); break;
+    case 64: FM_RB(64, 128, 4, 1, 4, 1, 32); break;
+    case 128: FM_RB(128, 64, 2, 2, 2, 2, 16); break;
+    default: FM_RB(256, 32, 1, 4, 1, 4, 32); break;
   }
 #undef FM_RB
   return (int)hipGetLastError();
