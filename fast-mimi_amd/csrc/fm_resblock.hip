@@ -218,41 +218,48 @@ __global__ __launch_bounds__(NT) void resblock_kernel(const float* __restrict__ 
 
 
 // ---------------------------------------------------------------------------
-// C = 64 residual block as a persistent kernel.  The whole block's weights fit
-// in registers as MFMA B fragments (W1^T [32][192]: 96 per lane; W2^T [64][32]:
-// 32 per lane), loaded once per wave.  Each of the 8 waves then takes 32-row
-// tiles in a grid-stride loop, with no block-level barrier: stage ELU(x) rows
-// t0-2 .. t0+31 in its own LDS slot, k3 conv (96 MFMAs, taps as row-shifted
-// views), hidden = ELU(acc + b1) into LDS, 1x1 conv (32 MFMAs), then the
-// output tile goes back through LDS so the epilogue (bias, raw residual, ELU)
-// runs on float4 runs.  Two waves per SIMD overlap one tile's loads and
-// ELUs with the other's MFMAs.  MFMA k-slots: lane half h at step 4q+e carries
-// k = 96h + 4q + e (k3 conv, k = tap*64 + c_in) or 16h + 4q + e (1x1 conv).
+// C = 64 residual block as a persistent kernel.  The block's weights are
+// staged once in LDS as MFMA B-fragment rows (W1^T [32][192], W2^T [64][32]),
+// shared by the 8 waves.  Each wave then takes 32-row tiles in a grid-stride
+// loop with no block-level barrier: stage ELU(x) rows t0-2 .. t0+31 in its own
+// LDS slot, issue the residual rows of this tile and the input rows of its
+// next tile (both land during the MFMAs), k3 conv (96 MFMAs in two chains,
+// taps as row-shifted views), hidden = ELU(acc + b1) into LDS, 1x1 conv (32
+// MFMAs), then the output tile goes back through LDS so the epilogue (bias,
+// raw residual, ELU) runs on float4 runs.  Two waves per SIMD overlap one
+// tile's memory and ELU work with the other's MFMAs.  MFMA k-slots: lane half
+// h at step 4q+e carries k = 96h + 4q + e (k3 conv, k = tap*64 + c_in) or
+// 16h + 4q + e (1x1 conv).
 constexpr int R64_WAVES = 8;
 constexpr int R64_PE = 68;   // pitch of the ELU(x) / output tile rows
 constexpr int R64_PH = 36;   // pitch of the hidden tile rows
 constexpr int R64_SLOT = 34 * R64_PE + 32 * R64_PH;
+constexpr int R64_P1 = 196;  // W1^T row pitch (4 mod 32: conflict-free 16-byte reads)
+constexpr int R64_P2 = 36;   // W2^T row pitch
 
 __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
     const float* __restrict__ x, int batch, int L, const float* __restrict__ w1,
     const float* __restrict__ b1, const float* __restrict__ w2, const float* __restrict__ b2,
     int elu_out, float* __restrict__ y) {
   constexpr int C = 64, HC = 32;
-  __shared__ __attribute__((aligned(16))) float smem[R64_WAVES * R64_SLOT];
+  __shared__ __attribute__((aligned(16))) float smem[R64_WAVES * R64_SLOT + 32 * R64_P1 + 64 * R64_P2];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, lcol = lane & 31;
   float* E = smem + wave * R64_SLOT;   // [34][68] ELU(x); later the [32][68] output tile
   float* H = E + 34 * R64_PE;          // [32][36] hidden
+  float* W1s = smem + R64_WAVES * R64_SLOT;
+  float* W2s = W1s + 32 * R64_P1;
 
-  floatx4 wa[24], wb[2][4];
-#pragma unroll
-  for (int q = 0; q < 24; ++q) wa[q] = *reinterpret_cast<const floatx4*>(w1 + lcol * 192 + 96 * h + 4 * q);
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      wb[j][q] = *reinterpret_cast<const floatx4*>(w2 + (j * 32 + lcol) * HC + 16 * h + 4 * q);
+  for (int i = threadIdx.x; i < 32 * 48; i += 64 * R64_WAVES) {
+    const int r = i / 48, c4 = (i % 48) * 4;
+    *reinterpret_cast<floatx4*>(W1s + r * R64_P1 + c4) = *reinterpret_cast<const floatx4*>(w1 + r * 192 + c4);
+  }
+  for (int i = threadIdx.x; i < 64 * 8; i += 64 * R64_WAVES) {
+    const int r = i / 8, c4 = (i % 8) * 4;
+    *reinterpret_cast<floatx4*>(W2s + r * R64_P2 + c4) = *reinterpret_cast<const floatx4*>(w2 + r * HC + c4);
+  }
   const float bias1 = b1[lcol];
+  __syncthreads();
 
   const int tpb = (L + 31) / 32;
   const long tiles = (long)batch * tpb;
@@ -275,9 +282,10 @@ __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
       xok |= (unsigned)ok << u;
     }
   };
+  if (tile < tiles) load_x(tile);
   for (; tile < tiles; tile += stride) {
     const int b = (int)(tile / tpb), t0 = (int)(tile % tpb) * 32;
-    load_x(tile);
+    const float* xb = x + (long)b * L * C;
     // ELU(x) into the slot (zero outside the sequence: the causal zero padding).
 #pragma unroll
     for (int u = 0; u < 9; ++u) {
@@ -287,22 +295,34 @@ __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
       *reinterpret_cast<floatx4*>(E + (c / 16) * R64_PE + (c % 16) * 4) =
           floatx4{fm_elu(v[0]), fm_elu(v[1]), fm_elu(v[2]), fm_elu(v[3])};
     }
+    // Raw residual rows t0 .. t0+31 (chunk c = lane + 64u, 8 per lane) and the
+    // next tile's input rows: both in flight during this tile's MFMAs.
+    floatx4 rv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int c = lane + 64 * u;
+      rv[u] = *reinterpret_cast<const floatx4*>(xb + (long)min(t0 + c / 16, L - 1) * C + (c % 16) * 4);
+    }
+    if (tile + stride < tiles) load_x(tile + stride);
     wave_lds_fence();
 
-    // k3 conv: rows = positions, columns = hidden channels.
-    floatx16 acc1;
+    // k3 conv: rows = positions, columns = hidden channels; two chains.
+    floatx16 acc1[2];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc1[r] = 0.0f;
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc1[c][r] = 0.0f;
 #pragma unroll
     for (int q = 0; q < 24; ++q) {
       const int k0 = 96 * h + 4 * q;
       const floatx4 a = *reinterpret_cast<const floatx4*>(E + (lcol + k0 / 64) * R64_PE + k0 % 64);
+      const floatx4 wq = *reinterpret_cast<const floatx4*>(W1s + lcol * R64_P1 + k0);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc1 = fm_mfma32(a[e], wa[q][e], acc1);
+      for (int e = 0; e < 4; ++e) acc1[q & 1] = fm_mfma32(a[e], wq[e], acc1[q & 1]);
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r)
-      H[fm_mfma32_row(r, lane) * R64_PH + lcol] = fm_elu(__fadd_rn(acc1[r], bias1));
+      H[fm_mfma32_row(r, lane) * R64_PH + lcol] = fm_elu(__fadd_rn(__fadd_rn(acc1[0][r], acc1[1][r]), bias1));
     wave_lds_fence();
 
     // 1x1 conv: columns = output channels (two 32-wide tiles).
@@ -315,24 +335,17 @@ __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
     for (int q = 0; q < 4; ++q) {
       const floatx4 a = *reinterpret_cast<const floatx4*>(H + lcol * R64_PH + 16 * h + 4 * q);
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
+      for (int j = 0; j < 2; ++j) {
+        const floatx4 wq = *reinterpret_cast<const floatx4*>(W2s + (j * 32 + lcol) * R64_P2 + 16 * h + 4 * q);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc2[j] = fm_mfma32(a[e], wb[j][q][e], acc2[j]);
+        for (int e = 0; e < 4; ++e) acc2[j] = fm_mfma32(a[e], wq[e], acc2[j]);
+      }
     }
     // Output tile through LDS (the ELU(x) rows are no longer read).
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) E[fm_mfma32_row(r, lane) * R64_PE + j * 32 + lcol] = acc2[j][r];
-    // Raw residual rows t0 .. t0+31 (chunk c = lane + 64u, 8 per lane); the
-    // other wave on this SIMD covers their latency.
-    const float* xb = x + (long)b * L * C;
-    floatx4 rv[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int c = lane + 64 * u;
-      rv[u] = *reinterpret_cast<const floatx4*>(xb + (long)min(t0 + c / 16, L - 1) * C + (c % 16) * 4);
-    }
     wave_lds_fence();
     float* yb = y + (long)b * L * C;
 #pragma unroll
