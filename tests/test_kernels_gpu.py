@@ -264,7 +264,7 @@ def attention_reference(qkv, B, T, H, D, window, cos, sin):
 
 @pytest.mark.parametrize("B,T,H,D,window", [(1, 250, 8, 64, 250), (1, 251, 8, 64, 250),
                                             (2, 700, 8, 64, 250), (1, 1, 8, 64, 250),
-                                            (16, 125, 8, 64, 250), (2, 18, 2, 8, 8)])
+                                            (16, 125, 8, 64, 250), (8, 300, 8, 64, 250), (2, 18, 2, 8, 8)])
 def test_window_attention(B, T, H, D, window):
     g = torch.Generator().manual_seed(T + H)
     qkv = torch.randn(B * T, 3 * H * D, generator=g)
