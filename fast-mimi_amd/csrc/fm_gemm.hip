@@ -962,6 +962,13 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
       tiles = tile_count(M, p.N, t);
       if (tiles >= t.fill) break;
     }
+    // A 128-row fast tile with K of a few hundred loses to the 64x64
+    // 16x16-MFMA tile once that one has a few hundred tiles (measured on the
+    // transformer's output projection at 2500-4000 rows).
+    if ((cfg.id == 0 || cfg.id == 1 || cfg.id == 2) && p.K >= 256 && tile_count(M, p.N, kMid64) >= 384) {
+      cfg = kMid64;
+      tiles = tile_count(M, p.N, cfg);
+    }
     // Global K-split for long K when even the K-split tile leaves CUs idle.
     const int kchunks = (p.K + KT - 1) / KT;
     if (cfg.WK > 1 && tiles < 384 && kchunks >= 32 && workspace)
