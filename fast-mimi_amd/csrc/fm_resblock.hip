@@ -3,219 +3,22 @@
 //   y = ELU?( x + conv1x1( ELU( conv_k3( ELU(x) ) + b1 ) ) + b2 )
 //
 // on channels-last x [batch, L, C] with causal (left) zero padding of 2 and
-// hidden width C/2.  One block owns BM consecutive positions of one batch
-// item.  ELU(x) for rows t0-2 .. t0+BM-1 (the causal halo included) is staged
-// in LDS once; the k3 convolution reads its three taps as row-shifted views
-// of that tile, so the input is read from HBM once instead of once per tap.
-// The hidden activations never leave LDS; the 1x1 convolution adds the raw
-// residual (read once, coalesced) and the block's trailing ELU in its
-// epilogue.  Both GEMMs run on FP32 MFMA with the k-permuted 16-byte fragment
-// reads of the main GEMM engine (k-slot of lane half h at step 4q+e carries
-// k = 16h + 4q + e).  Weights stream through a double-buffered LDS tile fed
-// from a 3-deep register prefetch ring: W1^T [C/2][3C] (k = tap*C + c_in, the
-// packed conv layout) then W2^T [C][C/2].
+// hidden width C/2.  A block owns 32-row tiles of one batch item.  ELU(x) for
+// rows t0-2 .. t0+BM-1 (the causal halo included) is staged in LDS once; the
+// k3 convolution reads its three taps as row-shifted views of that tile, so
+// the input is read from HBM once instead of once per tap.  The hidden
+// activations never leave LDS; the 1x1 convolution adds the raw residual
+// (read once, coalesced) and the block's trailing ELU in its epilogue.  Both
+// GEMMs run on FP32 MFMA with the k-permuted 16-byte fragment reads of the
+// main GEMM engine (k-slot of lane half h at step 4q+e carries k = 16h + 4q +
+// e).  Weights are the packed conv layout: W1^T [C/2][3C] (k = tap*C + c_in)
+// and W2^T [C][C/2].
 
 #include "fm_common.h"
 
 namespace {
 
 constexpr int NT = 256;
-
-// WBK: weight k-tile (16 keeps the LDS footprint low enough for two blocks
-// per CU at C = 128, so a second block's MFMAs cover one block's barriers).
-template <int C, int BM, int WM1, int WN1, int WM2, int WN2, int WBK>
-__global__ __launch_bounds__(NT) void resblock_kernel(const float* __restrict__ x, int L,
-                                                      const float* __restrict__ w1,
-                                                      const float* __restrict__ b1,
-                                                      const float* __restrict__ w2,
-                                                      const float* __restrict__ b2, int elu_out,
-                                                      float* __restrict__ y) {
-  constexpr int PW = WBK + 4;       // weight tile pitch
-  constexpr int HK = WBK / 2;       // k per MFMA lane half within a weight tile
-  constexpr int HC = C / 2;
-  constexpr int K1 = 3 * C;
-  constexpr int T1 = K1 / WBK, T2 = HC / WBK, T = T1 + T2;
-  constexpr int PX = C + 4, PH = HC + 4;
-  constexpr int FM1 = BM / WM1 / 32, FN1 = HC / WN1 / 32;
-  constexpr int FM2 = BM / WM2 / 32, FN2 = C / WN2 / 32;
-  constexpr int WROWS = C;                      // max rows of a weight tile
-  constexpr int WPT = (WROWS * WBK / 4) / NT;   // float4 per thread (W2 tiles)
-  static_assert(WM1 * WN1 == 4 && WM2 * WN2 == 4, "four waves");
-  static_assert(FM1 >= 1 && FN1 >= 1 && FM2 >= 1 && FN2 >= 1, "32x32 wave tiles");
-  static_assert(HC % WBK == 0 && WPT >= 1, "shapes");
-
-  __shared__ __attribute__((aligned(16))) float Xe[(BM + 2) * PX];
-  __shared__ __attribute__((aligned(16))) float Hs[BM * PH];
-  __shared__ __attribute__((aligned(16))) float Ws[2][WROWS * PW];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int h = lane >> 5, lcol = lane & 31;
-  const long b = blockIdx.y;
-  const int t0 = blockIdx.x * BM;
-  const float* xb = x + b * (long)L * C;
-
-  // Stage ELU(x) rows t0-2 .. t0+BM-1; loads batched ahead of the stores.
-  {
-    constexpr int CH = (BM + 2) * C / 4;
-    constexpr int U = (CH + NT - 1) / NT;
-    floatx4 v[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = tid + u * NT;
-      const int r = c / (C / 4), k = (c % (C / 4)) * 4;
-      const int t = t0 - 2 + r;
-      v[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-      if (c < CH && t >= 0 && t < L) v[u] = *reinterpret_cast<const floatx4*>(xb + (long)t * C + k);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = tid + u * NT;
-      if (c >= CH) continue;
-      const int r = c / (C / 4), k = (c % (C / 4)) * 4;
-      *reinterpret_cast<floatx4*>(&Xe[r * PX + k]) =
-          floatx4{fm_elu(v[u].x), fm_elu(v[u].y), fm_elu(v[u].z), fm_elu(v[u].w)};
-    }
-  }
-
-  // Weight tile w: rows of W1^T (w < T1) or W2^T, k columns [k0, k0 + 32).
-  // Tiles are fetched PD iterations ahead into a ring of register sets, so a
-  // tile's global-load latency overlaps PD iterations of MFMA work.
-  constexpr int PD = 3;
-  floatx4 rw[PD][WPT];
-  auto load_w = [&](int w, floatx4 (&dst)[WPT]) {
-    const bool first = w < T1;
-    const int rows = first ? HC : C;
-    const int ld = first ? K1 : HC;
-    const float* src = first ? w1 : w2;
-    const int k0 = (first ? w : w - T1) * WBK;
-#pragma unroll
-    for (int u = 0; u < WPT; ++u) {
-      const int c = tid + u * NT;
-      const int r = c / (WBK / 4), k = (c % (WBK / 4)) * 4;
-      dst[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-      if (w < T && r < rows) dst[u] = *reinterpret_cast<const floatx4*>(src + (long)r * ld + k0 + k);
-    }
-  };
-  auto store_w = [&](int stage, const floatx4 (&srcv)[WPT]) {
-#pragma unroll
-    for (int u = 0; u < WPT; ++u) {
-      const int c = tid + u * NT;
-      const int r = c / (WBK / 4), k = (c % (WBK / 4)) * 4;
-      *reinterpret_cast<floatx4*>(&Ws[stage][r * PW + k]) = srcv[u];
-    }
-  };
-
-  floatx16 acc1[FM1][FN1];
-  floatx16 acc2[FM2][FN2];
-#pragma unroll
-  for (int i = 0; i < FM1; ++i)
-#pragma unroll
-    for (int j = 0; j < FN1; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc1[i][j][r] = 0.0f;
-#pragma unroll
-  for (int i = 0; i < FM2; ++i)
-#pragma unroll
-    for (int j = 0; j < FN2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc2[i][j][r] = 0.0f;
-
-  const int wm1 = (wave / WN1) * (BM / WM1), wn1 = (wave % WN1) * (HC / WN1);
-  const int wm2 = (wave / WN2) * (BM / WM2), wn2 = (wave % WN2) * (C / WN2);
-
-#pragma unroll
-  for (int d = 0; d < PD; ++d) load_w(d, rw[d]);
-  store_w(0, rw[0]);
-  __syncthreads();
-#pragma unroll
-  for (int w = 0; w < T; ++w) {
-    const int cur = w & 1;
-    if (w + PD < T) load_w(w + PD, rw[w % PD]);  // set w % PD was stored to LDS already
-    const float* Wc = Ws[cur];
-    if (w < T1) {
-      const int kk0 = w * WBK;
-      const int tap = kk0 / C, ci0 = kk0 % C;
-#pragma unroll
-      for (int s4 = 0; s4 < WBK / 8; ++s4) {
-        floatx4 a[FM1], bb[FN1];
-#pragma unroll
-        for (int i = 0; i < FM1; ++i)
-          a[i] = *reinterpret_cast<const floatx4*>(&Xe[(wm1 + i * 32 + lcol + tap) * PX + ci0 + h * HK + s4 * 4]);
-#pragma unroll
-        for (int j = 0; j < FN1; ++j)
-          bb[j] = *reinterpret_cast<const floatx4*>(&Wc[(wn1 + j * 32 + lcol) * PW + h * HK + s4 * 4]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int i = 0; i < FM1; ++i)
-#pragma unroll
-            for (int j = 0; j < FN1; ++j) acc1[i][j] = fm_mfma32(a[i][e], bb[j][e], acc1[i][j]);
-      }
-      if (w == T1 - 1) {
-        // Hidden activations: ELU(conv_k3 + b1) into LDS.
-#pragma unroll
-        for (int j = 0; j < FN1; ++j) {
-          const int n = wn1 + j * 32 + lcol;
-          const float bias = b1[n];
-#pragma unroll
-          for (int i = 0; i < FM1; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-              Hs[(wm1 + i * 32 + fm_mfma32_row(r, lane)) * PH + n] = fm_elu(__fadd_rn(acc1[i][j][r], bias));
-        }
-      }
-    } else {
-      const int kk0 = (w - T1) * WBK;
-#pragma unroll
-      for (int s4 = 0; s4 < WBK / 8; ++s4) {
-        floatx4 a[FM2], bb[FN2];
-#pragma unroll
-        for (int i = 0; i < FM2; ++i)
-          a[i] = *reinterpret_cast<const floatx4*>(&Hs[(wm2 + i * 32 + lcol) * PH + kk0 + h * HK + s4 * 4]);
-#pragma unroll
-        for (int j = 0; j < FN2; ++j)
-          bb[j] = *reinterpret_cast<const floatx4*>(&Wc[(wn2 + j * 32 + lcol) * PW + h * HK + s4 * 4]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int i = 0; i < FM2; ++i)
-#pragma unroll
-            for (int j = 0; j < FN2; ++j) acc2[i][j] = fm_mfma32(a[i][e], bb[j][e], acc2[i][j]);
-      }
-    }
-    if (w + 1 < T) store_w(cur ^ 1, rw[(w + 1) % PD]);
-    __syncthreads();
-  }
-
-  // y = ELU?(x + (conv1x1 + b2)), rows t < L.  Residual loads are all issued
-  // before any store so they overlap.
-  float* yb = y + b * (long)L * C;
-  float rv[FN2][FM2][16];
-#pragma unroll
-  for (int j = 0; j < FN2; ++j)
-#pragma unroll
-    for (int i = 0; i < FM2; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int t = min(t0 + wm2 + i * 32 + fm_mfma32_row(r, lane), L - 1);
-        rv[j][i][r] = xb[(long)t * C + wn2 + j * 32 + lcol];
-      }
-#pragma unroll
-  for (int j = 0; j < FN2; ++j) {
-    const int n = wn2 + j * 32 + lcol;
-    const float bias = b2[n];
-#pragma unroll
-    for (int i = 0; i < FM2; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int t = t0 + wm2 + i * 32 + fm_mfma32_row(r, lane);
-        float v = __fadd_rn(rv[j][i][r], __fadd_rn(acc2[i][j][r], bias));
-        if (elu_out) v = fm_elu(v);
-        if (t < L) yb[(long)t * C + n] = v;
-      }
-  }
-}
-
 
 // ---------------------------------------------------------------------------
 // C = 64 residual block as a persistent kernel.  The block's weights are
@@ -366,6 +169,160 @@ __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Residual block with register-streamed weights.  Waves form WM x (4 / WM):
+// wave (wr, wc) owns output rows wr*32 .. +31 of the block, hidden columns
+// wc*HC/WN .. (one 32-wide MFMA tile) and output columns wc*C/WN .. (two
+// 32-wide tiles).  A wave's weight fragments are read straight from the
+// row-major W1^T [HC][3C] / W2^T [C][HC] (L2-resident, 16-byte k-permuted
+// lane reads) into a PD-deep register ring, so the k-loops have no block
+// barrier and LDS holds only ELU(x) with its causal halo and the hidden tile
+// (~52 KB: three blocks per CU).  One barrier separates the two convs.  In
+// the k3 conv the A fragments of the next 32-k step are read from LDS while
+// the current step's MFMAs run.
+template <int C, int BM, int WM, int PD>
+__global__ __launch_bounds__(NT, 3) void resblock_direct_kernel(
+    const float* __restrict__ x, int L, const float* __restrict__ w1, const float* __restrict__ b1,
+    const float* __restrict__ w2, const float* __restrict__ b2, int elu_out, float* __restrict__ y) {
+  constexpr int WN = 4 / WM, HC = C / 2, K1 = 3 * C;
+  constexpr int PX = C + 4, PH = HC + 4;
+  constexpr int T1 = K1 / 32, T2 = HC / 32, FN2 = 2;
+  constexpr int T = T1 + T2 * FN2;
+  static_assert(BM == 32 * WM && HC / WN == 32 && C / WN == 32 * FN2, "wave tiling");
+  __shared__ __attribute__((aligned(16))) float Xe[(BM + 2) * PX];
+  __shared__ __attribute__((aligned(16))) float Hs[BM * PH];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, lcol = lane & 31;
+  const int wr = wave / WN, wc = wave % WN;
+  const long b = blockIdx.y;
+  const int t0 = blockIdx.x * BM;
+  const float* xb = x + b * (long)L * C;
+
+  // Input rows first (the critical path), weight ring right behind them.
+  constexpr int CH = (BM + 2) * C / 4, U = (CH + NT - 1) / NT;
+  floatx4 xv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = tid + u * NT;
+    const int r = c / (C / 4), k = (c % (C / 4)) * 4;
+    const int t = t0 - 2 + r;
+    xv[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (c < CH && t >= 0 && t < L) xv[u] = *reinterpret_cast<const floatx4*>(xb + (long)t * C + k);
+  }
+  const float* w1p = w1 + (long)(wc * 32 + lcol) * K1 + 16 * h;
+  const float* w2p = w2 + (long)(wc * 64 + lcol) * HC + 16 * h;
+  floatx4 ring[PD][4];
+  auto load_unit = [&](int u, floatx4 (&d)[4]) {
+    const float* src;
+    if (u < T1) {
+      src = w1p + u * 32;
+    } else {
+      const int v = u - T1, kt = v / FN2, j = v % FN2;
+      src = w2p + (long)j * 32 * HC + kt * 32;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) d[q] = *reinterpret_cast<const floatx4*>(src + 4 * q);
+  };
+#pragma unroll
+  for (int d = 0; d < PD; ++d) load_unit(d, ring[d]);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = tid + u * NT;
+    if (c >= CH) continue;
+    const int r = c / (C / 4), k = (c % (C / 4)) * 4;
+    *reinterpret_cast<floatx4*>(&Xe[r * PX + k]) =
+        floatx4{fm_elu(xv[u].x), fm_elu(xv[u].y), fm_elu(xv[u].z), fm_elu(xv[u].w)};
+  }
+  __syncthreads();
+
+  const int arow = wr * 32 + lcol;
+  // Stage-1 A fragments of k-step u: the row-shifted view of tap u*32 / C.
+  auto load_a1 = [&](int u, floatx4 (&a)[4]) {
+    const int kk0 = u * 32, tap = kk0 / C, ci0 = kk0 % C;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      a[q] = *reinterpret_cast<const floatx4*>(&Xe[(arow + tap) * PX + ci0 + 16 * h + 4 * q]);
+  };
+  auto load_a2 = [&](int kt, floatx4 (&a)[4]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      a[q] = *reinterpret_cast<const floatx4*>(&Hs[arow * PH + kt * 32 + 16 * h + 4 * q]);
+  };
+
+  // conv k3: two accumulator chains (even / odd 4-k steps).
+  floatx16 acc1[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc1[i][r] = 0.0f;
+  floatx4 a[2][4];
+  load_a1(0, a[0]);
+#pragma unroll
+  for (int u = 0; u < T1; ++u) {
+    if (u + 1 < T1) load_a1(u + 1, a[(u + 1) & 1]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc1[q & 1] = fm_mfma32(a[u & 1][q][e], ring[u % PD][q][e], acc1[q & 1]);
+    // Refill the slot just consumed; the barrier keeps the compiler from
+    // sinking the loads to their use (which serialises them).
+    if (u + PD < T) load_unit(u + PD, ring[u % PD]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  {
+    const int n = wc * 32 + lcol;
+    const float bias = b1[n];
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      Hs[(wr * 32 + fm_mfma32_row(r, lane)) * PH + n] =
+          fm_elu(__fadd_rn(__fadd_rn(acc1[0][r], acc1[1][r]), bias));
+  }
+  __syncthreads();
+
+  // Residual rows land during the 1x1 conv.
+  float* yb = y + b * (long)L * C;
+  float rv[FN2][16];
+#pragma unroll
+  for (int j = 0; j < FN2; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = min(t0 + wr * 32 + fm_mfma32_row(r, lane), L - 1);
+      rv[j][r] = xb[(long)t * C + wc * 64 + j * 32 + lcol];
+    }
+  floatx16 acc2[FN2];
+#pragma unroll
+  for (int j = 0; j < FN2; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc2[j][r] = 0.0f;
+#pragma unroll
+  for (int kt = 0; kt < T2; ++kt) {
+    load_a2(kt, a[0]);
+#pragma unroll
+    for (int j = 0; j < FN2; ++j) {
+      const int u = T1 + kt * FN2 + j;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc2[j] = fm_mfma32(a[0][q][e], ring[u % PD][q][e], acc2[j]);
+      if (u + PD < T) load_unit(u + PD, ring[u % PD]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < FN2; ++j) {
+    const int n = wc * 64 + j * 32 + lcol;
+    const float bias = b2[n];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = t0 + wr * 32 + fm_mfma32_row(r, lane);
+      float v = __fadd_rn(rv[j][r], __fadd_rn(acc2[j][r], bias));
+      if (elu_out) v = fm_elu(v);
+      if (t < L) yb[(long)t * C + n] = v;
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -383,23 +340,19 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
   if (!fm_resblock_supported(channels)) return FM_UNSUPPORTED;
   if (x == y) return FM_BAD_ARGUMENT;  // the halo rows of other blocks must stay intact
   if (batch == 0 || length == 0) return FM_OK;
-#define FM_RB(C, BM, A, B_, C2, D, KB)                                                              \
-  hipLaunchKernelGGL((resblock_kernel<C, BM, A, B_, C2, D, KB>), dim3((length + BM - 1) / BM, batch), \
-                     dim3(NT), 0, stream, x, length, w1_packed, b1, w2_packed, b2, elu_out, y)
   if (channels == 64) {
     // Persistent: one 8-wave block per CU (LDS-bound), waves stride over 32-row tiles.
     const long tiles = (long)batch * ((length + 31) / 32);
     const int blocks = (int)std::min<long>((tiles + R64_WAVES - 1) / R64_WAVES, 256);
     hipLaunchKernelGGL(resblock64_kernel, dim3(blocks), dim3(64 * R64_WAVES), 0, stream, x, batch,
                        length, w1_packed, b1, w2_packed, b2, elu_out, y);
-    return (int)hipGetLastError();
+  } else if (channels == 128) {
+    hipLaunchKernelGGL((resblock_direct_kernel<128, 64, 2, 3>), dim3((length + 63) / 64, batch), dim3(NT),
+                       0, stream, x, length, w1_packed, b1, w2_packed, b2, elu_out, y);
+  } else {
+    hipLaunchKernelGGL((resblock_direct_kernel<256, 32, 1, 3>), dim3((length + 31) / 32, batch), dim3(NT),
+                       0, stream, x, length, w1_packed, b1, w2_packed, b2, elu_out, y);
   }
-  switch (channels) {
-    case 64: FM_RB(64, 128, 4, 1, 4, 1, 32); break;
-    case 128: FM_RB(128, 64, 2, 2, 2, 2, 16); break;
-    default: FM_RB(256, 32, 1, 4, 1, 4, 32); break;
-  }
-#undef FM_RB
   return (int)hipGetLastError();
 }
 

@@ -40,8 +40,6 @@ _WORKSPACE_BYTES = 64 << 20
 _ROW_LINEAR_MAX_ROWS = 1024
 # Up to this many rows the 16-row kernels on fragment-packed weights are used.
 _ROW16_MAX_ROWS = 512
-# Residual blocks of >= 256 channels run as two GEMM-engine convs from this many rows.
-_RES_UNFUSED_ROWS = 100_000
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -260,12 +258,9 @@ class MimiRuntime:
 
     def _resblock(self, x, B, L, block, elu_after: bool, tag: str = "res"):
         c1, c2 = block
-        # The fused kernel holds one block per CU at 256 channels; past ~10^5
-        # rows the two GEMM-engine convs (hidden tile through HBM) measured
-        # faster (batch 16 x 10 s: -0.36 ms), below it the fused kernel wins.
+        # The fused kernel (hidden tile kept on chip) covers the SEANet widths;
+        # other shapes run as two GEMM-engine convs.
         fused = c1.k == 3 and nat.library().fm_resblock_supported(c2.c_out)
-        if fused and c2.c_out >= 256 and B * L >= _RES_UNFUSED_ROWS:
-            fused = False
         if fused:
             self._tag = tag
             y = torch.empty_like(x)

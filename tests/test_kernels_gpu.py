@@ -150,7 +150,8 @@ def test_long_k_epilogues(B, C, L, ws):
 
 
 @pytest.mark.parametrize("B,C,L", [(1, 64, 1000), (2, 64, 129), (1, 128, 777), (3, 128, 1),
-                                   (1, 256, 300), (2, 256, 33), (1, 64, 240000)])
+                                   (1, 256, 300), (2, 256, 33), (1, 64, 240000), (2, 128, 6001),
+                                   (2, 256, 12001)])
 @pytest.mark.parametrize("elu_out", [1, 0])
 def test_fused_resblock(B, C, L, elu_out):
     """fm_resblock equals the reference block x + conv1x1(ELU(conv_k3(ELU(x))))."""
