@@ -814,6 +814,23 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
     __syncthreads();
   }
   load_a(0, 0);
+  // Epilogue operands (residual, LayerScale, RoPE tables) are fetched now so
+  // their latency hides under the MFMAs instead of trailing the reduction.
+  const int er = tid / (BN / OPT), ec = (tid % (BN / OPT)) * OPT;
+  const long m = m0 + er;
+  const long mc = min(m, (long)rows - 1);
+  const int tpos = (int)(mc % rows_per_seq);
+  const bool rope = BN == 64 && cos_t && n0 < rope_cols;
+  const bool res_scale = flags & FM_EPI_RES_SCALE;
+  float e_res[OPT], e_scale[OPT], e_cos[OPT], e_sin[OPT];
+#pragma unroll
+  for (int c = 0; c < OPT; ++c) {
+    const int n = n0 + ec + c;
+    e_res[c] = res_scale ? res[mc * N + n] : 0.0f;
+    e_scale[c] = res_scale ? scale[n] : 0.0f;
+    e_cos[c] = rope ? cos_t[(long)tpos * 64 + ec + c] : 0.0f;
+    e_sin[c] = rope ? sin_t[(long)tpos * 64 + ec + c] : 0.0f;
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   floatx4 acc[NT];
@@ -841,7 +858,6 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
     for (int r = 0; r < 4; ++r) red[(wave * BM + 4 * g + r) * PR + 16 * j + li] = acc[j][r];
   __syncthreads();
   // OPT consecutive outputs per thread, BN / OPT threads per row.
-  const int er = tid / (BN / OPT), ec = (tid % (BN / OPT)) * OPT;
   float out[OPT];
 #pragma unroll
   for (int c = 0; c < OPT; ++c) {
@@ -850,8 +866,6 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
     for (int q = 1; q < NWV; ++q) v = __fadd_rn(v, red[(q * BM + er) * PR + ec + c]);
     out[c] = v;
   }
-  const long m = m0 + er;
-  const bool rope = BN == 64 && cos_t && n0 < rope_cols;
   if (rope) {
     __syncthreads();
 #pragma unroll
@@ -859,19 +873,17 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
     __syncthreads();
   }
   if (m >= rows) return;
-  const int tpos = (int)(m % rows_per_seq);
 #pragma unroll
   for (int c = 0; c < OPT; ++c) {
-    const int n = n0 + ec + c;
     float v = out[c];
     if (rope) {
       const int d = ec + c;
       const float partner = red[er * PR + (d < 32 ? d + 32 : d - 32)];
       const float rot = d < 32 ? -partner : partner;
-      v = __fadd_rn(__fmul_rn(v, cos_t[(long)tpos * 64 + d]), __fmul_rn(rot, sin_t[(long)tpos * 64 + d]));
+      v = __fadd_rn(__fmul_rn(v, e_cos[c]), __fmul_rn(rot, e_sin[c]));
     }
     if (flags & FM_EPI_GELU) v = fm_gelu(v);
-    if (flags & FM_EPI_RES_SCALE) v = __fadd_rn(res[m * N + n], __fmul_rn(scale[n], v));
+    if (res_scale) v = __fadd_rn(e_res[c], __fmul_rn(e_scale[c], v));
     out[c] = v;
   }
   float* dst = y + m * N + n0 + ec;
