@@ -261,7 +261,15 @@ __global__ __launch_bounds__(256) void rvq_step_kernel(StepArgs a) {
 // k-part order before the distances.  The prologue resolves step j-1 (eight
 // lanes per row, shuffle-reduced) and forms residual_j and |residual_j|^2.
 template <int DIM, int KP>
-__global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a, const float* __restrict__ embed) {
+__global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a0, const float* __restrict__ e0,
+                                                            StepArgs a1, const float* __restrict__ e1) {
+  // blockIdx.z picks the branch (semantic / acoustic chains share launches).
+  const StepArgs a = blockIdx.z ? a1 : a0;
+  const float* __restrict__ embed = blockIdx.z ? e1 : e0;
+  // A branch one step past its last codebook only resolves that codebook
+  // (chunk-0 blocks write the codes).
+  const bool fin = a.embed_t == nullptr;
+  if (fin && blockIdx.y != 0) return;
   constexpr int EG = 4 / KP, KW = DIM / KP, NPC = KW / 64, PX = DIM + 4, PR = RB + 1;
   constexpr int CH = DIM / 32;  // float4 chunks per lane in the prologue (8 lanes per row)
   static_assert(KW % 64 == 0, "k-part of whole 64-dim pieces");
@@ -296,7 +304,7 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a, const fl
 #pragma unroll
     for (int j = 0; j < 8; ++j) dst[j] = *reinterpret_cast<const floatx4*>(src + 4 * j);
   };
-  const bool has_work = KP == 1 ? items > 0 : g < nsub;
+  const bool has_work = !fin && (KP == 1 ? items > 0 : g < nsub);
   if (has_work) load_piece(cur, 0);
 
   // ---- prologue: row r = tid / 8, lane part pt = tid % 8.
@@ -305,6 +313,13 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a, const fl
     const long m = m0 + r;
     const long mc = min(m, (long)a.M - 1);
     const bool valid = m < a.M;
+    // The residual rows do not depend on the previous code: issue them first.
+    floatx4 xv[CH], ev[CH];
+    if (!fin) {
+#pragma unroll
+      for (int u = 0; u < CH; ++u)
+        xv[u] = *reinterpret_cast<const floatx4*>(a.resid_in + mc * a.ld_in + 4 * (pt + 8 * u));
+    }
     int code = 0;
     if (a.prev_embed) {
       float bv;
@@ -316,11 +331,10 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a, const fl
         a.prev_codes[b * a.batch_stride + t] = code;
       }
     }
-    floatx4 xv[CH], ev[CH];
+    if (fin) return;
+    if (a.prev_embed) {
 #pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      xv[u] = *reinterpret_cast<const floatx4*>(a.resid_in + mc * a.ld_in + 4 * (pt + 8 * u));
-      if (a.prev_embed)
+      for (int u = 0; u < CH; ++u)
         ev[u] = *reinterpret_cast<const floatx4*>(a.prev_embed + (long)code * DIM + 4 * (pt + 8 * u));
     }
     for (int c = tid; c < e_end - e_begin; c += 256) normS[c] = a.norms[e_begin + c];
@@ -488,6 +502,122 @@ size_t step_lds_bytes(int dim) {
          RB * 4;
 }
 
+// Launch plan shared by every step of an encode: fast MFMA kernel with KP
+// k-parts per 32-entry sub-tile while the launch stays within ~1024 blocks,
+// else 128-entry (or larger) chunks.  General kernel: chunks doubling until
+// the launch has 512 blocks, multiples of NT entries.
+struct RvqPlan {
+  bool fast;
+  int kp, chunks, ce, row_blocks;
+  size_t lds;
+};
+
+RvqPlan rvq_plan(int rows, int dim, int entries) {
+  RvqPlan pl{};
+  pl.row_blocks = (rows + RB - 1) / RB;
+  pl.fast = (dim == 64 || dim == 128 || dim == 256);
+  pl.chunks = 1;
+  pl.kp = 1;
+  constexpr int blocks_cap = 1024;
+  if (pl.fast) {
+    const int sub = (entries + 31) / 32;
+    if (dim >= 256 && sub <= kMaxChunks && pl.row_blocks * sub <= blocks_cap) {
+      pl.kp = 4, pl.chunks = sub;
+    } else if (dim >= 128 && (sub + 1) / 2 <= kMaxChunks && pl.row_blocks * ((sub + 1) / 2) <= blocks_cap) {
+      pl.kp = 2, pl.chunks = (sub + 1) / 2;
+    } else {
+      int per = 128;
+      while ((entries + per - 1) / per > kMaxChunks || pl.row_blocks * ((entries + per - 1) / per) > blocks_cap) {
+        if (per >= entries) break;
+        per *= 2;
+      }
+      pl.chunks = (entries + per - 1) / per;
+    }
+  } else {
+    while (pl.chunks < 16 && pl.row_blocks * pl.chunks < 512 && entries / (pl.chunks * 2) >= NT) pl.chunks *= 2;
+  }
+  const int chunk_entries = pl.fast ? (pl.kp == 4 ? 32 : pl.kp == 2 ? 64 : (entries + pl.chunks - 1) / pl.chunks)
+                                    : ((entries + pl.chunks - 1) / pl.chunks + NT - 1) / NT * NT;
+  pl.ce = pl.fast && pl.kp == 1 ? (chunk_entries + 31) / 32 * 32 : chunk_entries;
+  pl.lds = pl.fast ? ((size_t)RB * (dim + 4) + RB + 2 * 4 * RB + 3 * 32 * (RB + 1) + pl.ce) * 4
+                   : step_lds_bytes(dim);
+  return pl;
+}
+
+// One branch's buffers: two residual / partial sets used alternately by the steps.
+struct RvqBranch {
+  const float* x;
+  int ld_x, count;
+  const float *embeds, *embeds_t, *norms;
+  int64_t* codes;
+  float* resid[2];
+  float* val[2];
+  int* idx[2];
+};
+
+RvqBranch rvq_branch(const float* x, int ld_x, int count, const float* embeds, const float* embeds_t,
+                     const float* norms, int64_t* codes, void* workspace, int rows, int dim) {
+  RvqBranch br{x, ld_x, count, embeds, embeds_t, norms, codes, {}, {}, {}};
+  char* ws = static_cast<char*>(workspace);
+  br.resid[0] = reinterpret_cast<float*>(ws);
+  br.resid[1] = br.resid[0] + (size_t)rows * dim;
+  ws += (size_t)2 * rows * dim * sizeof(float);
+  br.val[0] = reinterpret_cast<float*>(ws);
+  br.val[1] = br.val[0] + (size_t)kMaxChunks * rows;
+  ws += (size_t)2 * kMaxChunks * rows * sizeof(float);
+  br.idx[0] = reinterpret_cast<int*>(ws);
+  br.idx[1] = br.idx[0] + (size_t)kMaxChunks * rows;
+  return br;
+}
+
+// Step j of a branch (j == count: resolve the last codebook only).
+StepArgs rvq_step_args(const RvqBranch& br, int j, const RvqPlan& pl, int rows, int rows_per_batch,
+                       int dim, int entries, int batch_stride) {
+  StepArgs a{};
+  const int cur = j & 1, prev = cur ^ 1;
+  if (j == 0) {
+    a.resid_in = br.x;
+    a.ld_in = br.ld_x;
+  } else {
+    a.resid_in = (j == 1) ? br.x : br.resid[prev];
+    a.ld_in = (j == 1) ? br.ld_x : dim;
+    a.prev_embed = br.embeds + (size_t)(j - 1) * entries * dim;
+    a.prev_val = br.val[prev];
+    a.prev_idx = br.idx[prev];
+    a.resid_out = j < br.count ? br.resid[cur] : nullptr;
+    a.prev_codes = br.codes + (size_t)(j - 1) * rows_per_batch;
+  }
+  if (j < br.count) {
+    a.embed_t = br.embeds_t + (size_t)j * entries * dim;
+    a.norms = br.norms + (size_t)j * entries;
+    a.val = br.val[cur];
+    a.idx = br.idx[cur];
+  }
+  a.M = rows; a.dim = dim; a.entries = entries; a.chunk_entries = pl.ce;
+  a.chunks = pl.chunks; a.rows_per_batch = rows_per_batch; a.batch_stride = batch_stride;
+  return a;
+}
+
+int launch_fast_step(const RvqPlan& pl, int dim, dim3 grid, const StepArgs& a0, const float* e0,
+                     const StepArgs& a1, const float* e1, hipStream_t stream) {
+#define FM_RVQ(D, K) \
+  hipLaunchKernelGGL((rvq_step_mfma_kernel<D, K>), grid, dim3(256), pl.lds, stream, a0, e0, a1, e1)
+  if (dim == 256 && pl.kp == 4) FM_RVQ(256, 4);
+  else if (dim == 256 && pl.kp == 2) FM_RVQ(256, 2);
+  else if (dim == 256) FM_RVQ(256, 1);
+  else if (dim == 128 && pl.kp == 2) FM_RVQ(128, 2);
+  else if (dim == 128) FM_RVQ(128, 1);
+  else FM_RVQ(64, 1);
+#undef FM_RVQ
+  return (int)hipGetLastError();
+}
+
+bool rvq_args_ok(const float* x, int ld_x, int rows, int rows_per_batch, int dim, int entries,
+                 const float* embeds, const float* embeds_t, const float* norms, const int64_t* codes) {
+  return x && embeds && embeds_t && norms && codes && rows >= 0 && dim > 0 && dim % 4 == 0 &&
+         ld_x % 4 == 0 && entries > 0 && rows_per_batch > 0 && ld_x >= dim;
+}
+
 }  // namespace
 
 extern "C" {
@@ -518,89 +648,99 @@ int fm_rvq_encode(const float* x, int ld_x, int rows, int rows_per_batch, int di
                   int count, const float* embeds, const float* embeds_t, const float* norms,
                   int64_t* codes, int batch_stride, void* workspace, size_t workspace_bytes,
                   hipStream_t stream) {
-  if (!x || !embeds || !embeds_t || !norms || !codes || rows < 0 || dim <= 0 || dim % 4 || ld_x % 4 ||
-      entries <= 0 || count <= 0 || rows_per_batch <= 0 || ld_x < dim)
+  if (!rvq_args_ok(x, ld_x, rows, rows_per_batch, dim, entries, embeds, embeds_t, norms, codes) ||
+      count <= 0)
     return FM_BAD_ARGUMENT;
   if (rows == 0) return FM_OK;
   if (!workspace || workspace_bytes < fm_rvq_workspace_bytes(rows, dim, entries))
     return FM_WORKSPACE_TOO_SMALL;
-  const int row_blocks = (rows + RB - 1) / RB;
-  // Fast kernel: KP k-parts per 32-entry sub-tile while the launch stays
-  // within ~1024 blocks, else 128-entry (or larger) chunks.  General kernel:
-  // chunks doubling until the launch has 512 blocks, multiples of NT entries.
-  const bool fast = (dim == 64 || dim == 128 || dim == 256);
-  int chunks = 1, kp = 1;
-  if (fast) {
-    const int sub = (entries + 31) / 32;
-    if (dim >= 256 && sub <= kMaxChunks && row_blocks * sub <= 1024) {
-      kp = 4, chunks = sub;
-    } else if (dim >= 128 && (sub + 1) / 2 <= kMaxChunks && row_blocks * ((sub + 1) / 2) <= 1024) {
-      kp = 2, chunks = (sub + 1) / 2;
-    } else {
-      int per = 128;
-      while ((entries + per - 1) / per > kMaxChunks || row_blocks * ((entries + per - 1) / per) > 1024) {
-        if (per >= entries) break;
-        per *= 2;
-      }
-      chunks = (entries + per - 1) / per;
-    }
-  } else {
-    while (chunks < 16 && row_blocks * chunks < 512 && entries / (chunks * 2) >= NT) chunks *= 2;
-  }
-  const int chunk_entries = fast ? (kp == 4 ? 32 : kp == 2 ? 64 : (entries + chunks - 1) / chunks)
-                                 : ((entries + chunks - 1) / chunks + NT - 1) / NT * NT;
-  const int ce = fast && kp == 1 ? (chunk_entries + 31) / 32 * 32 : chunk_entries;
-
-  char* ws = static_cast<char*>(workspace);
-  float* resid[2] = {reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws) + (size_t)rows * dim};
-  ws += (size_t)2 * rows * dim * sizeof(float);
-  float* val[2] = {reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws) + (size_t)kMaxChunks * rows};
-  ws += (size_t)2 * kMaxChunks * rows * sizeof(float);
-  int* idx[2] = {reinterpret_cast<int*>(ws), reinterpret_cast<int*>(ws) + (size_t)kMaxChunks * rows};
-
-  const size_t lds = fast ? ((size_t)RB * (dim + 4) + RB + 2 * 4 * RB + 3 * 32 * (RB + 1) + ce) * 4
-                          : step_lds_bytes(dim);
-  if (lds > 64 * 1024) return FM_UNSUPPORTED;
+  const RvqPlan pl = rvq_plan(rows, dim, entries);
+  if (pl.lds > 64 * 1024) return FM_UNSUPPORTED;
+  const RvqBranch br = rvq_branch(x, ld_x, count, embeds, embeds_t, norms, codes, workspace, rows, dim);
+  const dim3 grid(pl.row_blocks, pl.chunks);
   for (int j = 0; j < count; ++j) {
-    StepArgs a{};
-    const int cur = j & 1, prev = cur ^ 1;
-    if (j == 0) {
-      a.resid_in = x;
-      a.ld_in = ld_x;
+    const StepArgs a = rvq_step_args(br, j, pl, rows, rows_per_batch, dim, entries, batch_stride);
+    int e;
+    if (!pl.fast) {
+      hipLaunchKernelGGL(rvq_step_kernel, grid, dim3(256), pl.lds, stream, a);
+      e = (int)hipGetLastError();
     } else {
-      a.resid_in = (j == 1) ? x : resid[prev];
-      a.ld_in = (j == 1) ? ld_x : dim;
-      a.prev_embed = embeds + (size_t)(j - 1) * entries * dim;
-      a.prev_val = val[prev];
-      a.prev_idx = idx[prev];
-      a.resid_out = resid[cur];
-      a.prev_codes = codes + (size_t)(j - 1) * rows_per_batch;
+      e = launch_fast_step(pl, dim, grid, a, br.embeds + (size_t)j * entries * dim, a, nullptr, stream);
     }
-    a.embed_t = embeds_t + (size_t)j * entries * dim;
-    a.norms = norms + (size_t)j * entries;
-    a.val = val[cur];
-    a.idx = idx[cur];
-    a.M = rows; a.dim = dim; a.entries = entries; a.chunk_entries = ce;
-    a.chunks = chunks; a.rows_per_batch = rows_per_batch; a.batch_stride = batch_stride;
-    const float* embed = embeds + (size_t)j * entries * dim;
-    const dim3 grid(row_blocks, chunks);
-#define FM_RVQ(D, K) hipLaunchKernelGGL((rvq_step_mfma_kernel<D, K>), grid, dim3(256), lds, stream, a, embed)
-    if (!fast) hipLaunchKernelGGL(rvq_step_kernel, grid, dim3(256), lds, stream, a);
-    else if (dim == 256 && kp == 4) FM_RVQ(256, 4);
-    else if (dim == 256 && kp == 2) FM_RVQ(256, 2);
-    else if (dim == 256) FM_RVQ(256, 1);
-    else if (dim == 128 && kp == 2) FM_RVQ(128, 2);
-    else if (dim == 128) FM_RVQ(128, 1);
-    else FM_RVQ(64, 1);
-#undef FM_RVQ
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return (int)e;
+    if (e != hipSuccess) return e;
   }
   const int last = (count - 1) & 1;
   hipLaunchKernelGGL(rvq_finalize_kernel, dim3((rows + 31) / 32), dim3(256), 0, stream,
-                     val[last], idx[last], chunks, rows,
+                     br.val[last], br.idx[last], pl.chunks, rows,
                      codes + (size_t)(count - 1) * rows_per_batch, rows_per_batch, batch_stride);
   return (int)hipGetLastError();
+}
+
+size_t fm_rvq_split_workspace_bytes(int rows, int dim, int entries) {
+  return 2 * fm_rvq_workspace_bytes(rows, dim, entries);
+}
+
+// Both branches of the split quantizer in shared launches: launch s runs
+// step s of every branch that still has one (blockIdx.z = branch) and
+// resolves the last codebook of a branch whose chain ended at s - 1.
+// x: semantic input in columns [0, dim), acoustic input in [dim, 2*dim).
+// Codebooks 0 .. n_semantic-1 are the semantic branch, the next n_acoustic
+// the acoustic one, all contiguous in embeds / embeds_t / norms.
+int fm_rvq_encode_split(const float* x, int ld_x, int rows, int rows_per_batch, int dim, int entries,
+                        int n_semantic, int n_acoustic, const float* embeds, const float* embeds_t,
+                        const float* norms, int64_t* codes, int batch_stride, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+  if (!rvq_args_ok(x, ld_x, rows, rows_per_batch, dim, entries, embeds, embeds_t, norms, codes) ||
+      n_semantic < 0 || n_acoustic < 0 || n_semantic + n_acoustic <= 0 || ld_x < 2 * dim)
+    return FM_BAD_ARGUMENT;
+  if (rows == 0) return FM_OK;
+  const size_t one = fm_rvq_workspace_bytes(rows, dim, entries);
+  if (!workspace || workspace_bytes < 2 * one) return FM_WORKSPACE_TOO_SMALL;
+  const size_t cb = (size_t)entries * dim;
+  char* ws = static_cast<char*>(workspace);
+  const bool fast = (dim == 64 || dim == 128 || dim == 256);
+  if (!fast || n_semantic == 0 || n_acoustic == 0) {
+    // One chain (or the general kernel): the branches run one after the other.
+    if (n_semantic > 0) {
+      const int e = fm_rvq_encode(x, ld_x, rows, rows_per_batch, dim, entries, n_semantic, embeds,
+                                  embeds_t, norms, codes, batch_stride, ws, one, stream);
+      if (e != FM_OK) return e;
+    }
+    if (n_acoustic > 0)
+      return fm_rvq_encode(x + dim, ld_x, rows, rows_per_batch, dim, entries, n_acoustic,
+                           embeds + n_semantic * cb, embeds_t + n_semantic * cb,
+                           norms + (size_t)n_semantic * entries,
+                           codes + (size_t)n_semantic * rows_per_batch, batch_stride, ws + one, one,
+                           stream);
+    return FM_OK;
+  }
+  const RvqPlan pl = rvq_plan(rows, dim, entries);
+  if (pl.lds > 64 * 1024) return FM_UNSUPPORTED;
+  RvqBranch br[2] = {
+      rvq_branch(x, ld_x, n_semantic, embeds, embeds_t, norms, codes, ws, rows, dim),
+      rvq_branch(x + dim, ld_x, n_acoustic, embeds + n_semantic * cb, embeds_t + n_semantic * cb,
+                 norms + (size_t)n_semantic * entries, codes + (size_t)n_semantic * rows_per_batch,
+                 ws + one, rows, dim)};
+  const int steps = std::max(n_semantic, n_acoustic);
+  for (int s = 0; s <= steps; ++s) {
+    // Branches active at launch s: step s (s < count) or the resolve of the last one (s == count).
+    int act[2], na = 0;
+    bool any_step = false;
+    for (int b = 0; b < 2; ++b)
+      if (s <= br[b].count) {
+        act[na++] = b;
+        any_step |= s < br[b].count;
+      }
+    if (na == 0) continue;
+    const StepArgs a0 = rvq_step_args(br[act[0]], s, pl, rows, rows_per_batch, dim, entries, batch_stride);
+    const StepArgs a1 = na > 1 ? rvq_step_args(br[act[1]], s, pl, rows, rows_per_batch, dim, entries, batch_stride) : a0;
+    const float* e0 = s < br[act[0]].count ? br[act[0]].embeds + (size_t)s * cb : nullptr;
+    const float* e1 = na > 1 && s < br[act[1]].count ? br[act[1]].embeds + (size_t)s * cb : nullptr;
+    const dim3 grid(pl.row_blocks, any_step ? pl.chunks : 1, na);
+    const int e = launch_fast_step(pl, dim, grid, a0, e0, a1, e1, stream);
+    if (e != hipSuccess) return e;
+  }
+  return FM_OK;
 }
 
 int fm_rvq_decode(const int64_t* codes, int batch, int num_codebooks, int frames,

@@ -60,6 +60,8 @@ _SIGNATURES = {
     "fm_rvq_prepare_codebook": ([_P, _P, _I, _I, _F, _P, _P, _P, _P], _I),
     "fm_rvq_workspace_bytes": ([_I, _I, _I], _S),
     "fm_rvq_encode": ([_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _S, _P], _I),
+    "fm_rvq_split_workspace_bytes": ([_I, _I, _I], _S),
+    "fm_rvq_encode_split": ([_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _S, _P], _I),
     "fm_rvq_decode": ([_P, _I, _I, _I, _I, _P, _I, _I, _P, _P], _I),
     "fm_upsample_depthwise": ([_P, _I, _I, _I, _P, _I, _I, _P, _P], _I),
     "fm_resblock_supported": ([_I], _I),

@@ -480,20 +480,14 @@ class MimiRuntime:
         proj = self._proj(h.reshape(M, cfg.hidden_size), M, self.w_in)
         self._tag = "rvq.encode"
         codes = torch.empty((B, nq, T), dtype=torch.int64, device=self.device)
-        ws_bytes = nat.library().fm_rvq_workspace_bytes(M, vq, cfg.codebook_size)
-        n_sem = cfg.num_semantic_quantizers
-        branches = [(0, 0, n_sem), (vq, n_sem, nq - n_sem)]
-        branches = [b for b in branches if b[2] > 0]
-        # The two branches run back to back on one stream: forking the
-        # semantic chain onto a second stream measured slower in the captured
-        # graph (cross-queue waits cost more than the overlap gains).
+        ws_bytes = nat.library().fm_rvq_split_workspace_bytes(M, vq, cfg.codebook_size)
+        n_sem = min(cfg.num_semantic_quantizers, nq)
+        # Both chains in shared launches (step s of each branch in one grid).
         ws = torch.empty((ws_bytes + 3) // 4, device=self.device)
-        s = self._stream()
-        for col, first, count in branches:
-            self._call("fm_rvq_encode", proj.data_ptr() + col * 4, 2 * vq, M, T, vq,
-                       cfg.codebook_size, count, self.embeds[first].data_ptr(),
-                       self.embeds_t[first].data_ptr(), self.norms[first].data_ptr(),
-                       codes.data_ptr() + first * T * 8, nq * T, ws.data_ptr(), ws_bytes, s)
+        self._call("fm_rvq_encode_split", proj.data_ptr(), 2 * vq, M, T, vq, cfg.codebook_size,
+                   n_sem, nq - n_sem, self.embeds.data_ptr(), self.embeds_t.data_ptr(),
+                   self.norms.data_ptr(), codes.data_ptr(), nq * T, ws.data_ptr(), ws_bytes,
+                   self._stream())
         return codes
 
     def decode(self, codes: torch.Tensor, out_length: int | None = None, kv_cache=None) -> torch.Tensor:

@@ -230,6 +230,25 @@ int fm_rvq_encode(const float* x, int ld_x, int rows, int rows_per_batch, int di
                   int64_t* codes, int batch_stride, void* workspace, size_t workspace_bytes,
                   hipStream_t stream);
 
+/* Bytes of workspace fm_rvq_encode_split needs (two branches' worth). */
+size_t fm_rvq_split_workspace_bytes(int rows, int dim, int entries);
+
+/*
+ * Split residual VQ encode: the semantic branch (codebooks 0..n_semantic-1,
+ * input columns [0, dim) of x) and the acoustic branch (the next n_acoustic
+ * codebooks, input columns [dim, 2*dim)) with the per-codebook rule of
+ * fm_rvq_encode.  The two chains share launches (step s of both branches in
+ * one grid), so the semantic chain adds no launches of its own.  ld_x >=
+ * 2*dim; embeds / embeds_t / norms hold all n_semantic + n_acoustic
+ * codebooks contiguously; codebook j's codes land at
+ * codes[b * batch_stride + j * rows_per_batch + t].
+ * Replaces MimiSplitResidualVectorQuantizer._encode_eager (model.py:2485-2501).
+ */
+int fm_rvq_encode_split(const float* x, int ld_x, int rows, int rows_per_batch, int dim, int entries,
+                        int n_semantic, int n_acoustic, const float* embeds, const float* embeds_t,
+                        const float* norms, int64_t* codes, int batch_stride, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+
 /*
  * Split-RVQ decode gather-sum: out[(b*frames + t)][0:dim] = 0 + E_0[c_0]
  * (the num_semantic first codebooks summed left to right),

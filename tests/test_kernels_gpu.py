@@ -556,6 +556,46 @@ def test_rvq_encode_matches_reference_loop(B, T, nq, e, d):
     assert n <= max(2, B * T * nq // 2000)
 
 
+@pytest.mark.parametrize("B,T,nsem,nac,e,d", [
+    (1, 125, 1, 7, 2048, 256),    # 32-entry chunks, 4 k-parts
+    (16, 125, 1, 7, 2048, 256),   # 128-entry chunks
+    (64, 125, 1, 31, 2048, 256),  # long acoustic chain
+    (3, 100, 2, 3, 1000, 128),    # ragged last chunk, two semantic codebooks
+    (2, 70, 1, 2, 100, 64),
+    (1, 33, 1, 0, 2048, 256),     # semantic only
+    (1, 33, 0, 3, 2048, 256),     # acoustic only
+    (2, 40, 1, 2, 48, 8),         # general kernel: branches one after the other
+])
+def test_rvq_encode_split_matches_two_branches(B, T, nsem, nac, e, d):
+    """Shared-launch split encode == the two branches encoded separately (bit-exact codes)."""
+    g = torch.Generator().manual_seed(B * T + nsem + nac + e + d)
+    n = nsem + nac
+    embed_sum = torch.randn(n, e, d, generator=g) / 16
+    emb, emb_t, norms = prepare_codebooks(embed_sum, torch.ones(n, e))
+    M = B * T
+    x = (torch.randn(M, 2 * d, generator=g) * 0.3).to(DEV)
+    lib = nat.library()
+    codes = torch.full((B, n, T), -1, dtype=torch.int64, device=DEV)
+    wsb = lib.fm_rvq_split_workspace_bytes(M, d, e)
+    ws = torch.empty((wsb + 3) // 4, device=DEV)
+    nat.call("fm_rvq_encode_split", x.data_ptr(), 2 * d, M, T, d, e, nsem, nac, emb.data_ptr(),
+             emb_t.data_ptr(), norms.data_ptr(), codes.data_ptr(), n * T, ws.data_ptr(), wsb, stream())
+    want = torch.full((B, n, T), -2, dtype=torch.int64, device=DEV)
+    wsb1 = lib.fm_rvq_workspace_bytes(M, d, e)
+    ws1 = torch.empty((wsb1 + 3) // 4, device=DEV)
+    for col, first, count in ((0, 0, nsem), (d, nsem, nac)):
+        if count == 0:
+            continue
+        nat.call("fm_rvq_encode", x.data_ptr() + col * 4, 2 * d, M, T, d, e, count,
+                 emb[first].data_ptr(), emb_t[first].data_ptr(), norms[first].data_ptr(),
+                 want.data_ptr() + first * T * 8, n * T, ws1.data_ptr(), wsb1, stream())
+    torch.cuda.synchronize()
+    assert torch.equal(codes.cpu(), want.cpu())
+    # Empty input is a no-op.
+    nat.call("fm_rvq_encode_split", x.data_ptr(), 2 * d, 0, T, d, e, nsem, nac, emb.data_ptr(),
+             emb_t.data_ptr(), norms.data_ptr(), codes.data_ptr(), n * T, ws.data_ptr(), wsb, stream())
+
+
 def test_rvq_tie_picks_lowest_index():
     e, d = 256, 256
     g = torch.Generator().manual_seed(9)
