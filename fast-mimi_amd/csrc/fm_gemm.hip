@@ -836,53 +836,64 @@ __global__ __launch_bounds__(256) void conv_cin1_kernel(const float* __restrict_
 }
 
 // Single-output-channel causal conv (the num_filters -> waveform last layer):
-// y[b, t] = bias + sum_{j, c} w[j*C + c] * act(x[b, t - pad + j, c]) for t < y_len.
-// Four threads per output position each sum a quarter of the channels (their
-// weights held in registers, all 16-byte input loads issued up front), then
-// the four partial sums combine in order.
+// y[b, t] = bias + sum_{j, c} w[j*C + c] * act(x[b, t - (K-1) + j, c]) for t < y_len.
+// Each input row is read once: a block stages rows t0-(K-1) .. t0+OUT-1 with
+// four threads per row (a quarter of the channels each, 16-byte loads), every
+// thread forms its row's contribution to all K taps, the four quarters combine
+// in order, and output t0+i sums tap j of row i+j over j through LDS.
 template <int C, int K>
 __global__ __launch_bounds__(256) void conv_cout1_kernel(const float* __restrict__ x, int L,
                                                          const float* __restrict__ w,
                                                          const float* __restrict__ bias,
                                                          int flags, int y_len,
                                                          float* __restrict__ y) {
-  constexpr int CQ = C / 4;  // channels per thread
+  constexpr int CQ = C / 4;            // channels per thread
+  constexpr int ROWS = 64;             // staged rows per block
+  constexpr int OUT = ROWS - (K - 1);  // outputs per block
+  __shared__ float D[ROWS][K];
   const long b = blockIdx.y;
-  const int t = blockIdx.x * 64 + threadIdx.x / 4;
-  const int part = threadIdx.x % 4;
+  const int t0 = blockIdx.x * OUT;
+  const int r = threadIdx.x / 4, part = threadIdx.x % 4;
+  const int tin = t0 - (K - 1) + r;
+  const bool ok = tin >= 0 && tin < L;
+  const float* row = x + (b * L + (ok ? tin : 0)) * (long)C + part * CQ;
+  floatx4 v[CQ / 4];
+#pragma unroll
+  for (int c = 0; c < CQ / 4; ++c)
+    v[c] = ok ? *reinterpret_cast<const floatx4*>(row + 4 * c) : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   float wr[K][CQ];
 #pragma unroll
   for (int j = 0; j < K; ++j)
 #pragma unroll
     for (int c = 0; c < CQ; ++c) wr[j][c] = w[j * C + part * CQ + c];
-  floatx4 v[K][CQ / 4];
+  if (flags & FM_ELU_IN) {
+#pragma unroll
+    for (int c = 0; c < CQ / 4; ++c) v[c] = floatx4{fm_elu(v[c].x), fm_elu(v[c].y), fm_elu(v[c].z), fm_elu(v[c].w)};
+  }
 #pragma unroll
   for (int j = 0; j < K; ++j) {
-    const int tin = t - (K - 1) + j;
-    const bool ok = t < y_len && tin >= 0 && tin < L;
-    const float* row = x + (b * L + (ok ? tin : 0)) * (long)C + part * CQ;
-#pragma unroll
-    for (int c = 0; c < CQ / 4; ++c)
-      v[j][c] = ok ? *reinterpret_cast<const floatx4*>(row + 4 * c) : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-  }
-  float acc = 0.0f;
-#pragma unroll
-  for (int j = 0; j < K; ++j)
+    float acc = 0.0f;
 #pragma unroll
     for (int c = 0; c < CQ / 4; ++c) {
-      floatx4 a = v[j][c];
-      if (flags & FM_ELU_IN) a = floatx4{fm_elu(a.x), fm_elu(a.y), fm_elu(a.z), fm_elu(a.w)};
-      acc = fmaf(wr[j][4 * c], a.x, acc);
-      acc = fmaf(wr[j][4 * c + 1], a.y, acc);
-      acc = fmaf(wr[j][4 * c + 2], a.z, acc);
-      acc = fmaf(wr[j][4 * c + 3], a.w, acc);
+      acc = fmaf(wr[j][4 * c], v[c].x, acc);
+      acc = fmaf(wr[j][4 * c + 1], v[c].y, acc);
+      acc = fmaf(wr[j][4 * c + 2], v[c].z, acc);
+      acc = fmaf(wr[j][4 * c + 3], v[c].w, acc);
     }
-  // Ordered combine of the four partial sums.
-  const float p1 = __shfl_down(acc, 1, 4), p2 = __shfl_down(acc, 2, 4), p3 = __shfl_down(acc, 3, 4);
-  if (part == 0 && t < y_len) {
-    float r = __fadd_rn(__fadd_rn(__fadd_rn(acc, p1), p2), p3);
-    if (bias) r = __fadd_rn(r, bias[0]);
-    y[b * y_len + t] = r;
+    // Ordered combine of the four quarters.
+    const float p1 = __shfl_down(acc, 1, 4), p2 = __shfl_down(acc, 2, 4), p3 = __shfl_down(acc, 3, 4);
+    if (part == 0) D[r][j] = __fadd_rn(__fadd_rn(__fadd_rn(acc, p1), p2), p3);
+  }
+  __syncthreads();
+  if (threadIdx.x < OUT) {
+    const int i = threadIdx.x, t = t0 + i;
+    if (t < y_len) {
+      float s = D[i][0];
+#pragma unroll
+      for (int j = 1; j < K; ++j) s = __fadd_rn(s, D[i + j][j]);
+      if (bias) s = __fadd_rn(s, bias[0]);
+      y[b * y_len + t] = s;
+    }
   }
 }
 
@@ -1039,7 +1050,7 @@ int fm_conv1d(const float* x, int batch, int length, int in_channels, const floa
     }
     if (out_channels == 1 && in_channels == 64 && kernel == 3 && !(p.flags & FM_EPI_ELU)) {
       if (y_length == 0) return FM_OK;
-      hipLaunchKernelGGL((conv_cout1_kernel<64, 3>), dim3((y_length + 63) / 64, batch), dim3(256), 0,
+      hipLaunchKernelGGL((conv_cout1_kernel<64, 3>), dim3((y_length + 61) / 62, batch), dim3(256), 0,
                          stream, x, length, weight_packed, bias, p.flags, y_length, y);
       return (int)hipGetLastError();
     }

@@ -100,6 +100,22 @@ def test_conv1d(B, cin, cout, k, stride, L, ws):
     close(got, want)
 
 
+@pytest.mark.parametrize("B,L,y_len", [(1, 1, 1), (2, 2, 2), (1, 62, 62), (2, 63, 60), (3, 999, 999),
+                                       (1, 240000, 240000), (2, 24001, 23995)])
+@pytest.mark.parametrize("elu_in", [0, 1])
+def test_conv1d_single_output_channel(B, L, y_len, elu_in, ws):
+    """The waveform layer (64 -> 1, k = 3): ELU on load, crop, block seams."""
+    g = torch.Generator().manual_seed(B * 7 + L + y_len)
+    x = torch.randn(B, 64, L, generator=g)
+    w = torch.randn(1, 64, 3, generator=g) / 8
+    b = torch.randn(1, generator=g) * 0.1
+    got = run_conv(x, w, b, 1, "constant", nat.ELU_IN if elu_in else 0, ws, y_len=y_len)
+    xin = F.elu(x.double()) if elu_in else x.double()
+    want = causal_conv1d(xin, w.double(), b.double())[..., :y_len]
+    assert got.shape == want.shape
+    close(got, want)
+
+
 @pytest.mark.parametrize("B,L", [(1, 250), (2, 7), (1, 1), (3, 64)])
 def test_conv1d_replicate(B, L, ws):
     g = torch.Generator().manual_seed(L)
