@@ -33,25 +33,36 @@ constexpr int NT = 256;
 // tile's memory and ELU work with the other's MFMAs.  MFMA k-slots: lane half
 // h at step 4q+e carries k = 96h + 4q + e (k3 conv, k = tap*64 + c_in) or
 // 16h + 4q + e (1x1 conv).
+// WAVE_IN: x is the 1-channel waveform [batch][L] and the block's input is
+// the encoder's first conv, x64[t][c] = b0[c] + sum_j w0[c][j] * wav[t-6+j]
+// (j = 0..6, zero outside the waveform; the FMA order of conv_cin1_kernel).
+// Each wave stages the 40 samples its tile needs and every lane forms its
+// input rows (ELU'd into the slot) and residual rows in registers, so the
+// 64-channel activation never goes through HBM.
 constexpr int R64_WAVES = 8;
 constexpr int R64_PE = 68;   // pitch of the ELU(x) / output tile rows
 constexpr int R64_PH = 36;   // pitch of the hidden tile rows
 constexpr int R64_SLOT = 34 * R64_PE + 32 * R64_PH;
 constexpr int R64_P1 = 196;  // W1^T row pitch (4 mod 32: conflict-free 16-byte reads)
 constexpr int R64_P2 = 36;   // W2^T row pitch
+constexpr int R64_WIN = 40;  // waveform samples per tile (WAVE_IN)
+constexpr int R64_WINP = 44; // their per-wave LDS pitch (reads reach index 41)
 
+template <bool WAVE_IN>
 __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
     const float* __restrict__ x, int batch, int L, const float* __restrict__ w1,
     const float* __restrict__ b1, const float* __restrict__ w2, const float* __restrict__ b2,
-    int elu_out, float* __restrict__ y) {
+    int elu_out, float* __restrict__ y, const float* __restrict__ w0, const float* __restrict__ b0) {
   constexpr int C = 64, HC = 32;
-  __shared__ __attribute__((aligned(16))) float smem[R64_WAVES * R64_SLOT + 32 * R64_P1 + 64 * R64_P2];
+  constexpr int WIN_F = WAVE_IN ? R64_WAVES * R64_WINP : 0;
+  __shared__ __attribute__((aligned(16))) float smem[R64_WAVES * R64_SLOT + 32 * R64_P1 + 64 * R64_P2 + WIN_F];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, lcol = lane & 31;
   float* E = smem + wave * R64_SLOT;   // [34][68] ELU(x); later the [32][68] output tile
   float* H = E + 34 * R64_PE;          // [32][36] hidden
   float* W1s = smem + R64_WAVES * R64_SLOT;
   float* W2s = W1s + 32 * R64_P1;
+  float* Win = W2s + 64 * R64_P2 + wave * R64_WINP;  // WAVE_IN: this wave's samples t0-8 .. t0+31
 
   for (int i = threadIdx.x; i < 32 * 48; i += 64 * R64_WAVES) {
     const int r = i / 48, c4 = (i % 48) * 4;
@@ -62,6 +73,17 @@ __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
     *reinterpret_cast<floatx4*>(W2s + r * R64_P2 + c4) = *reinterpret_cast<const floatx4*>(w2 + r * HC + c4);
   }
   const float bias1 = b1[lcol];
+  // WAVE_IN: the first conv's weights for this lane's four channels.
+  const int cg4 = (lane & 15) * 4, q = lane >> 4;
+  float w0r[4][7], b0r[4];
+  if constexpr (WAVE_IN) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      b0r[e] = b0[cg4 + e];
+#pragma unroll
+      for (int j = 0; j < 7; ++j) w0r[e][j] = w0[(cg4 + e) * 7 + j];
+    }
+  }
   __syncthreads();
 
   const int tpb = (L + 31) / 32;
@@ -72,8 +94,14 @@ __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
   // x rows t0-2 .. t0+31 of a tile: 544 float4 chunks, 9 per lane (chunk c = lane + 64u).
   floatx4 xv[9];
   unsigned xok = 0;
+  float wv = 0.0f;  // WAVE_IN: sample t0 - 8 + lane of the tile (lanes < 40)
   auto load_x = [&](long tl) {
     const int b = (int)(tl / tpb), t0 = (int)(tl % tpb) * 32;
+    if constexpr (WAVE_IN) {
+      const int t = t0 - 8 + lane;
+      wv = (lane < R64_WIN && t >= 0 && t < L) ? x[(long)b * L + t] : 0.0f;
+      return;
+    }
     const float* xb = x + (long)b * L * C;
     xok = 0;
 #pragma unroll
@@ -88,25 +116,60 @@ __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
   if (tile < tiles) load_x(tile);
   for (; tile < tiles; tile += stride) {
     const int b = (int)(tile / tpb), t0 = (int)(tile % tpb) * 32;
-    const float* xb = x + (long)b * L * C;
-    // ELU(x) into the slot (zero outside the sequence: the causal zero padding).
-#pragma unroll
-    for (int u = 0; u < 9; ++u) {
-      const int c = lane + 64 * u;
-      if (c >= 544) continue;
-      floatx4 v = ((xok >> u) & 1) ? xv[u] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-      *reinterpret_cast<floatx4*>(E + (c / 16) * R64_PE + (c % 16) * 4) =
-          floatx4{fm_elu(v[0]), fm_elu(v[1]), fm_elu(v[2]), fm_elu(v[3])};
-    }
-    // Raw residual rows t0 .. t0+31 (chunk c = lane + 64u, 8 per lane) and the
-    // next tile's input rows: both in flight during this tile's MFMAs.
     floatx4 rv[8];
+    if constexpr (WAVE_IN) {
+      // Samples t0-8 .. t0+31 into the wave's window; lane (q, cg) then needs
+      // samples q .. q+38 of it.  Staged row rr (t = t0-2+rr) reads
+      // window[rr .. rr+6]; the lane forms rows rr = q + 4u + 2 (u < 8: the
+      // block's own rows t0 + q + 4u, which are also its residual rows) and,
+      // for q < 2, the causal halo row rr = q.
+      if (lane < R64_WIN) Win[lane] = wv;
+      wave_lds_fence();
+      if (tile + stride < tiles) load_x(tile + stride);
+      float s[39];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int c = lane + 64 * u;
-      rv[u] = *reinterpret_cast<const floatx4*>(xb + (long)min(t0 + c / 16, L - 1) * C + (c % 16) * 4);
+      for (int i = 0; i < 39; ++i) s[i] = Win[q + i];
+      auto conv0 = [&](int base) {
+        floatx4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float acc = b0r[e];
+#pragma unroll
+          for (int j = 0; j < 7; ++j) acc = fmaf(w0r[e][j], s[base + j], acc);
+          v[e] = acc;
+        }
+        return v;
+      };
+      auto stage = [&](int rr, floatx4 v) {
+        *reinterpret_cast<floatx4*>(E + rr * R64_PE + cg4) =
+            floatx4{fm_elu(v[0]), fm_elu(v[1]), fm_elu(v[2]), fm_elu(v[3])};
+      };
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        rv[u] = conv0(4 * u + 2);
+        stage(q + 4 * u + 2, t0 + q + 4 * u < L ? rv[u] : floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+      }
+      if (q < 2) stage(q, t0 - 2 + q >= 0 ? conv0(0) : floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+    } else {
+      const float* xb = x + (long)b * L * C;
+      // ELU(x) into the slot (zero outside the sequence: the causal zero padding).
+#pragma unroll
+      for (int u = 0; u < 9; ++u) {
+        const int c = lane + 64 * u;
+        if (c >= 544) continue;
+        floatx4 v = ((xok >> u) & 1) ? xv[u] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        *reinterpret_cast<floatx4*>(E + (c / 16) * R64_PE + (c % 16) * 4) =
+            floatx4{fm_elu(v[0]), fm_elu(v[1]), fm_elu(v[2]), fm_elu(v[3])};
+      }
+      // Raw residual rows t0 .. t0+31 (chunk c = lane + 64u, 8 per lane) and the
+      // next tile's input rows: both in flight during this tile's MFMAs.
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int c = lane + 64 * u;
+        rv[u] = *reinterpret_cast<const floatx4*>(xb + (long)min(t0 + c / 16, L - 1) * C + (c % 16) * 4);
+      }
+      if (tile + stride < tiles) load_x(tile + stride);
     }
-    if (tile + stride < tiles) load_x(tile + stride);
     wave_lds_fence();
 
     // k3 conv: rows = positions, columns = hidden channels; two chains.
@@ -344,8 +407,8 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
     // Persistent: one 8-wave block per CU (LDS-bound), waves stride over 32-row tiles.
     const long tiles = (long)batch * ((length + 31) / 32);
     const int blocks = (int)std::min<long>((tiles + R64_WAVES - 1) / R64_WAVES, 256);
-    hipLaunchKernelGGL(resblock64_kernel, dim3(blocks), dim3(64 * R64_WAVES), 0, stream, x, batch,
-                       length, w1_packed, b1, w2_packed, b2, elu_out, y);
+    hipLaunchKernelGGL(resblock64_kernel<false>, dim3(blocks), dim3(64 * R64_WAVES), 0, stream, x,
+                       batch, length, w1_packed, b1, w2_packed, b2, elu_out, y, nullptr, nullptr);
   } else if (channels == 128) {
     hipLaunchKernelGGL((resblock_direct_kernel<128, 64, 2, 3>), dim3((length + 63) / 64, batch), dim3(NT),
                        0, stream, x, length, w1_packed, b1, w2_packed, b2, elu_out, y);
@@ -353,6 +416,23 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
     hipLaunchKernelGGL((resblock_direct_kernel<256, 32, 1, 3>), dim3((length + 31) / 32, batch), dim3(NT),
                        0, stream, x, length, w1_packed, b1, w2_packed, b2, elu_out, y);
   }
+  return (int)hipGetLastError();
+}
+
+// The encoder's first conv (1 -> 64 channels, kernel 7, causal) fused into
+// the residual block that follows it: y = block(conv(wav)).
+int fm_conv_resblock64(const float* wav, int batch, int length, const float* w0_packed,
+                       const float* b0, const float* w1_packed, const float* b1,
+                       const float* w2_packed, const float* b2, int elu_out, float* y,
+                       hipStream_t stream) {
+  if (!wav || !w0_packed || !b0 || !w1_packed || !b1 || !w2_packed || !b2 || !y || batch < 0 ||
+      length < 0)
+    return FM_BAD_ARGUMENT;
+  if (batch == 0 || length == 0) return FM_OK;
+  const long tiles = (long)batch * ((length + 31) / 32);
+  const int blocks = (int)std::min<long>((tiles + R64_WAVES - 1) / R64_WAVES, 256);
+  hipLaunchKernelGGL(resblock64_kernel<true>, dim3(blocks), dim3(64 * R64_WAVES), 0, stream, wav,
+                     batch, length, w1_packed, b1, w2_packed, b2, elu_out, y, w0_packed, b0);
   return (int)hipGetLastError();
 }
 

@@ -66,6 +66,7 @@ _SIGNATURES = {
     "fm_upsample_depthwise": ([_P, _I, _I, _I, _P, _I, _I, _P, _P], _I),
     "fm_resblock_supported": ([_I], _I),
     "fm_resblock": ([_P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P], _I),
+    "fm_conv_resblock64": ([_P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P], _I),
 }
 
 _lock = threading.Lock()

@@ -363,11 +363,24 @@ class MimiRuntime:
         return self.quantize(h, B, L, num_quantizers)
 
     def _encoder_seanet(self, x, B, S):
-        self._tag = "enc.first"
-        h, L = self._conv(x, B, S, self.enc_first)
         n = len(self.enc_stages)
+        first, (c1, c2) = self.enc_first, self.enc_stages[0][0]
+        if (first.c_in == 1 and first.k == 7 and first.stride == 1 and first.c_out == 64
+                and not first.replicate and c1.k == 3 and c2.c_out == 64 and first.b is not None):
+            # The first conv is formed inside the first residual block.
+            self._tag = "enc.first+res64"
+            h = torch.empty((B, S, 64), device=self.device)
+            self._call("fm_conv_resblock64", x.data_ptr(), B, S, first.w.data_ptr(),
+                       first.b.data_ptr(), c1.w.data_ptr(), c1.b.data_ptr(), c2.w.data_ptr(),
+                       c2.b.data_ptr(), 1, h.data_ptr(), self._stream())
+            L, start = S, 1
+        else:
+            self._tag = "enc.first"
+            h, L = self._conv(x, B, S, self.enc_first)
+            start = 0
         for i, (block, down) in enumerate(self.enc_stages):
-            h = self._resblock(h, B, L, block, elu_after=True, tag=f"enc.res{down.c_in}")
+            if i >= start:
+                h = self._resblock(h, B, L, block, elu_after=True, tag=f"enc.res{down.c_in}")
             self._tag = f"enc.down{down.stride}"
             h, L = self._conv(h, B, L, down, nat.EPI_ELU if i == n - 1 else 0)
         self._tag = "enc.last"

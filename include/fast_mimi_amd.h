@@ -112,6 +112,19 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
                 hipStream_t stream);
 
 /*
+ * The SEANet encoder's first conv (1 -> 64 channels, kernel 7, causal, no
+ * activation) fused into the 64-channel residual block after it:
+ * y = fm_resblock(conv(wav)), wav [batch][length], y [batch][length][64].
+ * w0_packed is the conv's packed [64][7] weight.  The 64-channel conv output
+ * is formed on chip and never stored.
+ * Replaces MimiEncoder layers.0 + layers.1 (model.py:1013-1031).
+ */
+int fm_conv_resblock64(const float* wav, int batch, int length, const float* w0_packed,
+                       const float* b0, const float* w1_packed, const float* b1,
+                       const float* w2_packed, const float* b2, int elu_out, float* y,
+                       hipStream_t stream);
+
+/*
  * Transformer projection y[rows][out] = epilogue(LN?(x) . W^T), no bias:
  *   - ln_gamma/ln_beta non-NULL: x rows are layer-normalised (biased variance,
  *     eps ln_eps) inside the kernel first;

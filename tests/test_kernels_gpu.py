@@ -191,6 +191,42 @@ def test_fused_resblock(B, C, L, elu_out):
     close(y.cpu().transpose(1, 2), want, rel=5e-5)
 
 
+@pytest.mark.parametrize("B,L", [(1, 240000), (2, 1001), (1, 1), (3, 33), (1, 31), (2, 32), (1, 70000)])
+@pytest.mark.parametrize("elu_out", [1, 0])
+def test_conv_resblock64_equals_conv_then_block(B, L, elu_out, ws):
+    """fm_conv_resblock64 == fm_conv1d (1 -> 64, k 7) then fm_resblock, bit for bit."""
+    g = torch.Generator().manual_seed(B * 31 + L)
+    wav = torch.randn(B, 1, L, generator=g) * 0.5
+    w0 = torch.randn(64, 1, 7, generator=g) / 3
+    b0 = torch.randn(64, generator=g) * 0.1
+    w1 = torch.randn(32, 64, 3, generator=g) / math.sqrt(192)
+    b1 = torch.randn(32, generator=g) * 0.1
+    w2 = torch.randn(64, 32, 1, generator=g) / math.sqrt(32)
+    b2 = torch.randn(64, generator=g) * 0.1
+    c0 = _Conv(w0.to(DEV), b0.to(DEV))
+    c1, c2 = _Conv(w1.to(DEV), b1.to(DEV)), _Conv(w2.to(DEV), b2.to(DEV))
+    wd = wav.reshape(B, L).contiguous().to(DEV)
+    h = torch.empty(B, L, 64, device=DEV)
+    nat.call("fm_conv1d", wd.data_ptr(), B, L, 1, c0.w.data_ptr(), c0.b.data_ptr(), 64, 7, 1, 0, 0,
+             None, h.data_ptr(), L, ws.data_ptr(), WS_BYTES, stream())
+    want = torch.empty_like(h)
+    nat.call("fm_resblock", h.data_ptr(), B, L, 64, c1.w.data_ptr(), c1.b.data_ptr(), c2.w.data_ptr(),
+             c2.b.data_ptr(), elu_out, want.data_ptr(), stream())
+    got = torch.full_like(h, float("nan"))
+    nat.call("fm_conv_resblock64", wd.data_ptr(), B, L, c0.w.data_ptr(), c0.b.data_ptr(),
+             c1.w.data_ptr(), c1.b.data_ptr(), c2.w.data_ptr(), c2.b.data_ptr(), elu_out,
+             got.data_ptr(), stream())
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    if L <= 2000:  # and against the float64 reference of the two layers
+        x64 = causal_conv1d(wav.double(), w0.double(), b0.double())
+        hid = F.elu(causal_conv1d(F.elu(x64), w1.double(), b1.double()))
+        ref = x64 + causal_conv1d(hid, w2.double(), b2.double())
+        if elu_out:
+            ref = F.elu(ref)
+        close(got.cpu().transpose(1, 2), ref, rel=5e-5)
+
+
 def test_conv1d_crop(ws):
     g = torch.Generator().manual_seed(5)
     x = torch.randn(2, 8, 100, generator=g)
