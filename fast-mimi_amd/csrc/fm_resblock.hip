@@ -39,6 +39,10 @@ constexpr int NT = 256;
 // Each wave stages the 40 samples its tile needs and every lane forms its
 // input rows (ELU'd into the slot) and residual rows in registers, so the
 // 64-channel activation never goes through HBM.
+// WAVE_OUT: the block feeds the decoder's last conv (64 -> 1, kernel 3): the
+// output rows go back into the slot and each row's three tap dot products
+// w3[j] . y[t] are stored (float4 per row, D[b][t] = {d0, d1, d2, 0}) instead
+// of y; conv3_finish_kernel then sums the taps of rows t-2, t-1, t.
 constexpr int R64_WAVES = 8;
 constexpr int R64_PE = 68;   // pitch of the ELU(x) / output tile rows
 constexpr int R64_PH = 36;   // pitch of the hidden tile rows
@@ -48,14 +52,15 @@ constexpr int R64_P2 = 36;   // W2^T row pitch
 constexpr int R64_WIN = 40;  // waveform samples per tile (WAVE_IN)
 constexpr int R64_WINP = 44; // their per-wave LDS pitch (reads reach index 41)
 
-template <bool WAVE_IN>
+template <bool WAVE_IN, bool WAVE_OUT>
 __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
     const float* __restrict__ x, int batch, int L, const float* __restrict__ w1,
     const float* __restrict__ b1, const float* __restrict__ w2, const float* __restrict__ b2,
     int elu_out, float* __restrict__ y, const float* __restrict__ w0, const float* __restrict__ b0) {
   constexpr int C = 64, HC = 32;
   constexpr int WIN_F = WAVE_IN ? R64_WAVES * R64_WINP : 0;
-  __shared__ __attribute__((aligned(16))) float smem[R64_WAVES * R64_SLOT + 32 * R64_P1 + 64 * R64_P2 + WIN_F];
+  constexpr int W3_F = WAVE_OUT ? 3 * 64 : 0;
+  __shared__ __attribute__((aligned(16))) float smem[R64_WAVES * R64_SLOT + 32 * R64_P1 + 64 * R64_P2 + WIN_F + W3_F];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, lcol = lane & 31;
   float* E = smem + wave * R64_SLOT;   // [34][68] ELU(x); later the [32][68] output tile
@@ -63,6 +68,10 @@ __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
   float* W1s = smem + R64_WAVES * R64_SLOT;
   float* W2s = W1s + 32 * R64_P1;
   float* Win = W2s + 64 * R64_P2 + wave * R64_WINP;  // WAVE_IN: this wave's samples t0-8 .. t0+31
+  float* W3s = W2s + 64 * R64_P2 + WIN_F;             // WAVE_OUT: w3 [3][64] (w0 carries it)
+  if constexpr (WAVE_OUT) {
+    if (threadIdx.x < 3 * 64) W3s[threadIdx.x] = w0[threadIdx.x];
+  }
 
   for (int i = threadIdx.x; i < 32 * 48; i += 64 * R64_WAVES) {
     const int r = i / 48, c4 = (i % 48) * 4;
@@ -76,7 +85,7 @@ __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
   // WAVE_IN: the first conv's weights for this lane's four channels.
   const int cg4 = (lane & 15) * 4, q = lane >> 4;
   float w0r[4][7], b0r[4];
-  if constexpr (WAVE_IN) {
+  if constexpr (WAVE_IN && !WAVE_OUT) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       b0r[e] = b0[cg4 + e];
@@ -226,10 +235,54 @@ __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
         v[e] = __fadd_rn(rv[u][e], __fadd_rn(acc[e], bb[e]));
         if (elu_out) v[e] = fm_elu(v[e]);
       }
-      if (t0 + r < L) *reinterpret_cast<floatx4*>(yb + (long)(t0 + r) * C + c4) = v;
+      if constexpr (WAVE_OUT) {
+        *reinterpret_cast<floatx4*>(E + r * R64_PE + c4) = v;
+      } else {
+        if (t0 + r < L) *reinterpret_cast<floatx4*>(yb + (long)(t0 + r) * C + c4) = v;
+      }
+    }
+    if constexpr (WAVE_OUT) {
+      // Row r = lane % 32, channel half hh = lane / 32: the three tap dot
+      // products over 32 channels, then half 0 + half 1.
+      wave_lds_fence();
+      const int r = lane & 31, hh = lane >> 5;
+      float d[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < 32; c += 4) {
+        const floatx4 v = *reinterpret_cast<const floatx4*>(E + r * R64_PE + 32 * hh + c);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          const floatx4 wj = *reinterpret_cast<const floatx4*>(W3s + j * 64 + 32 * hh + c);
+          d[j] = fmaf(wj[0], v[0], d[j]);
+          d[j] = fmaf(wj[1], v[1], d[j]);
+          d[j] = fmaf(wj[2], v[2], d[j]);
+          d[j] = fmaf(wj[3], v[3], d[j]);
+        }
+      }
+      floatx4 o;
+#pragma unroll
+      for (int j = 0; j < 3; ++j) o[j] = __fadd_rn(d[j], __shfl_xor(d[j], 32, 64));
+      o[3] = 0.0f;
+      if (hh == 0 && t0 + r < L) *reinterpret_cast<floatx4*>(y + ((long)b * L + t0 + r) * 4) = o;
     }
     wave_lds_fence();  // the slot is rewritten by the next tile
   }
+}
+
+// out[b][t] = ((d0[t-2] + d1[t-1]) + d2[t]) + bias for t < y_len, with the
+// per-row tap products D of resblock64_kernel<*, true> (rows < 0 are zero).
+__global__ __launch_bounds__(256) void conv3_finish_kernel(const float* __restrict__ D, int L,
+                                                           int y_len, const float* __restrict__ bias,
+                                                           float* __restrict__ out) {
+  const long b = blockIdx.y;
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= y_len) return;
+  const float* Db = D + b * (long)L * 4;
+  const float d0 = t >= 2 ? Db[(long)(t - 2) * 4 + 0] : 0.0f;
+  const float d1 = t >= 1 ? Db[(long)(t - 1) * 4 + 1] : 0.0f;
+  float s = __fadd_rn(__fadd_rn(d0, d1), Db[(long)t * 4 + 2]);
+  if (bias) s = __fadd_rn(s, bias[0]);
+  out[b * y_len + t] = s;
 }
 
 // ---------------------------------------------------------------------------
@@ -407,7 +460,7 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
     // Persistent: one 8-wave block per CU (LDS-bound), waves stride over 32-row tiles.
     const long tiles = (long)batch * ((length + 31) / 32);
     const int blocks = (int)std::min<long>((tiles + R64_WAVES - 1) / R64_WAVES, 256);
-    hipLaunchKernelGGL(resblock64_kernel<false>, dim3(blocks), dim3(64 * R64_WAVES), 0, stream, x,
+    hipLaunchKernelGGL((resblock64_kernel<false, false>), dim3(blocks), dim3(64 * R64_WAVES), 0, stream, x,
                        batch, length, w1_packed, b1, w2_packed, b2, elu_out, y, nullptr, nullptr);
   } else if (channels == 128) {
     hipLaunchKernelGGL((resblock_direct_kernel<128, 64, 2, 3>), dim3((length + 63) / 64, batch), dim3(NT),
@@ -431,8 +484,37 @@ int fm_conv_resblock64(const float* wav, int batch, int length, const float* w0_
   if (batch == 0 || length == 0) return FM_OK;
   const long tiles = (long)batch * ((length + 31) / 32);
   const int blocks = (int)std::min<long>((tiles + R64_WAVES - 1) / R64_WAVES, 256);
-  hipLaunchKernelGGL(resblock64_kernel<true>, dim3(blocks), dim3(64 * R64_WAVES), 0, stream, wav,
+  hipLaunchKernelGGL((resblock64_kernel<true, false>), dim3(blocks), dim3(64 * R64_WAVES), 0, stream, wav,
                      batch, length, w1_packed, b1, w2_packed, b2, elu_out, y, w0_packed, b0);
+  return (int)hipGetLastError();
+}
+
+// The decoder's last 64-channel residual block fused with the waveform conv
+// after it (64 -> 1 channel, kernel 3, causal): out = conv(block(x)) cropped
+// to y_len rows.  workspace: fm_resblock64_conv_workspace_bytes.
+size_t fm_resblock64_conv_workspace_bytes(int batch, int length) {
+  return (size_t)batch * length * 4 * sizeof(float);
+}
+
+int fm_resblock64_conv(const float* x, int batch, int length, const float* w1_packed,
+                       const float* b1, const float* w2_packed, const float* b2, int elu_mid,
+                       const float* w3_packed, const float* b3, int y_len, float* out,
+                       float* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!x || !w1_packed || !b1 || !w2_packed || !b2 || !w3_packed || !out || batch < 0 ||
+      length < 0 || y_len < 0 || y_len > length)
+    return FM_BAD_ARGUMENT;
+  if (batch == 0 || y_len == 0) return FM_OK;
+  if (!workspace || workspace_bytes < fm_resblock64_conv_workspace_bytes(batch, length))
+    return FM_WORKSPACE_TOO_SMALL;
+  const long tiles = (long)batch * ((length + 31) / 32);
+  const int blocks = (int)std::min<long>((tiles + R64_WAVES - 1) / R64_WAVES, 256);
+  hipLaunchKernelGGL((resblock64_kernel<false, true>), dim3(blocks), dim3(64 * R64_WAVES), 0, stream,
+                     x, batch, length, w1_packed, b1, w2_packed, b2, elu_mid, workspace, w3_packed,
+                     nullptr);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(conv3_finish_kernel, dim3((y_len + 255) / 256, batch), dim3(256), 0, stream,
+                     workspace, length, y_len, b3, out);
   return (int)hipGetLastError();
 }
 

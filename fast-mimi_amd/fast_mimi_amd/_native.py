@@ -67,6 +67,8 @@ _SIGNATURES = {
     "fm_resblock_supported": ([_I], _I),
     "fm_resblock": ([_P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P], _I),
     "fm_conv_resblock64": ([_P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P], _I),
+    "fm_resblock64_conv_workspace_bytes": ([_I, _I], _S),
+    "fm_resblock64_conv": ([_P, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _S, _P], _I),
 }
 
 _lock = threading.Lock()

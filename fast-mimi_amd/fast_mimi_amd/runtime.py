@@ -256,6 +256,14 @@ class MimiRuntime:
                    rope_cols, per_seq, y.data_ptr(), self._stream())
         return y
 
+    def _fuse_last(self, block) -> bool:
+        """The decoder's last residual block and waveform conv run as one
+        kernel pair when they have the SEANet shapes (64 channels, k = 3)."""
+        c1, c2 = block
+        last = self.dec_last
+        return (c1.k == 3 and c2.c_out == 64 and last.c_in == 64 and last.c_out == 1
+                and last.k == 3 and last.stride == 1 and not last.replicate)
+
     def _resblock(self, x, B, L, block, elu_after: bool, tag: str = "res"):
         c1, c2 = block
         # The fused kernel (hidden tile kept on chip) covers the SEANet widths;
@@ -534,6 +542,20 @@ class MimiRuntime:
         for i, (convt, block) in enumerate(self.dec_stages):
             self._tag = f"dec.up{convt.stride}"
             h, L = self._convt(h, B, L, convt)
+            c1, c2 = block
+            if i == n - 1 and self._fuse_last(block):
+                # The last block feeds the waveform conv on chip.
+                full = L
+                out_length = full if out_length is None else min(out_length, full)
+                self._tag = "dec.res64+last"
+                lib = nat.library()
+                d = torch.empty((lib.fm_resblock64_conv_workspace_bytes(B, L) + 3) // 4, device=self.device)
+                y = torch.empty((B, out_length), device=self.device)
+                last = self.dec_last
+                self._call("fm_resblock64_conv", h.data_ptr(), B, L, c1.w.data_ptr(), c1.b.data_ptr(),
+                           c2.w.data_ptr(), c2.b.data_ptr(), 1, last.w.data_ptr(), _ptr(last.b),
+                           out_length, y.data_ptr(), d.data_ptr(), d.numel() * 4, self._stream())
+                return y.view(B, 1, out_length)
             h = self._resblock(h, B, L, block, elu_after=True, tag=f"dec.res{convt.c_out}")
         full = L
         out_length = full if out_length is None else min(out_length, full)

@@ -125,6 +125,23 @@ int fm_conv_resblock64(const float* wav, int batch, int length, const float* w0_
                        hipStream_t stream);
 
 /*
+ * The SEANet decoder's last 64-channel residual block (ELU after it when
+ * elu_mid != 0) fused with the waveform conv after it (64 -> 1 channel,
+ * kernel 3, causal): out[b][t] = b3 + sum_j w3[j] . block(x)[b][t-2+j] for
+ * t < y_len, out [batch][y_len].  w3_packed is the conv's packed [3][64]
+ * weight (b3 may be NULL).  The 64-channel block output is reduced on chip
+ * to three tap products per row (the workspace,
+ * fm_resblock64_conv_workspace_bytes) and never stored.
+ * Replaces MimiDecoder's last MimiResnetBlock + ELU + MimiConv1d
+ * (model.py:1269-1285).
+ */
+size_t fm_resblock64_conv_workspace_bytes(int batch, int length);
+int fm_resblock64_conv(const float* x, int batch, int length, const float* w1_packed,
+                       const float* b1, const float* w2_packed, const float* b2, int elu_mid,
+                       const float* w3_packed, const float* b3, int y_len, float* out,
+                       float* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/*
  * Transformer projection y[rows][out] = epilogue(LN?(x) . W^T), no bias:
  *   - ln_gamma/ln_beta non-NULL: x rows are layer-normalised (biased variance,
  *     eps ln_eps) inside the kernel first;

@@ -227,6 +227,47 @@ def test_conv_resblock64_equals_conv_then_block(B, L, elu_out, ws):
         close(got.cpu().transpose(1, 2), ref, rel=5e-5)
 
 
+@pytest.mark.parametrize("B,L,y_len", [(1, 240000, 240000), (2, 1001, 990), (1, 1, 1), (3, 33, 33),
+                                       (1, 31, 2), (2, 32, 32), (1, 70000, 69999)])
+def test_resblock64_conv_matches_reference(B, L, y_len):
+    """fm_resblock64_conv == block (ELU after) then the 64 -> 1, k = 3 conv, cropped."""
+    g = torch.Generator().manual_seed(B * 17 + L + y_len)
+    x = torch.randn(B, 64, L, generator=g)
+    w1 = torch.randn(32, 64, 3, generator=g) / math.sqrt(192)
+    b1 = torch.randn(32, generator=g) * 0.1
+    w2 = torch.randn(64, 32, 1, generator=g) / math.sqrt(32)
+    b2 = torch.randn(64, generator=g) * 0.1
+    w3 = torch.randn(1, 64, 3, generator=g) / 8
+    b3 = torch.randn(1, generator=g) * 0.1
+    c1, c2, c3 = _Conv(w1.to(DEV), b1.to(DEV)), _Conv(w2.to(DEV), b2.to(DEV)), _Conv(w3.to(DEV), b3.to(DEV))
+    xd = x.transpose(1, 2).contiguous().to(DEV)
+    lib = nat.library()
+    wsb = lib.fm_resblock64_conv_workspace_bytes(B, L)
+    d = torch.empty((wsb + 3) // 4, device=DEV)
+    out = torch.full((B, y_len), float("nan"), device=DEV)
+    nat.call("fm_resblock64_conv", xd.data_ptr(), B, L, c1.w.data_ptr(), c1.b.data_ptr(), c2.w.data_ptr(),
+             c2.b.data_ptr(), 1, c3.w.data_ptr(), c3.b.data_ptr(), y_len, out.data_ptr(), d.data_ptr(),
+             wsb, stream())
+    torch.cuda.synchronize()
+    if L <= 2000:
+        x64 = x.double()
+        hid = F.elu(causal_conv1d(F.elu(x64), w1.double(), b1.double()))
+        blk = F.elu(x64 + causal_conv1d(hid, w2.double(), b2.double()))
+        want = causal_conv1d(blk, w3.double(), b3.double())[..., :y_len]
+        close(out.cpu().view(B, 1, y_len), want, rel=5e-5)
+    else:  # long inputs: against the two separate kernels
+        h = torch.empty_like(xd)
+        nat.call("fm_resblock", xd.data_ptr(), B, L, 64, c1.w.data_ptr(), c1.b.data_ptr(),
+                 c2.w.data_ptr(), c2.b.data_ptr(), 1, h.data_ptr(), stream())
+        ws = torch.empty(WS_BYTES // 4, device=DEV)
+        ref = torch.empty(B, y_len, 1, device=DEV)
+        nat.call("fm_conv1d", h.data_ptr(), B, L, 64, c3.w.data_ptr(), c3.b.data_ptr(), 1, 3, 1, 0, 0,
+                 None, ref.data_ptr(), y_len, ws.data_ptr(), WS_BYTES, stream())
+        torch.cuda.synchronize()
+        err = (out.cpu() - ref.cpu().view(B, y_len)).abs().max().item()
+        assert err <= 1e-5 * max(1.0, ref.abs().max().item()), err
+
+
 def test_conv1d_crop(ws):
     g = torch.Generator().manual_seed(5)
     x = torch.randn(2, 8, 100, generator=g)
