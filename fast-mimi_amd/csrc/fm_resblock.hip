@@ -23,16 +23,16 @@ constexpr int NT = 256;
 // ---------------------------------------------------------------------------
 // C = 64 residual block as a persistent kernel.  The block's weights are
 // staged once in LDS as MFMA B-fragment rows (W1^T [32][192], W2^T [64][32]),
-// shared by the 8 waves.  Each wave then takes 32-row tiles in a grid-stride
+// shared by the 12 waves.  Each wave then takes 32-row tiles in a grid-stride
 // loop with no block-level barrier: stage ELU(x) rows t0-2 .. t0+31 in its own
-// LDS slot, issue the residual rows of this tile and the input rows of its
-// next tile (both land during the MFMAs), k3 conv (96 MFMAs in two chains,
-// taps as row-shifted views), hidden = ELU(acc + b1) into LDS, 1x1 conv (32
-// MFMAs), then the output tile goes back through LDS so the epilogue (bias,
-// raw residual, ELU) runs on float4 runs.  Two waves per SIMD overlap one
-// tile's memory and ELU work with the other's MFMAs.  MFMA k-slots: lane half
-// h at step 4q+e carries k = 96h + 4q + e (k3 conv, k = tap*64 + c_in) or
-// 16h + 4q + e (1x1 conv).
+// LDS slot, issue the residual rows of this tile (they land during the
+// MFMAs), k3 conv (96 MFMAs in two chains, taps as row-shifted views), hidden
+// = ELU(acc + b1) into the same slot, 1x1 conv (32 MFMAs), then the output
+// tile goes back through the slot so the epilogue (bias, raw residual, ELU)
+// runs on float4 runs.  One 9 KB slot per wave keeps three waves per SIMD,
+// which overlap one tile's memory and ELU work with the others' MFMAs.
+// MFMA k-slots: lane half h at step 4q+e carries k = 96h + 4q + e (k3 conv,
+// k = tap*64 + c_in) or 16h + 4q + e (1x1 conv).
 // WAVE_IN: x is the 1-channel waveform [batch][L] and the block's input is
 // the encoder's first conv, x64[t][c] = b0[c] + sum_j w0[c][j] * wav[t-6+j]
 // (j = 0..6, zero outside the waveform; the FMA order of conv_cin1_kernel).
@@ -43,10 +43,10 @@ constexpr int NT = 256;
 // output rows go back into the slot and each row's three tap dot products
 // w3[j] . y[t] are stored (float4 per row, D[b][t] = {d0, d1, d2, 0}) instead
 // of y; conv3_finish_kernel then sums the taps of rows t-2, t-1, t.
-constexpr int R64_WAVES = 8;
+constexpr int R64_WAVES = 12;
 constexpr int R64_PE = 68;   // pitch of the ELU(x) / output tile rows
 constexpr int R64_PH = 36;   // pitch of the hidden tile rows
-constexpr int R64_SLOT = 34 * R64_PE + 32 * R64_PH;
+constexpr int R64_SLOT = 34 * R64_PE;  // the hidden tile reuses the ELU(x) rows
 constexpr int R64_P1 = 196;  // W1^T row pitch (4 mod 32: conflict-free 16-byte reads)
 constexpr int R64_P2 = 36;   // W2^T row pitch
 constexpr int R64_WIN = 40;  // waveform samples per tile (WAVE_IN)
@@ -64,7 +64,7 @@ __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, lcol = lane & 31;
   float* E = smem + wave * R64_SLOT;   // [34][68] ELU(x); later the [32][68] output tile
-  float* H = E + 34 * R64_PE;          // [32][36] hidden
+  float* H = E;                        // [32][36] hidden, over the consumed ELU(x) rows
   float* W1s = smem + R64_WAVES * R64_SLOT;
   float* W2s = W1s + 32 * R64_P1;
   float* Win = W2s + 64 * R64_P2 + wave * R64_WINP;  // WAVE_IN: this wave's samples t0-8 .. t0+31
@@ -122,9 +122,13 @@ __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
       xok |= (unsigned)ok << u;
     }
   };
-  if (tile < tiles) load_x(tile);
+  // The 1-sample waveform window is prefetched a tile ahead; 64-channel rows
+  // are loaded at the start of their own tile (three waves per SIMD cover the
+  // latency, and a second register set would not fit their budget).
+  if (WAVE_IN && tile < tiles) load_x(tile);
   for (; tile < tiles; tile += stride) {
     const int b = (int)(tile / tpb), t0 = (int)(tile % tpb) * 32;
+    if constexpr (!WAVE_IN) load_x(tile);
     floatx4 rv[8];
     if constexpr (WAVE_IN) {
       // Samples t0-8 .. t0+31 into the wave's window; lane (q, cg) then needs
@@ -177,7 +181,6 @@ __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
         const int c = lane + 64 * u;
         rv[u] = *reinterpret_cast<const floatx4*>(xb + (long)min(t0 + c / 16, L - 1) * C + (c % 16) * 4);
       }
-      if (tile + stride < tiles) load_x(tile + stride);
     }
     wave_lds_fence();
 
@@ -195,6 +198,7 @@ __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc1[q & 1] = fm_mfma32(a[e], wq[e], acc1[q & 1]);
     }
+    wave_lds_fence();  // the k3 conv's reads of the ELU(x) rows are done before H overwrites them
 #pragma unroll
     for (int r = 0; r < 16; ++r)
       H[fm_mfma32_row(r, lane) * R64_PH + lcol] = fm_elu(__fadd_rn(__fadd_rn(acc1[0][r], acc1[1][r]), bias1));
@@ -216,7 +220,8 @@ __global__ __launch_bounds__(64 * R64_WAVES) void resblock64_kernel(
         for (int e = 0; e < 4; ++e) acc2[j] = fm_mfma32(a[e], wq[e], acc2[j]);
       }
     }
-    // Output tile through LDS (the ELU(x) rows are no longer read).
+    // Output tile through LDS, over H once the 1x1 conv has read it.
+    wave_lds_fence();
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -457,7 +462,7 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
   if (x == y) return FM_BAD_ARGUMENT;  // the halo rows of other blocks must stay intact
   if (batch == 0 || length == 0) return FM_OK;
   if (channels == 64) {
-    // Persistent: one 8-wave block per CU (LDS-bound), waves stride over 32-row tiles.
+    // Persistent: one 12-wave block per CU (LDS-bound), waves stride over 32-row tiles.
     const long tiles = (long)batch * ((length + 31) / 32);
     const int blocks = (int)std::min<long>((tiles + R64_WAVES - 1) / R64_WAVES, 256);
     hipLaunchKernelGGL((resblock64_kernel<false, false>), dim3(blocks), dim3(64 * R64_WAVES), 0, stream, x,
