@@ -953,6 +953,13 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     cfg = big;
     tiles = big_tiles;
     splits = pick_splits(tiles, p.K, 512, 8, 128);
+  } else if (p.K >= 1024 && M < 1024 && p.N >= 1024 && big_ok && workspace) {
+    // Few rows, long K, wide output (the 12.5-25 Hz convs into 1024+
+    // columns): the 128x128 tile split along K to ~256 blocks measured
+    // 4-6 us faster than the 64x64 mid tile (enc.down8, dec.first, dec.up8).
+    cfg = big;
+    tiles = big_tiles;
+    splits = pick_splits(tiles, p.K, 256, 16, 128);
   } else if (p.K >= 1024 && M < 1024 && workspace) {
     // Few rows, long K: 64x64 (or, up to 128 rows, 32x32 with the K split
     // inside the block) 16x16-MFMA tiles split along K to ~384 blocks.
