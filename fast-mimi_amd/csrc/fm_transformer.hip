@@ -334,11 +334,9 @@ __global__ __launch_bounds__(64 * NW) void window_attention16_kernel(
   constexpr int SLOT = KB * PK + KB * PVV;
   static_assert(D * P <= SLOT, "merge tile fits the slot");
   __shared__ __attribute__((aligned(16))) float stage[NW][SLOT];
-  __shared__ __attribute__((aligned(16))) float Qs[QT * PK];
+  __shared__ __attribute__((aligned(16))) float Qs[ROPE ? QT * PK : 4];
   __shared__ float Mm[NW][QT];
   __shared__ float Lm[NW][QT];
-  __shared__ float Fm[NW][QT];
-  __shared__ float Dm[QT];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, i = lane & 15;
@@ -360,18 +358,29 @@ __global__ __launch_bounds__(64 * NW) void window_attention16_kernel(
     kr.load(lane, kcol, ld, k_lo + wave * KB, k_hi, cos_t, sin_t);
     vr.load(lane, vcol, ld, k_lo + wave * KB, k_hi);
   }
-  {
+  float qv[16];  // query i, dims 16g .. 16g+15
+  if constexpr (ROPE) {
+    // RoPE pairs dims d and d +- 32: the tile is rotated while staged in LDS.
     RowTile<D, NTH, ROPE, QT> qr;
     qr.load(tid, seq + q_off + head * D, ld, q0, T - 1, cos_t, sin_t);
     qr.store(tid, Qs, PK);
-  }
-  __syncthreads();
-  float qv[16];  // query i, dims 16g .. 16g+15
+    __syncthreads();
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const floatx4 t4 = *reinterpret_cast<const floatx4*>(Qs + i * PK + 16 * g + 4 * t);
+    for (int t = 0; t < 4; ++t) {
+      const floatx4 t4 = *reinterpret_cast<const floatx4*>(Qs + i * PK + 16 * g + 4 * t);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) qv[4 * t + e] = t4[e];
+      for (int e = 0; e < 4; ++e) qv[4 * t + e] = t4[e];
+    }
+  } else {
+    // Each wave reads its query fragments straight from memory: no LDS pass
+    // and no block barrier before the key loop.
+    const float* qrow = seq + (long)min(q, T - 1) * ld + q_off + head * D + 16 * g;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const floatx4 t4 = *reinterpret_cast<const floatx4*>(qrow + 4 * t);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qv[4 * t + e] = t4[e];
+    }
   }
 
   float m_run = -INFINITY, l_run = 0.0f;
@@ -449,7 +458,9 @@ __global__ __launch_bounds__(64 * NW) void window_attention16_kernel(
   }
 
   // Merge the waves: O = sum_w O_w f_w / sum_w l_w f_w, f_w = exp(m_w - M).
-  __syncthreads();
+  // Each wave parks its running state in its own slot (its key-loop reads of
+  // that slot are fenced above), so one barrier suffices; every output
+  // element then forms the factors of its query in wave order.
   float* Om = stage[wave];
   if (g == 0) Mm[wave][i] = m_run, Lm[wave][i] = l_run;
 #pragma unroll
@@ -457,29 +468,22 @@ __global__ __launch_bounds__(64 * NW) void window_attention16_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) Om[(16 * dt + 4 * g + r) * P + i] = o[dt][r];
   __syncthreads();
-  if (tid < QT) {
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, Mm[w][tid]);
-    float den = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float f = (Mm[w][tid] == -INFINITY) ? 0.0f : expf(Mm[w][tid] - M);
-      Fm[w][tid] = f;
-      if (Mm[w][tid] != -INFINITY) den += Lm[w][tid] * f;
-    }
-    Dm[tid] = den;
-  }
-  __syncthreads();
   for (int e = tid; e < QT * D; e += NTH) {
     const int qi = e / D, d = e % D;
     const int qg = q0 + qi;
     if (qg >= T) continue;
-    float num = 0.0f;
+    float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < NW; ++w)
-      if (Mm[w][qi] != -INFINITY) num += stage[w][d * P + qi] * Fm[w][qi];
-    out[(b * (long)(T - q_start) + qg - q_start) * ld_out + head * D + d] = num / Dm[qi];
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, Mm[w][qi]);
+    float num = 0.0f, den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      if (Mm[w][qi] == -INFINITY) continue;
+      const float f = expf(Mm[w][qi] - M);
+      num += stage[w][d * P + qi] * f;
+      den += Lm[w][qi] * f;
+    }
+    out[(b * (long)(T - q_start) + qg - q_start) * ld_out + head * D + d] = num / den;
   }
 }
 
