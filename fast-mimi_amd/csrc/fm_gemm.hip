@@ -913,9 +913,32 @@ constexpr TileCfg kBigTile = kTiles[0];
 constexpr TileCfg kBigSquare = {128, 128, 1, 32, 9, 160};  // double-buffered, for N >= 128
 constexpr TileCfg kMid64 = {64, 64, 1, 128, 7, 0};
 constexpr TileCfg kMid32 = {32, 32, 4, 128, 8, 0};
+constexpr TileCfg kBig192 = {192, 128, 1, 32, 10, 0};  // double-buffered, one block per CU
+constexpr TileCfg kBig64 = {64, 128, 1, 32, 11, 0};    // double-buffered, 32x32 per wave
+
 
 long tile_count(long M, int N, const TileCfg& t) {
   return ((M + t.BM - 1) / t.BM) * ((N + t.BN - 1) / t.BN);
+}
+
+// Relative MFMA efficiency of a tile at full occupancy (measured on the
+// transformer and SEANet shapes): the per-CU work model below divides by it.
+double tile_eff(int id) {
+  switch (id) {
+    case 9: case 6: return 1.0;
+    case 10: return 0.95;
+    case 11: return 0.85;
+    case 7: case 0: case 1: case 2: return 0.7;
+    case 8: return 0.6;
+    default: return 0.55;
+  }
+}
+
+// Work of the busiest CU (tiles dealt over 256 CUs), in output elements per
+// unit of efficiency; K is common to all candidates.
+double cu_load(long M, int N, const TileCfg& t) {
+  const long per_cu = (tile_count(M, N, t) + 255) / 256;
+  return (double)per_cu * t.BM * t.BN / tile_eff(t.id);
 }
 
 // Smallest power-of-two K-split (<= cap) that brings tiles * splits to
@@ -987,6 +1010,21 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
       cfg = kMid64;
       tiles = tile_count(M, p.N, cfg);
     }
+    // Few-hundred-tile shapes: the tile whose busiest CU does the least work
+    // (a 192x128 tile gives the 4000-row qkv projection one tile per CU; 64x128
+    // spreads the 512-column output projection over all CUs).  Switches only
+    // on a clear (10%) predicted gain.
+    if (big_ok && M >= 1024) {
+      double best = cu_load(M, p.N, cfg);
+      for (const TileCfg& t : {kBigSquare, kBig192, kBig64}) {
+        const double l = cu_load(M, p.N, t);
+        if (l < 0.9 * best) {
+          best = l;
+          cfg = t;
+        }
+      }
+      tiles = tile_count(M, p.N, cfg);
+    }
     // Global K-split for long K when even the K-split tile leaves CUs idle.
     const int kchunks = (p.K + KT - 1) / KT;
     if (cfg.WK > 1 && tiles < 384 && kchunks >= 32 && workspace)
@@ -1012,6 +1050,8 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     case 3: hipLaunchKernelGGL((gemm_fast_kernel<32, 64, 1, 1, 4, 32>), grid, dim3(NTHREADS), 0, s, p); break;
     case 6: hipLaunchKernelGGL((gemm_big_kernel<256, 64, 4, 2, false>), grid, dim3(512), 0, s, p); break;
     case 9: hipLaunchKernelGGL((gemm_big_kernel<128, 128, 2, 4, true>), grid, dim3(512), 0, s, p); break;
+    case 10: hipLaunchKernelGGL((gemm_big_kernel<192, 128, 2, 4, true>), grid, dim3(512), 0, s, p); break;
+    case 11: hipLaunchKernelGGL((gemm_big_kernel<64, 128, 2, 4, true>), grid, dim3(512), 0, s, p); break;
     case 7: hipLaunchKernelGGL((gemm_mid_kernel<64, 64, 1>), grid, dim3(NTHREADS), 0, s, p); break;
     case 8: hipLaunchKernelGGL((gemm_mid_kernel<32, 32, 4>), grid, dim3(NTHREADS), 0, s, p); break;
     default: hipLaunchKernelGGL(gemm_generic_kernel, grid, dim3(256), 0, s, p); break;

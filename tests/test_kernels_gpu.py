@@ -311,7 +311,10 @@ def run_linear(x, w, flags=0, res=None, scale=None, ws=None, out=None):
 
 @pytest.mark.parametrize("rows,k,n", [(250, 512, 1536), (4000, 512, 2048), (250, 2048, 512),
                                       (1, 512, 512), (37, 16, 48), (125, 512, 512),
-                                      (60000, 256, 256), (60001, 96, 200)])
+                                      (60000, 256, 256), (60001, 96, 200),
+                                      (4000, 512, 1536), (4001, 512, 1536),  # 192x128 tiles
+                                      (2500, 512, 512), (4001, 512, 512),    # 64x128 tiles
+                                      (2500, 512, 2048)])
 def test_linear_epilogues(rows, k, n, ws):
     g = torch.Generator().manual_seed(rows + k + n)
     x = torch.randn(rows, k, generator=g)
