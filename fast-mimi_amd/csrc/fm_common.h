@@ -29,18 +29,18 @@ enum FmGemmFlags {
   FM_EPI_RES_SCALE = 32 // y = res + scale[n] * acc
 };
 
-// e^x - 1 for x <= 0, branch-free.  Near zero (x > -1/4) the Taylor series
-// of e^x - 1 through x^8 (truncation < 1e-11, below half an ulp of the
-// result), in Horner form with FMAs; further out e^x - 1 from the hardware
-// exponential, where the result is at least 0.22 in magnitude so the
-// subtraction loses nothing.  Within a few ulp of expm1 over x <= 0.
+// e^x - 1 for x <= 0, branch-free.  Near zero (x > -1/4) x * q(x), q a
+// degree-4 polynomial fitted to expm1(x) / x on [-1/4, 0] (iteratively
+// reweighted least squares toward equal relative error; evaluated in FP32
+// Horner form with FMAs it stays within 1.12 ulp of float64 expm1 over 4M
+// samples of the interval, against 1.06 ulp for the degree-8 Taylor series);
+// further out e^x - 1 from the hardware exponential, where the result is at
+// least 0.22 in magnitude so the subtraction loses nothing.  Within a few ulp
+// of expm1 over x <= 0.
 FM_DEVICE float fm_expm1_neg(float x) {
-  float p = fmaf(x, 1.0f / 40320.0f, 1.0f / 5040.0f);
-  p = fmaf(x, p, 1.0f / 720.0f);
-  p = fmaf(x, p, 1.0f / 120.0f);
-  p = fmaf(x, p, 1.0f / 24.0f);
-  p = fmaf(x, p, 1.0f / 6.0f);
-  p = fmaf(x, p, 0.5f);
+  float p = fmaf(x, 0.007509505841881037f, 0.04148859530687332f);
+  p = fmaf(x, p, 0.16665075719356537f);
+  p = fmaf(x, p, 0.4999994933605194f);
   p = fmaf(x, p, 1.0f);
   const float small = x * p;
   const float large = __expf(x) - 1.0f;
