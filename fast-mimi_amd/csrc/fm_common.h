@@ -47,8 +47,14 @@ FM_DEVICE float fm_expm1_neg(float x) {
   return x > -0.25f ? small : large;
 }
 
-// ELU with alpha = 1 (torch.nn.ELU): x for x > 0, e^x - 1 otherwise.
-FM_DEVICE float fm_elu(float x) { return x > 0.0f ? x : fm_expm1_neg(fminf(x, 0.0f)); }
+// ELU with alpha = 1 (torch.nn.ELU): x for x > 0, e^x - 1 otherwise.  The
+// expm1 branch is evaluated for every lane and selected (x > 0 only discards
+// it; NaN propagates through it): a per-element branch would be taken by
+// almost every wave anyway.
+FM_DEVICE float fm_elu(float x) {
+  const float r = fm_expm1_neg(x);
+  return x > 0.0f ? x : r;
+}
 
 // Exact-erf GELU (torch.nn.functional.gelu, approximate='none').
 FM_DEVICE float fm_gelu(float x) {
