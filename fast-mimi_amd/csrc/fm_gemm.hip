@@ -332,7 +332,16 @@ __global__ __launch_bounds__(NTHREADS) void gemm_fast_kernel(GemmArgs p) {
 // phase overlaps the other's MFMAs.  The 128x128 form measured 3-4% faster
 // wherever N >= 128.  Loads are branch-free (clamped address plus a select)
 // so the in-order instruction stream stays short.
-template <int BM, int BN, int WM, int WN, bool DB>
+// Sixteen zero bytes: the source of every out-of-window operand load in the
+// zero-page loader (referenced from device code only).
+__device__ __attribute__((aligned(16))) float g_zero16[4];
+
+// ZP (zero padding and C_in a multiple of BK): a k-tile lies in one tap, so
+// the tap comes from the uniform k0 (no per-lane division), each A row reads
+// at its window start + k, and loads outside the window, past K or past N
+// read g_zero16 instead of being masked after the load: about a third fewer
+// VALU instructions per k-tile, which on this part do not overlap the MFMAs.
+template <int BM, int BN, int WM, int WN, bool DB, bool ZP = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
   constexpr int NTH = 64 * WM * WN;
   constexpr int BK = 32, P = BK + 4, CPR = BK / 4, HK = BK / 2;
@@ -365,18 +374,24 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
   // b*L.  Rows past M get p0 = INT_MIN / 2 so every position test fails.
   long a_org[APT];
   int a_p0[APT], a_bL[APT];
+  const float* a_row[APT];  // ZP: the row's window start (tap 0)
 #pragma unroll
   for (int i = 0; i < APT; ++i) {
-    const long m = min(m0 + rrow + i * RPP, M - 1);
-    const int b = (int)(m / p.rows);
-    const int t = (int)(m - (long)b * p.rows);
+    const int m = (int)min(m0 + rrow + i * RPP, M - 1);  // M < 2^31 (checked at launch)
+    const int b = m / p.rows;
+    const int t = m - b * p.rows;
     a_p0[i] = (m0 + rrow + i * RPP < M) ? t * p.rs - p.padL : INT_MIN / 2;
     a_bL[i] = b * p.L_in;
     a_org[i] = (long)b * p.L_in * p.C_in;
+    a_row[i] = p.x + a_org[i] + (long)a_p0[i] * p.C_in;
   }
   int b_n[BPT];
+  const float* b_row[BPT];  // ZP: weight row, null past N
 #pragma unroll
-  for (int i = 0; i < BPT; ++i) b_n[i] = n0 + rrow + i * RPP;
+  for (int i = 0; i < BPT; ++i) {
+    b_n[i] = n0 + rrow + i * RPP;
+    b_row[i] = b_n[i] < p.N ? p.w + (long)b_n[i] * p.K : nullptr;
+  }
 
   // Prefetched rows stay raw in registers, with a validity mask; the zeroing
   // select happens at the LDS store, so nothing waits on the loads until the
@@ -384,6 +399,22 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
   floatx4 ra[APT], rb[BPT];
   unsigned amask = 0, bmask = 0;
   auto load = [&](int k0) {
+    if constexpr (ZP) {
+      const int kg = k0 + ck;
+      const bool kok = kg < k_end;
+      const int tap = k0 / p.C_in;  // uniform
+#pragma unroll
+      for (int i = 0; i < APT; ++i) {
+        const bool ok = kok & ((unsigned)(a_p0[i] + tap) < (unsigned)p.L_in);
+        ra[i] = *reinterpret_cast<const floatx4*>(ok ? a_row[i] + kg : g_zero16);
+      }
+#pragma unroll
+      for (int i = 0; i < BPT; ++i) {
+        const bool ok = kok & (b_row[i] != nullptr);
+        rb[i] = *reinterpret_cast<const floatx4*>(ok ? b_row[i] + kg : g_zero16);
+      }
+      return;
+    }
     const int kg = k0 + ck;
     const bool kok = kg < k_end;
     const int kc = min(kg, p.K - 4);
@@ -421,14 +452,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
     float* Bs = As + BM * P;
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
-      floatx4 v = ((amask >> i) & 1) ? ra[i] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      floatx4 v = (ZP || ((amask >> i) & 1)) ? ra[i] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
       if (elu_in) v = floatx4{fm_elu(v.x), fm_elu(v.y), fm_elu(v.z), fm_elu(v.w)};
       *reinterpret_cast<floatx4*>(As + (rrow + i * RPP) * P + ck) = v;
     }
 #pragma unroll
     for (int i = 0; i < BPT; ++i)
       *reinterpret_cast<floatx4*>(Bs + (rrow + i * RPP) * P + ck) =
-          ((bmask >> i) & 1) ? rb[i] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+          (ZP || ((bmask >> i) & 1)) ? rb[i] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   };
   auto mma = [&](int stage) {
     const float* As = smem + stage * STAGE_F;
@@ -1043,15 +1074,21 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
   p.partial = splits > 1 ? workspace : nullptr;
 
   dim3 grid((unsigned)tiles, splits);
+  // Zero-page loader of the large tiles (their k-tile is 32).
+  const bool zp = !(p.flags & FM_REPLICATE) && p.C_in % 32 == 0;
   switch (cfg.id) {
     case 0: hipLaunchKernelGGL((gemm_fast_kernel<128, 128, 2, 2, 1, 64>), grid, dim3(NTHREADS), 0, s, p); break;
     case 1: hipLaunchKernelGGL((gemm_fast_kernel<128, 64, 4, 1, 1, 64>), grid, dim3(NTHREADS), 0, s, p); break;
     case 2: hipLaunchKernelGGL((gemm_fast_kernel<128, 32, 4, 1, 1, 64>), grid, dim3(NTHREADS), 0, s, p); break;
     case 3: hipLaunchKernelGGL((gemm_fast_kernel<32, 64, 1, 1, 4, 32>), grid, dim3(NTHREADS), 0, s, p); break;
-    case 6: hipLaunchKernelGGL((gemm_big_kernel<256, 64, 4, 2, false>), grid, dim3(512), 0, s, p); break;
-    case 9: hipLaunchKernelGGL((gemm_big_kernel<128, 128, 2, 4, true>), grid, dim3(512), 0, s, p); break;
-    case 10: hipLaunchKernelGGL((gemm_big_kernel<192, 128, 2, 4, true>), grid, dim3(512), 0, s, p); break;
-    case 11: hipLaunchKernelGGL((gemm_big_kernel<64, 128, 2, 4, true>), grid, dim3(512), 0, s, p); break;
+#define FM_BIG(BM_, BN_, WM_, WN_, DB_)                                                              \
+  if (zp) hipLaunchKernelGGL((gemm_big_kernel<BM_, BN_, WM_, WN_, DB_, true>), grid, dim3(512), 0, s, p); \
+  else hipLaunchKernelGGL((gemm_big_kernel<BM_, BN_, WM_, WN_, DB_, false>), grid, dim3(512), 0, s, p)
+    case 6: FM_BIG(256, 64, 4, 2, false); break;
+    case 9: FM_BIG(128, 128, 2, 4, true); break;
+    case 10: FM_BIG(192, 128, 2, 4, true); break;
+    case 11: FM_BIG(64, 128, 2, 4, true); break;
+#undef FM_BIG
     case 7: hipLaunchKernelGGL((gemm_mid_kernel<64, 64, 1>), grid, dim3(NTHREADS), 0, s, p); break;
     case 8: hipLaunchKernelGGL((gemm_mid_kernel<32, 32, 4>), grid, dim3(NTHREADS), 0, s, p); break;
     default: hipLaunchKernelGGL(gemm_generic_kernel, grid, dim3(256), 0, s, p); break;
