@@ -72,6 +72,23 @@ FM_DEVICE int fm_mfma32_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >
 
 static inline int fm_ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
 
+// Raw buffer (gfx9 descriptor word 3 = 0x00020000) over `bytes` bytes at
+// `base`.  An access is a per-lane 32-bit byte offset plus a wave-uniform one
+// (an SGPR: compile-time row offsets cost no vector instructions).  Callers
+// keep every access inside the buffer.
+FM_DEVICE __amdgpu_buffer_rsrc_t fm_buffer(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+FM_DEVICE floatx4 fm_buf_load4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+FM_DEVICE float fm_buf_load1(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+FM_DEVICE void fm_buf_store1(float v, __amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, voff, soff, 0);
+}
+
 // Orders this wave's LDS accesses: everything before completes before
 // anything after is issued (the compiler may not move memory ops across).
 FM_DEVICE void wave_lds_fence() {

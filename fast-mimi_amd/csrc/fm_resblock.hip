@@ -319,17 +319,35 @@ __global__ __launch_bounds__(NT, 3) void resblock_direct_kernel(
   const long b = blockIdx.y;
   const int t0 = blockIdx.x * BM;
   const float* xb = x + b * (long)L * C;
+  // Interior blocks (halo and rows inside the sequence) address every row
+  // through raw buffers: a lane offset plus compile-time row offsets, no
+  // per-element bounds checks.  Edge blocks take the checked path.
+  const bool fast = t0 >= 2 && t0 + BM <= L && (long)L * C * 4 <= 0x7fffffffL;
+  const __amdgpu_buffer_rsrc_t rx = fm_buffer(xb, L * C * 4);
+  const __amdgpu_buffer_rsrc_t ry = fm_buffer(y + b * (long)L * C, L * C * 4);
+  const int vrow = ((t0 + wr * 32 + 4 * h) * C + wc * 64 + lcol) * 4;  // this lane's first output element
+  auto row_off = [&](int r, int j) { return ((8 * (r >> 2) + (r & 3)) * C + j * 32) * 4; };
 
   // Input rows first (the critical path), weight ring right behind them.
   constexpr int CH = (BM + 2) * C / 4, U = (CH + NT - 1) / NT;
   floatx4 xv[U];
+  if (fast) {
+    // The tile's rows t0-2 .. t0+BM-1 are one contiguous run of CH chunks.
+    const int vo = ((t0 - 2) * C + 4 * tid) * 4;
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int c = tid + u * NT;
-    const int r = c / (C / 4), k = (c % (C / 4)) * 4;
-    const int t = t0 - 2 + r;
-    xv[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (c < CH && t >= 0 && t < L) xv[u] = *reinterpret_cast<const floatx4*>(xb + (long)t * C + k);
+    for (int u = 0; u < U; ++u) {
+      xv[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (u + 1 < U || tid + u * NT < CH) xv[u] = fm_buf_load4(rx, vo, u * NT * 16);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = tid + u * NT;
+      const int r = c / (C / 4), k = (c % (C / 4)) * 4;
+      const int t = t0 - 2 + r;
+      xv[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (c < CH && t >= 0 && t < L) xv[u] = *reinterpret_cast<const floatx4*>(xb + (long)t * C + k);
+    }
   }
   const float* w1p = w1 + (long)(wc * 32 + lcol) * K1 + 16 * h;
   const float* w2p = w2 + (long)(wc * 64 + lcol) * HC + 16 * h;
@@ -404,13 +422,20 @@ __global__ __launch_bounds__(NT, 3) void resblock_direct_kernel(
   // Residual rows land during the 1x1 conv.
   float* yb = y + b * (long)L * C;
   float rv[FN2][16];
+  if (fast) {
 #pragma unroll
-  for (int j = 0; j < FN2; ++j)
+    for (int j = 0; j < FN2; ++j)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int t = min(t0 + wr * 32 + fm_mfma32_row(r, lane), L - 1);
-      rv[j][r] = xb[(long)t * C + wc * 64 + j * 32 + lcol];
-    }
+      for (int r = 0; r < 16; ++r) rv[j][r] = fm_buf_load1(rx, vrow, row_off(r, j));
+  } else {
+#pragma unroll
+    for (int j = 0; j < FN2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = min(t0 + wr * 32 + fm_mfma32_row(r, lane), L - 1);
+        rv[j][r] = xb[(long)t * C + wc * 64 + j * 32 + lcol];
+      }
+  }
   floatx16 acc2[FN2];
 #pragma unroll
   for (int j = 0; j < FN2; ++j)
@@ -439,7 +464,11 @@ __global__ __launch_bounds__(NT, 3) void resblock_direct_kernel(
       const int t = t0 + wr * 32 + fm_mfma32_row(r, lane);
       float v = __fadd_rn(rv[j][r], __fadd_rn(acc2[j][r], bias));
       if (elu_out) v = fm_elu(v);
-      if (t < L) yb[(long)t * C + n] = v;
+      if (fast) {
+        fm_buf_store1(v, ry, vrow, row_off(r, j));
+      } else if (t < L) {
+        yb[(long)t * C + n] = v;
+      }
     }
   }
 }
