@@ -383,6 +383,9 @@ __global__ __launch_bounds__(64 * NW) void window_attention16_kernel(
     }
   }
 
+  // Scores are kept in base-2 units (scale * log2 e folded in) so every
+  // exponential is one hardware exp2.
+  const float scale2 = scale * 1.44269504088896341f;
   float m_run = -INFINITY, l_run = 0.0f;
   floatx4 o[4];
 #pragma unroll
@@ -415,31 +418,48 @@ __global__ __launch_bounds__(64 * NW) void window_attention16_kernel(
       }
     float sv[2][4];
     float cmax = -INFINITY;
+    // A tile whose keys lie inside every query's window (and the sequence)
+    // needs no per-score mask: only the diagonal and window-edge tiles do.
+    const bool full = q0 + QT <= T && k0 + KB - 1 <= k_hi && k0 + KB - 1 <= q0 &&
+                      k0 > q0 + QT - 1 - window;
+    if (full) {
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = k0 + 16 * kt + 4 * g + r;
-        const bool ok = q < T && key <= k_hi && key <= q && key > q - window;
-        const float v = sc[kt][0][r] + sc[kt][1][r];
-        sv[kt][r] = ok ? v * scale : -INFINITY;
-        cmax = fmaxf(cmax, sv[kt][r]);
-      }
+        for (int r = 0; r < 4; ++r) {
+          sv[kt][r] = (sc[kt][0][r] + sc[kt][1][r]) * scale2;
+          cmax = fmaxf(cmax, sv[kt][r]);
+        }
+    } else {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = k0 + 16 * kt + 4 * g + r;
+          const bool ok = q < T && key <= k_hi && key <= q && key > q - window;
+          const float v = sc[kt][0][r] + sc[kt][1][r];
+          sv[kt][r] = ok ? v * scale2 : -INFINITY;
+          cmax = fmaxf(cmax, sv[kt][r]);
+        }
+    }
     cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
     cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
     const float m_new = fmaxf(m_run, cmax);
+    // exp2(-inf) = 0 covers masked scores; a query with nothing unmasked yet
+    // subtracts 0 instead of -inf so no -inf - -inf NaN forms.
+    const float m_sub = m_new == -INFINITY ? 0.0f : m_new;
     float psum = 0.0f;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float pv = (sv[kt][r] == -INFINITY) ? 0.0f : expf(sv[kt][r] - m_new);
+        const float pv = __builtin_amdgcn_exp2f(sv[kt][r] - m_sub);
         sv[kt][r] = pv;
         psum += pv;
       }
     psum += __shfl_xor(psum, 16, 64);
     psum += __shfl_xor(psum, 32, 64);
-    const float corr = (m_run == -INFINITY) ? 0.0f : expf(m_run - m_new);
+    const float corr = __builtin_amdgcn_exp2f(m_run - m_sub);
     l_run = l_run * corr + psum;
     m_run = m_new;
 #pragma unroll
@@ -457,7 +477,7 @@ __global__ __launch_bounds__(64 * NW) void window_attention16_kernel(
     wave_lds_fence();  // this tile's LDS reads are done before the slot is rewritten
   }
 
-  // Merge the waves: O = sum_w O_w f_w / sum_w l_w f_w, f_w = exp(m_w - M).
+  // Merge the waves: O = sum_w O_w f_w / sum_w l_w f_w, f_w = 2^(m_w - M), m in base-2 units.
   // Each wave parks its running state in its own slot (its key-loop reads of
   // that slot are fenced above), so one barrier suffices; every output
   // element then forms the factors of its query in wave order.
@@ -479,7 +499,7 @@ __global__ __launch_bounds__(64 * NW) void window_attention16_kernel(
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       if (Mm[w][qi] == -INFINITY) continue;
-      const float f = expf(Mm[w][qi] - M);
+      const float f = __builtin_amdgcn_exp2f(Mm[w][qi] - M);
       num += stage[w][d * P + qi] * f;
       den += Lm[w][qi] * f;
     }
