@@ -508,6 +508,214 @@ __global__ __launch_bounds__(64 * NW) void window_attention16_kernel(
 }
 
 
+// Whole-sequence attention for head_dim 64 and sequences of at most 256
+// frames (the batched 12.5-25 Hz transformers): one block per (half, head,
+// sequence) stages the head's K (rotated when ROPE) and V for every frame in
+// LDS once, so no key row is fetched twice by a block.  The 16 query tiles of
+// 16 frames are paired (j, 15 - j) so that every pair costs the same number
+// of key tiles under the causal mask; block half s owns pairs 4s .. 4s+3.
+// Waves w and w + 4 share pair w and split its key tiles (even / odd 32-key
+// tiles), then merge their (max, sum, O) through LDS after each query tile.
+// The inner step is the one of window_attention16_kernel: S^T = K Q^T on
+// 16x16x4 MFMA with K from 16-byte LDS reads and Q^T from registers, an
+// online softmax in base-2 units, and O^T += V^T P^T with P^T from the S^T
+// registers.  A key tile may run up to 31 rows past the staged frames; those
+// rows are masked, and the LDS layout (V, then K, then the merge area) keeps
+// such reads inside the array on finite values (V overruns read K rows).
+constexpr int SEQ_MAX = 256;
+template <bool ROPE>
+__global__ __launch_bounds__(512) void window_attention_seq_kernel(
+    const float* __restrict__ qkv, int ld, int q_off, int k_off, int v_off,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int T, int heads,
+    int kv_heads, int window, float scale, float* __restrict__ out, int ld_out) {
+  constexpr int D = 64, QT = 16, PK = D + 4, PV = D + 4, P = QT + 1;
+  constexpr int PARK = D * P + 2 * QT;  // one wave pair's parked O^T, max and sum
+  __shared__ __attribute__((aligned(16))) float lds[SEQ_MAX * (PV + PK) + 4 * PARK];
+  float* Vs = lds;                       // [SEQ_MAX][PV]
+  float* Ks = Vs + SEQ_MAX * PV;          // [SEQ_MAX][PK]
+  float* park = Ks + SEQ_MAX * PK;        // [4][PARK]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, i = lane & 15;
+  const int pair = wave & 3, kh = wave >> 2;
+  const int head = blockIdx.y;
+  const int hk = head / (heads / kv_heads);
+  const long b = blockIdx.z;
+  const float* seq = qkv + b * (long)T * ld;
+
+  // Stage every frame's K (rotated) and V; rows T .. SEQ_MAX-1 are zero.
+  {
+    constexpr int PAIRS = SEQ_MAX * D / 8, KN = PAIRS / 512;
+    const float* kcol = seq + k_off + hk * D;
+#pragma unroll
+    for (int u = 0; u < KN; ++u) {
+      const int e = tid + u * 512;
+      const int r = e / (D / 8), d = (e % (D / 8)) * 4;
+      const int t = min(r, T - 1);
+      floatx4 lo = *reinterpret_cast<const floatx4*>(kcol + (long)t * ld + d);
+      floatx4 hi = *reinterpret_cast<const floatx4*>(kcol + (long)t * ld + d + D / 2);
+      if (r >= T) lo = hi = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (ROPE) {
+        const floatx4 c = *reinterpret_cast<const floatx4*>(cos_t + (long)t * D + d);
+        const floatx4 s = *reinterpret_cast<const floatx4*>(sin_t + (long)t * D + d);
+        rope_pair(lo, hi, c, s);
+      }
+      *reinterpret_cast<floatx4*>(Ks + r * PK + d) = lo;
+      *reinterpret_cast<floatx4*>(Ks + r * PK + d + D / 2) = hi;
+    }
+    constexpr int CH = SEQ_MAX * D / 4, VN = CH / 512;
+    const float* vcol = seq + v_off + hk * D;
+#pragma unroll
+    for (int u = 0; u < VN; ++u) {
+      const int e = tid + u * 512;
+      const int r = e / (D / 4), d = (e % (D / 4)) * 4;
+      floatx4 v = *reinterpret_cast<const floatx4*>(vcol + (long)min(r, T - 1) * ld + d);
+      if (r >= T) v = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      *reinterpret_cast<floatx4*>(Vs + r * PV + d) = v;
+    }
+  }
+  __syncthreads();
+
+  const float scale2 = scale * 1.44269504088896341f;
+  float* pk = park + pair * PARK;
+  const int jp = blockIdx.x * 4 + pair;
+#pragma unroll 1
+  for (int half = 0; half < 2; ++half) {
+    const int qt = half == 0 ? jp : 15 - jp;
+    const int q0 = qt * QT;
+    const bool live = q0 < T;
+    const int q = q0 + i;
+    float m_run = -INFINITY, l_run = 0.0f;
+    floatx4 o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (live) {
+      // Query i, dims 16g .. 16g+15, rotated in registers (RoPE pairs d, d +- 32).
+      float qv[16];
+      const float* qrow = seq + (long)min(q, T - 1) * ld + q_off + head * D;
+#pragma unroll
+      for (int t4 = 0; t4 < 4; ++t4) {
+        const int d = 16 * g + 4 * t4;
+        floatx4 x = *reinterpret_cast<const floatx4*>(qrow + d);
+        if (ROPE) {
+          const int dl = d & (D / 2 - 1);  // the pair's lower dim
+          const floatx4 y = *reinterpret_cast<const floatx4*>(qrow + (d ^ (D / 2)));
+          const floatx4 c = *reinterpret_cast<const floatx4*>(cos_t + (long)min(q, T - 1) * D + dl);
+          const floatx4 s = *reinterpret_cast<const floatx4*>(sin_t + (long)min(q, T - 1) * D + dl);
+          floatx4 lo = d < D / 2 ? x : y, hi = d < D / 2 ? y : x;
+          rope_pair(lo, hi, c, s);
+          x = d < D / 2 ? lo : hi;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qv[4 * t4 + e] = x[e];
+      }
+      const int k_lo = max(0, q0 - window + 1);
+      const int k_hi = min(T, q0 + QT) - 1;
+      const int ntiles = (k_hi - k_lo + KB) / KB;
+      for (int tile = kh; tile < ntiles; tile += 2) {
+        const int k0 = k_lo + tile * KB;
+        const float* Kt = Ks + k0 * PK;
+        const float* Vt = Vs + k0 * PV;
+        floatx4 sc[2][2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int par = 0; par < 2; ++par) sc[kt][par] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt) {
+            const floatx4 a4 = *reinterpret_cast<const floatx4*>(Kt + (16 * kt + i) * PK + 16 * g + 4 * t);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sc[kt][t & 1] = fm_mfma16(a4[e], qv[4 * t + e], sc[kt][t & 1]);
+          }
+        float sv[2][4];
+        float cmax = -INFINITY;
+        const bool full = q0 + QT <= T && k0 + KB - 1 <= k_hi && k0 + KB - 1 <= q0 &&
+                          k0 > q0 + QT - 1 - window;
+        if (full) {
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              sv[kt][r] = (sc[kt][0][r] + sc[kt][1][r]) * scale2;
+              cmax = fmaxf(cmax, sv[kt][r]);
+            }
+        } else {
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int key = k0 + 16 * kt + 4 * g + r;
+              const bool ok = q < T && key <= k_hi && key <= q && key > q - window;
+              const float v = sc[kt][0][r] + sc[kt][1][r];
+              sv[kt][r] = ok ? v * scale2 : -INFINITY;
+              cmax = fmaxf(cmax, sv[kt][r]);
+            }
+        }
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+        const float m_new = fmaxf(m_run, cmax);
+        const float m_sub = m_new == -INFINITY ? 0.0f : m_new;
+        float psum = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float pv = __builtin_amdgcn_exp2f(sv[kt][r] - m_sub);
+            sv[kt][r] = pv;
+            psum += pv;
+          }
+        psum += __shfl_xor(psum, 16, 64);
+        psum += __shfl_xor(psum, 32, 64);
+        const float corr = __builtin_amdgcn_exp2f(m_run - m_sub);
+        l_run = l_run * corr + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[dt][r] *= corr;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float* vrow = Vt + (16 * kt + 4 * g + r) * PV + i;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) o[dt] = fm_mfma16(vrow[16 * dt], sv[kt][r], o[dt]);
+          }
+      }
+    }
+    // Merge the pair: the odd-tile wave parks its state, the even-tile wave
+    // forms O = (O_0 f_0 + O_1 f_1) / (l_0 f_0 + l_1 f_1), f_w = 2^(m_w - M).
+    if (kh == 1) {
+      if (g == 0) pk[D * P + i] = m_run, pk[D * P + QT + i] = l_run;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pk[(16 * dt + 4 * g + r) * P + i] = o[dt][r];
+    }
+    __syncthreads();
+    if (kh == 0 && live) {
+      const float m1 = pk[D * P + i], l1 = pk[D * P + QT + i];
+      const float M = fmaxf(m_run, m1);
+      const float f0 = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
+      const float f1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - M);
+      const float den = l_run * f0 + l1 * f1;
+      if (q < T) {
+        float* orow = out + (b * (long)T + q) * ld_out + head * D;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int d = 16 * dt + 4 * g + r;
+            orow[d] = (o[dt][r] * f0 + pk[d * P + i] * f1) / den;
+          }
+      }
+    }
+    __syncthreads();  // the park area is free again
+  }
+}
+
 // Grids of the row-block kernels put the column block in blockIdx.x: blocks
 // are dealt round-robin to the 8 XCDs, so each XCD's L2 holds a slice of the
 // weights (read once) plus the small activation block, instead of every XCD
@@ -1104,6 +1312,19 @@ int fm_window_attention_rows(const float* qkv, int ld_qkv, int q_offset, int k_o
   if ((ld_qkv | q_offset | k_offset | v_offset) % 4) return FM_BAD_ARGUMENT;
   if (query_start < 0 || query_start > length) return FM_BAD_ARGUMENT;
   if (batch == 0 || length == query_start) return FM_OK;
+  if (head_dim == 64 && query_start == 0 && length <= SEQ_MAX && (long)batch * heads >= 128) {
+    // Enough (sequence, head) pairs to fill the GPU with two blocks each.
+    const dim3 gs(2, heads, batch);
+    if (cos_table)
+      hipLaunchKernelGGL((window_attention_seq_kernel<true>), gs, dim3(512), 0, stream, qkv,
+                         ld_qkv, q_offset, k_offset, v_offset, cos_table, sin_table, length, heads,
+                         kv_heads, window, scale, out, ld_out);
+    else
+      hipLaunchKernelGGL((window_attention_seq_kernel<false>), gs, dim3(512), 0, stream, qkv,
+                         ld_qkv, q_offset, k_offset, v_offset, cos_table, sin_table, length, heads,
+                         kv_heads, window, scale, out, ld_out);
+    return (int)hipGetLastError();
+  }
   if (head_dim == 64) {
     // 16-query blocks; eight waves per block (fewer key tiles per wave) while
     // the grid is too small to fill the GPU, four once blocks are plentiful.

@@ -361,7 +361,10 @@ def attention_reference(qkv, B, T, H, D, window, cos, sin):
 
 @pytest.mark.parametrize("B,T,H,D,window", [(1, 250, 8, 64, 250), (1, 251, 8, 64, 250),
                                             (2, 700, 8, 64, 250), (1, 1, 8, 64, 250),
-                                            (16, 125, 8, 64, 250), (8, 300, 8, 64, 250), (2, 18, 2, 8, 8)])
+                                            (16, 125, 8, 64, 250), (8, 300, 8, 64, 250), (2, 18, 2, 8, 8),
+                                            # whole-sequence kernel (>= 128 sequence-heads, T <= 256)
+                                            (16, 250, 8, 64, 250), (16, 256, 8, 64, 250),
+                                            (20, 200, 8, 64, 64), (32, 97, 8, 64, 250), (128, 1, 8, 64, 250)])
 def test_window_attention(B, T, H, D, window):
     g = torch.Generator().manual_seed(T + H)
     qkv = torch.randn(B * T, 3 * H * D, generator=g)
@@ -376,17 +379,18 @@ def test_window_attention(B, T, H, D, window):
     close(out.cpu(), attention_reference(qkv, B, T, H, D, window, cos, sin), rel=5e-5)
 
 
-def test_window_attention_prerotated():
+@pytest.mark.parametrize("B,T", [(1, 300), (16, 250)])
+def test_window_attention_prerotated(B, T):
     """NULL RoPE tables: q/k are consumed as given (rotated by their producer)."""
-    B, T, H, D, window = 1, 300, 8, 64, 250
+    H, D, window = 8, 64, 250
     g = torch.Generator().manual_seed(5)
     qkv = torch.randn(B * T, 3 * H * D, generator=g)
     cfg = MimiConfig()
     cos, sin = rope_tables(cfg, T)
-    q, k, v = qkv.view(T, 3, H, D).unbind(1)
+    q, k, v = qkv.view(B, T, 3, H, D).unbind(2)
     rot = MimiOracle._rotate_half
-    pre = torch.stack([q * cos[:, None] + rot(q) * sin[:, None],
-                       k * cos[:, None] + rot(k) * sin[:, None], v], 1).reshape(T, 3 * H * D)
+    c, s_ = cos[None, :, None], sin[None, :, None]
+    pre = torch.stack([q * c + rot(q) * s_, k * c + rot(k) * s_, v], 2).reshape(B * T, 3 * H * D)
     out = torch.empty(B * T, H * D, device=DEV)
     pre_d = pre.contiguous().to(DEV)
     nat.call("fm_window_attention", pre_d.data_ptr(), 3 * H * D, 0, H * D, 2 * H * D, None, None,
