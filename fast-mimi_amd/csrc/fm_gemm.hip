@@ -568,6 +568,204 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Direct-load kernel: the operand tiles travel from global memory straight
+// into LDS (global_load_lds_dwordx4, one 16-byte chunk per lane, written at
+// lane * 16 bytes of the wave's 1 KB window), so the k-loop holds no prefetch
+// registers and issues no vector instructions to stage operands.  An NST-deep
+// LDS ring of BK-deep k-tiles is refilled NST - 1 k-tiles ahead, with one
+// barrier per k-tile (the shipped tiles: BK = 32, two stages; BK = 16 with
+// three stages measured slower).  Each lane picks the global chunk that
+// belongs in its LDS slot: slot (row r, position cp) holds chunk
+// cp ^ ((r / SWR) % CPR) of row r, so the MFMA fragment reads (eight rows per
+// 16-byte read phase) spread over all 64 banks.  Loads that fall outside the
+// input window, past M or past N read the zero page g_zero16.
+// Requirements: zero padding, no ELU on load, C_in, K and the K-split
+// boundaries multiples of BK (run_gemm guarantees them).  8 waves as
+// 2 x WN; the epilogue runs in two halves of BM / 2 rows (one wave row each)
+// so that the output tile fits in the ring's LDS: 64 KB at 128 x 128, two
+// blocks per CU.
+template <int BM, int BN, int WN, int BK, int NST, int WPE>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void gemm_dl_kernel(GemmArgs p) {
+  constexpr int NTH = 512, WM = 2;
+  static_assert((BK == 16 || BK == 32) && (NST == 2 || NST == 3), "ring shape");
+  constexpr int CPR = BK / 4, RPI = 64 / CPR;  // chunks per row, rows per load instruction
+  constexpr int SWR = 64 / BK;                 // rows per full sweep of the 64 banks
+  static_assert(WM * WN == 8, "eight waves");
+  constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
+  constexpr int AI = BM / (8 * RPI), BI = BN / (8 * RPI);  // load instructions per wave per stage
+  static_assert(FM >= 1 && FN >= 1 && AI >= 1 && BI >= 1 && AI * 8 * RPI == BM && BI * 8 * RPI == BN, "tiling");
+  constexpr int LPS = AI + BI;
+  constexpr int STAGE_F = (BM + BN) * BK;
+  constexpr int HM = BM / 2, PC = BN + 4, TILE_F = HM * PC;
+  __shared__ __attribute__((aligned(16))) float smem[NST * STAGE_F > TILE_F ? NST * STAGE_F : TILE_F];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave / WN;
+  const int wm0 = wr * WTM, wn0 = (wave % WN) * WTN;
+  const long M = (long)p.batch * p.rows;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int tile = tile_index();
+  const long m0 = (long)(tile / tiles_n) * BM;
+  const int n0 = (tile % tiles_n) * BN;
+  const int k_begin = blockIdx.y * p.k_split;
+  const int k_end = min(p.K, k_begin + p.k_split);
+
+  // This lane's chunk of each load instruction: tile row lr + 16 * (instr),
+  // chunk position cp within the row, global chunk cg.
+  const int lr = lane / CPR, cp = lane % CPR;
+  const float* a_row[AI];
+  int a_p0[AI];
+#pragma unroll
+  for (int i = 0; i < AI; ++i) {
+    const int r = (wave * AI + i) * RPI + lr;
+    const long mm = m0 + r;
+    const int m = (int)min(mm, M - 1);
+    const int b = m / p.rows;
+    const int t = m - b * p.rows;
+    a_p0[i] = mm < M ? t * p.rs - p.padL : INT_MIN / 2;
+    a_row[i] = p.x + (long)b * p.L_in * p.C_in + (long)a_p0[i] * p.C_in + 4 * (cp ^ ((r / SWR) & (CPR - 1)));
+  }
+  const float* b_row[BI];
+#pragma unroll
+  for (int i = 0; i < BI; ++i) {
+    const int r = (wave * BI + i) * RPI + lr;
+    const int n = n0 + r;
+    b_row[i] = n < p.N ? p.w + (long)n * p.K + 4 * (cp ^ ((r / SWR) & (CPR - 1))) : nullptr;
+  }
+  auto issue = [&](int stage, int k0) {
+    float* As = smem + stage * STAGE_F;
+    float* Bs = As + BM * BK;
+    const int tap = k0 / p.C_in;  // uniform: a k-tile lies in one tap
+#pragma unroll
+    for (int i = 0; i < AI; ++i) {
+      const bool ok = (unsigned)(a_p0[i] + tap) < (unsigned)p.L_in;
+      const float* src = ok ? a_row[i] + k0 : g_zero16;
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(As + (wave * AI + i) * RPI * BK),
+                                       16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < BI; ++i) {
+      const float* src = b_row[i] ? b_row[i] + k0 : g_zero16;
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(Bs + (wave * BI + i) * RPI * BK),
+                                       16, 0, 0);
+    }
+  };
+
+  floatx16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int h = lane >> 5, lcol = lane & 31;
+  const int nkt = (k_end - k_begin) / BK;
+  if (nkt > 0) issue(0, k_begin);
+  if (NST == 3 && nkt > 1) issue(1, k_begin + BK);
+  for (int kt = 0; kt < nkt; ++kt) {
+    // This lane's loads of stage kt are done once at most the next stage's remain.
+    if (NST == 3 && kt + 1 < nkt) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPS) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // Every wave's loads of stage kt landed, and every wave's reads of stage
+    // (kt + 2) % 3 completed (their values fed the previous MFMAs).  A bare
+    // s_barrier: __syncthreads would also wait for the stage kt + 1 loads.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (kt + NST - 1 < nkt) issue((kt + NST - 1) % NST, k_begin + (kt + NST - 1) * BK);
+    const float* As = smem + (kt % NST) * STAGE_F;
+    const float* Bs = As + BM * BK;
+#pragma unroll
+    for (int q = 0; q < BK / 8; ++q) {
+      const int c = (BK / 8) * h + q;  // k = (BK / 2) h + 4q + e at MFMA step 4q + e
+      floatx4 a[FM], b[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int row = wm0 + i * 32 + lcol;
+        a[i] = *reinterpret_cast<const floatx4*>(As + row * BK + 4 * (c ^ ((row / SWR) & (CPR - 1))));
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int row = wn0 + j * 32 + lcol;
+        b[j] = *reinterpret_cast<const floatx4*>(Bs + row * BK + 4 * (c ^ ((row / SWR) & (CPR - 1))));
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) acc[i][j] = fm_mfma32(a[i][e], b[j][e], acc[i][j]);
+    }
+  }
+  __syncthreads();  // every wave is done reading the ring
+
+  const bool crop = p.y_rows != p.rows;
+  const bool has_res = p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE);
+  float* part = p.partial ? p.partial + (long)blockIdx.y * M * p.N : nullptr;
+  constexpr int CG = BN / 4, RSTEP = NTH / CG, NRUN = HM / RSTEP, RB = WPE > 4 ? 1 : (NRUN < 2 ? NRUN : 2);
+  static_assert(NTH % CG == 0 && HM % RSTEP == 0 && NRUN % RB == 0, "epilogue runs");
+  const int c = (tid % CG) * 4, r0 = tid / CG;
+  const int n = n0 + c;
+  const bool n_ok = n < p.N;
+  const int ncl = n_ok ? n : 0;
+  const floatx4 bias = (p.bias && !part) ? *reinterpret_cast<const floatx4*>(p.bias + ncl % p.bias_len)
+                                         : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  const floatx4 scale = ((p.flags & FM_EPI_RES_SCALE) && !part)
+                            ? *reinterpret_cast<const floatx4*>(p.scale + ncl)
+                            : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    if (wr == hf) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            smem[(i * 32 + fm_mfma32_row(r, lane)) * PC + wn0 + j * 32 + lcol] = acc[i][j][r];
+    }
+    __syncthreads();
+    const long mh = m0 + hf * HM;
+#pragma unroll
+    for (int u0 = 0; u0 < NRUN; u0 += RB) {
+      floatx4 v[RB], res[RB];
+#pragma unroll
+      for (int u = 0; u < RB; ++u) {
+        const int r = r0 + (u0 + u) * RSTEP;
+        const long m = min(mh + r, M - 1);
+        v[u] = *reinterpret_cast<const floatx4*>(smem + r * PC + c);
+        res[u] = (has_res && !part) ? *reinterpret_cast<const floatx4*>(p.res + m * p.N + ncl)
+                                    : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (int u = 0; u < RB; ++u) {
+        const long m = mh + r0 + (u0 + u) * RSTEP;
+        if (m >= M || !n_ok) continue;
+        if (part) {
+          *reinterpret_cast<floatx4*>(part + m * p.N + n) = v[u];
+          continue;
+        }
+        floatx4 o = v[u];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = epilogue_v(o[e], bias[e], res[u][e], scale[e], p.flags);
+        long dst = m * p.N + n;
+        if (crop) {
+          const int b = (int)(m / p.rows);
+          const int t = (int)(m - (long)b * p.rows);
+          if (t >= p.y_rows) continue;
+          dst = ((long)b * p.y_rows + t) * p.N + n;
+        }
+        *reinterpret_cast<floatx4*>(p.y + dst) = o;
+      }
+    }
+    __syncthreads();  // the half tile is consumed before the next half lands
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Mid-size kernel for few-row / long-K contractions: BM x BN in {32, 64}^2,
 // 4 waves, each owning a 32x32 output tile as 2x2 independent 16x16x4 FP32
 // MFMA chains; the waves form (BM/32) x (BN/32) x WK groups, and with WK > 1
@@ -946,6 +1144,14 @@ constexpr TileCfg kMid64 = {64, 64, 1, 128, 7, 0};
 constexpr TileCfg kMid32 = {32, 32, 4, 128, 8, 0};
 constexpr TileCfg kBig192 = {192, 128, 1, 32, 10, 0};  // double-buffered, one block per CU
 constexpr TileCfg kBig64 = {64, 128, 1, 32, 11, 0};    // double-buffered, 32x32 per wave
+// Direct-load forms of the three double-buffered tiles (taken when the
+// operands allow, see gemm_dl_kernel).
+constexpr TileCfg kDl128 = {128, 128, 1, 32, 13, 0};
+constexpr TileCfg kDl192 = {192, 128, 1, 32, 14, 0};
+constexpr TileCfg kDl64 = {64, 128, 1, 32, 15, 0};
+#ifndef FM_DL_MODE
+#define FM_DL_MODE 2
+#endif
 
 
 long tile_count(long M, int N, const TileCfg& t) {
@@ -1061,6 +1267,14 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     if (cfg.WK > 1 && tiles < 384 && kchunks >= 32 && workspace)
       splits = (int)std::min<long>((512 + tiles - 1) / tiles, kchunks / 16);
   }
+  // The direct-load tiles need every k-tile (32 deep) inside one tap.
+  const bool dl_ok = big_ok && !(p.flags & (FM_REPLICATE | FM_ELU_IN)) && p.C_in % 32 == 0 &&
+                     p.K % 32 == 0;
+  if (FM_DL_MODE && dl_ok) {
+    if (cfg.id == 9) cfg = kDl128;
+    if (FM_DL_MODE >= 2 && cfg.id == 10) cfg = kDl192;
+    if (FM_DL_MODE >= 2 && cfg.id == 11) cfg = kDl64;
+  }
   if (splits > 1) {
     const size_t per = (size_t)M * p.N * sizeof(float);
     while (splits > 1 && per * splits > workspace_bytes) --splits;
@@ -1089,6 +1303,9 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     case 10: FM_BIG(192, 128, 2, 4, true); break;
     case 11: FM_BIG(64, 128, 2, 4, true); break;
 #undef FM_BIG
+    case 13: hipLaunchKernelGGL((gemm_dl_kernel<128, 128, 4, 32, 2, 4>), grid, dim3(512), 0, s, p); break;
+    case 14: hipLaunchKernelGGL((gemm_dl_kernel<192, 128, 4, 32, 2, 4>), grid, dim3(512), 0, s, p); break;
+    case 15: hipLaunchKernelGGL((gemm_dl_kernel<64, 128, 4, 32, 2, 4>), grid, dim3(512), 0, s, p); break;
     case 7: hipLaunchKernelGGL((gemm_mid_kernel<64, 64, 1>), grid, dim3(NTHREADS), 0, s, p); break;
     case 8: hipLaunchKernelGGL((gemm_mid_kernel<32, 32, 4>), grid, dim3(NTHREADS), 0, s, p); break;
     default: hipLaunchKernelGGL(gemm_generic_kernel, grid, dim3(256), 0, s, p); break;

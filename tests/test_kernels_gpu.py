@@ -100,6 +100,41 @@ def test_conv1d(B, cin, cout, k, stride, L, ws):
     close(got, want)
 
 
+# Direct-load tiles (C_in a multiple of 16, zero padding, no ELU on load):
+# 128x128 with a partial column tile and an odd row count, the 192x128 and
+# 64x128 picks of few-hundred-tile shapes, and a K-split one.
+DL_CASES = [
+    # B, Cin, Cout, k, stride, L, y_len
+    (1, 64, 160, 4, 2, 70001, None),
+    (2, 48, 132, 2, 1, 40003, 39000),
+    (1, 512, 1536, 1, 1, 4000, None),
+    (1, 512, 512, 1, 1, 4000, 3999),
+    (16, 512, 512, 1, 1, 250, None),
+    (1, 256, 512, 12, 6, 12003, None),
+]
+
+
+@pytest.mark.parametrize("B,cin,cout,k,stride,L,y_len", DL_CASES)
+@pytest.mark.parametrize("epi", ["plain", "res_elu"])
+def test_conv1d_direct_load_tiles(B, cin, cout, k, stride, L, y_len, epi, ws):
+    g = torch.Generator().manual_seed(B * 31 + cin + cout + k + L)
+    x = torch.randn(B, cin, L, generator=g)
+    w = torch.randn(cout, cin, k, generator=g) / math.sqrt(cin * k)
+    b = torch.randn(cout, generator=g) * 0.1
+    rows = -(-L // stride)
+    want = causal_conv1d(x.double(), w.double(), b.double(), stride)
+    if epi == "plain":
+        got = run_conv(x, w, b, stride, "constant", 0, ws, y_len=y_len)
+    else:
+        res = torch.randn(B, cout, rows, generator=g)
+        got = run_conv(x, w, b, stride, "constant", nat.EPI_RES_ADD | nat.EPI_ELU, ws,
+                       residual_ncl=res, y_len=y_len)
+        want = F.elu(res.double() + want)
+    want = want[..., :y_len] if y_len is not None else want
+    assert got.shape == want.shape
+    close(got, want)
+
+
 @pytest.mark.parametrize("B,L,y_len", [(1, 1, 1), (2, 2, 2), (1, 62, 62), (2, 63, 60), (3, 999, 999),
                                        (1, 240000, 240000), (2, 24001, 23995)])
 @pytest.mark.parametrize("elu_in", [0, 1])
