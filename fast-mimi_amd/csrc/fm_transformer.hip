@@ -38,6 +38,57 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float* __restrict
     yr[c] = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(xr[c], mean), rstd), gamma[c]), beta[c]);
 }
 
+// LayerNorm for C = 512: 32 lanes per row, each holding float4 chunks
+// p, p + 32, p + 64, p + 96 of it, so the row is read once and the
+// statistics come from registers.  The arithmetic (per-lane partial sums,
+// shuffle order, two-pass variance) is the one of the LayerNorm prologue of
+// row16_linear_kernel, so both paths round identically.
+__global__ __launch_bounds__(256) void layer_norm512_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ gamma,
+                                                            const float* __restrict__ beta,
+                                                            long rows, float eps,
+                                                            float* __restrict__ y) {
+  constexpr int K = 512, TPR = 32, CH = K / 4 / TPR;
+  const long row = (long)blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int p = threadIdx.x & 31;
+  const float* xr = x + min(row, rows - 1) * K;
+  floatx4 v[CH], gv[CH], bv[CH];
+#pragma unroll
+  for (int u = 0; u < CH; ++u) v[u] = *reinterpret_cast<const floatx4*>(xr + 4 * (p + TPR * u));
+#pragma unroll
+  for (int u = 0; u < CH; ++u) {
+    gv[u] = *reinterpret_cast<const floatx4*>(gamma + 4 * (p + TPR * u));
+    bv[u] = *reinterpret_cast<const floatx4*>(beta + 4 * (p + TPR * u));
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int u = 0; u < CH; ++u) s += (v[u][0] + v[u][1]) + (v[u][2] + v[u][3]);
+#pragma unroll
+  for (int o = 1; o < TPR; o <<= 1) s += __shfl_xor(s, o, 64);
+  const float mean = s / (float)K;
+  float var = 0.0f;
+#pragma unroll
+  for (int u = 0; u < CH; ++u)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float d = v[u][e] - mean;
+      var = fmaf(d, d, var);
+    }
+#pragma unroll
+  for (int o = 1; o < TPR; o <<= 1) var += __shfl_xor(var, o, 64);
+  const float rstd = 1.0f / sqrtf(var / (float)K + eps);
+  if (row >= rows) return;
+  float* yr = y + row * K;
+#pragma unroll
+  for (int u = 0; u < CH; ++u) {
+    floatx4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(v[u][e], mean), rstd), gv[u][e]), bv[u][e]);
+    *reinterpret_cast<floatx4*>(yr + 4 * (p + TPR * u)) = o;
+  }
+}
+
 FM_DEVICE floatx4 fm_mfma16(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
@@ -1277,6 +1328,11 @@ int fm_layer_norm(const float* x, const float* gamma, const float* beta, long ro
   if (!x || !gamma || !beta || !y || rows < 0 || channels <= 0) return FM_BAD_ARGUMENT;
   if (rows == 0) return FM_OK;
   const long blocks = (rows + 3) / 4;
+  if (channels == 512 && ((uintptr_t)x | (uintptr_t)y | (uintptr_t)gamma | (uintptr_t)beta) % 16 == 0) {
+    hipLaunchKernelGGL(layer_norm512_kernel, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, stream,
+                       x, gamma, beta, rows, eps, y);
+    return (int)hipGetLastError();
+  }
   hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, x, gamma,
                      beta, rows, channels, eps, y);
   return (int)hipGetLastError();
