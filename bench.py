@@ -150,12 +150,13 @@ def cpu_baseline(audio: np.ndarray, mask: np.ndarray, nq: int, runs: int) -> dic
             oracle.forward(a, m, nq)
             times.append((time.perf_counter_ns() - t0) / 1e6)
     med = statistics.median(times)
+    total_s = sum(times) / 1e3
     seconds = audio.shape[0] * audio.shape[-1] / 24_000
     return {"value": round(seconds / (med / 1e3), 3), "unit": "audio-sec/sec", "cores": cores,
             "kind": "port", "median_ms": round(med, 2), "cpu": cpu_model(),
             "sample": f"B1 x 10 s, nq={nq} (the bench workload itself), CPU oracle (PyTorch "
                       f"eager restatement of the reference model.py path), median of {runs} "
-                      f"after 2 warm-ups, {cores} threads"}
+                      f"after 2 warm-ups ({total_s:.1f} s of timed CPU work), {cores} threads"}
 
 
 def cpu_model() -> str:
@@ -173,7 +174,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cpu-runs", type=int, default=10)
+    ap.add_argument("--cpu-runs", type=int, default=50)
     ap.add_argument("--no-extra", action="store_true", help="skip the 100 s and B64/nq32 sections")
     ap.add_argument("--dominant-only", action="store_true")
     ap.add_argument("--iters", type=int, default=20)
