@@ -72,6 +72,25 @@ FM_DEVICE int fm_mfma32_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >
 
 static inline int fm_ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
 
+// Division by a runtime constant d >= 1 for numerators n < 2^31:
+// n / d = (umulhi(magic, n) + n) >> shift with shift = ceil(log2 d) and
+// magic = floor(2^32 (2^shift - d) / d) + 1 (the round-up method of Granlund
+// and Montgomery; t + n stays below 2^32 because t <= n < 2^31).  Three vector
+// instructions instead of a ~30-instruction integer division.
+struct FmDivisor {
+  unsigned magic;
+  int shift;
+};
+static inline FmDivisor fm_divisor(unsigned d) {
+  int l = 0;
+  while ((1ull << l) < d) ++l;
+  const unsigned long long m = ((1ull << 32) * ((1ull << l) - d)) / d + 1;
+  return FmDivisor{(unsigned)m, l};
+}
+FM_DEVICE unsigned fm_div(unsigned n, FmDivisor d) {
+  return (__umulhi(d.magic, n) + n) >> d.shift;
+}
+
 // Raw buffer (gfx9 descriptor word 3 = 0x00020000) over `bytes` bytes at
 // `base`.  An access is a per-lane 32-bit byte offset plus a wave-uniform one
 // (an SGPR: compile-time row offsets cost no vector instructions).  Callers

@@ -46,6 +46,7 @@ struct GemmArgs {
   float* y;
   float* partial;  // global split-K partials [splits][M][N], or null
   int batch, L_in, C_in, rows, rs, padL, K, N, y_rows, bias_len, k_split, flags;
+  FmDivisor rows_div;  // division by `rows` (set by run_gemm)
 };
 
 constexpr int KT = 32;  // k granularity of K-splits (every tile's BK divides it or is 64)
@@ -332,6 +333,14 @@ __global__ __launch_bounds__(NTHREADS) void gemm_fast_kernel(GemmArgs p) {
 // phase overlaps the other's MFMAs.  The 128x128 form measured 3-4% faster
 // wherever N >= 128.  Loads are branch-free (clamped address plus a select)
 // so the in-order instruction stream stays short.
+// Block barrier that orders LDS accesses only (outstanding global loads and
+// stores keep flying): this wave's LDS operations complete, then s_barrier.
+FM_DEVICE void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Sixteen zero bytes: the source of every out-of-window operand load in the
 // zero-page loader (referenced from device code only).
 __device__ __attribute__((aligned(16))) float g_zero16[4];
@@ -599,7 +608,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   constexpr int HM = BM / 2, PC = BN + 4, TILE_F = HM * PC;
   __shared__ __attribute__((aligned(16))) float smem[NST * STAGE_F > TILE_F ? NST * STAGE_F : TILE_F];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // The wave index is uniform: LDS window addresses stay in scalar registers.
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = wave / WN;
   const int wm0 = wr * WTM, wn0 = (wave % WN) * WTN;
   const long M = (long)p.batch * p.rows;
@@ -620,7 +630,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     const int r = (wave * AI + i) * RPI + lr;
     const long mm = m0 + r;
     const int m = (int)min(mm, M - 1);
-    const int b = m / p.rows;
+    const int b = (int)fm_div((unsigned)m, p.rows_div);
     const int t = m - b * p.rows;
     a_p0[i] = mm < M ? t * p.rs - p.padL : INT_MIN / 2;
     a_row[i] = p.x + (long)b * p.L_in * p.C_in + (long)a_p0[i] * p.C_in + 4 * (cp ^ ((r / SWR) & (CPR - 1)));
@@ -700,7 +710,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
           for (int j = 0; j < FN; ++j) acc[i][j] = fm_mfma32(a[i][e], b[j][e], acc[i][j]);
     }
   }
-  __syncthreads();  // every wave is done reading the ring
+  // Every wave is done reading the ring.  The epilogue's barriers order LDS
+  // traffic only: __syncthreads would also wait for the previous half's
+  // global stores to complete, serialising the two halves' HBM writes.
+  lds_barrier();
 
   const bool crop = p.y_rows != p.rows;
   const bool has_res = p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE);
@@ -727,7 +740,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
           for (int r = 0; r < 16; ++r)
             smem[(i * 32 + fm_mfma32_row(r, lane)) * PC + wn0 + j * 32 + lcol] = acc[i][j][r];
     }
-    __syncthreads();
+    lds_barrier();
     const long mh = m0 + hf * HM;
 #pragma unroll
     for (int u0 = 0; u0 < NRUN; u0 += RB) {
@@ -761,7 +774,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
         *reinterpret_cast<floatx4*>(p.y + dst) = o;
       }
     }
-    __syncthreads();  // the half tile is consumed before the next half lands
+    if (hf == 0) lds_barrier();  // the half tile is consumed before the next half lands
   }
 }
 
@@ -1197,6 +1210,7 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
   if (M == 0 || p.y_rows == 0) return FM_OK;
   if (p.L_in == 0 || M > INT_MAX / 2) return FM_BAD_ARGUMENT;
 
+  p.rows_div = fm_divisor((unsigned)p.rows);
   const bool fast = (p.C_in % 4 == 0) && (p.K % 4 == 0);
   TileCfg cfg = kSplitTile;
   long tiles = 0;
