@@ -559,6 +559,202 @@ __global__ __launch_bounds__(64 * NW) void window_attention16_kernel(
 }
 
 
+// Long-sequence attention for head_dim 64 (hundreds to thousands of frames,
+// few sequence-heads): block = 16 * NWQ consecutive queries of one head, NWQ
+// waves, wave w owning queries q0 + 16w .. +15.  The block's key range
+// [q0 - window + 1, q0 + 16 NWQ - 1] streams through LDS in 32-key chunks (K
+// rotated while staged when ROPE), double-buffered from a one-chunk register
+// prefetch, one barrier per chunk, so each key row is fetched once per block
+// instead of once per 16 queries.  Each wave runs the online softmax of
+// window_attention16_kernel over the chunks that meet its own window and
+// writes its rows; no cross-wave merge.  Several blocks share a CU (35 KB of
+// LDS each).  Measured at 2500 frames: two waves per block (32 queries) 35 us
+// per layer, four 36 us, one 50 us (the 16-query kernel: 47.5 us); 64- or
+// 128-key chunks are slower (their register prefetch spills).
+template <bool ROPE, int NWQ>
+__global__ __launch_bounds__(64 * NWQ) void window_attention_flash_kernel(
+    const float* __restrict__ qkv, int ld, int q_off, int k_off, int v_off,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int T, int q_start,
+    int heads, int kv_heads, int window, float scale, float* __restrict__ out, int ld_out) {
+  constexpr int D = 64, QT = 16, QBLK = QT * NWQ, NTH = 64 * NWQ, PK = D + 4, PV = D + 4;
+  constexpr int CK = KB;  // keys per chunk
+  constexpr int STAGE = CK * (PK + PV);
+  constexpr int KPT = CK * (D / 8) / NTH, VPT = CK * (D / 4) / NTH;  // K pairs / V chunks per thread
+  static_assert(KPT >= 1 && VPT >= 1, "chunk loader");
+  __shared__ __attribute__((aligned(16))) float lds[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, i = lane & 15;
+  const int head = blockIdx.y;
+  const int hk = head / (heads / kv_heads);
+  const long b = blockIdx.z;
+  const int q0 = q_start + blockIdx.x * QBLK;
+  const int q0w = q0 + QT * wave;
+  const int q = q0w + i;
+  const float* seq = qkv + b * (long)T * ld;
+  const float* kcol = seq + k_off + hk * D;
+  const float* vcol = seq + v_off + hk * D;
+  const int kb_lo = max(0, q0 - window + 1);
+  const int kb_hi = min(T, q0 + QBLK) - 1;
+  const int nch = (kb_hi - kb_lo + CK) / CK;
+  const bool live = q0w < T;
+  const int wk_lo = max(0, q0w - window + 1);
+  const int wk_hi = min(T, q0w + QT) - 1;
+
+  // Chunk loader: K pair e = tid + u * NTH is row e / 8, dims 4(e % 8) and
+  // +32; V chunk e = tid + u * NTH is row e / 16, dims 4(e % 16).
+  floatx4 klo[KPT], khi[KPT], kc[KPT], ks[KPT], vv[VPT];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const int e = tid + u * NTH, kr = e >> 3, kd = (e & 7) * 4;
+      const int t = min(k0 + kr, kb_hi);
+      klo[u] = *reinterpret_cast<const floatx4*>(kcol + (long)t * ld + kd);
+      khi[u] = *reinterpret_cast<const floatx4*>(kcol + (long)t * ld + kd + D / 2);
+      if (ROPE) {
+        kc[u] = *reinterpret_cast<const floatx4*>(cos_t + (long)t * D + kd);
+        ks[u] = *reinterpret_cast<const floatx4*>(sin_t + (long)t * D + kd);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+      const int e = tid + u * NTH;
+      vv[u] = *reinterpret_cast<const floatx4*>(vcol + (long)min(k0 + e / 16, kb_hi) * ld + (e % 16) * 4);
+    }
+  };
+  auto store = [&](int stage) {
+    float* Ks = lds + stage * STAGE;
+    float* Vs = Ks + CK * PK;
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const int e = tid + u * NTH, kr = e >> 3, kd = (e & 7) * 4;
+      floatx4 l = klo[u], hh = khi[u];
+      if (ROPE) rope_pair(l, hh, kc[u], ks[u]);
+      *reinterpret_cast<floatx4*>(Ks + kr * PK + kd) = l;
+      *reinterpret_cast<floatx4*>(Ks + kr * PK + kd + D / 2) = hh;
+    }
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+      const int e = tid + u * NTH;
+      *reinterpret_cast<floatx4*>(Vs + (e / 16) * PV + (e % 16) * 4) = vv[u];
+    }
+  };
+
+  load(kb_lo);
+  // Query i of this wave, dims 16g .. 16g+15, rotated in registers.
+  float qv[16];
+  {
+    const int qc = min(q, T - 1);
+    const float* qrow = seq + (long)qc * ld + q_off + head * D;
+#pragma unroll
+    for (int t4 = 0; t4 < 4; ++t4) {
+      const int d = 16 * g + 4 * t4;
+      floatx4 x = *reinterpret_cast<const floatx4*>(qrow + d);
+      if (ROPE) {
+        const int dl = d & (D / 2 - 1);
+        const floatx4 y = *reinterpret_cast<const floatx4*>(qrow + (d ^ (D / 2)));
+        const floatx4 c = *reinterpret_cast<const floatx4*>(cos_t + (long)qc * D + dl);
+        const floatx4 sn = *reinterpret_cast<const floatx4*>(sin_t + (long)qc * D + dl);
+        floatx4 lo = d < D / 2 ? x : y, hi = d < D / 2 ? y : x;
+        rope_pair(lo, hi, c, sn);
+        x = d < D / 2 ? lo : hi;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qv[4 * t4 + e] = x[e];
+    }
+  }
+
+  const float scale2 = scale * 1.44269504088896341f;
+  float m_run = -INFINITY, l_run = 0.0f;
+  floatx4 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int c = 0; c < nch; ++c) {
+    const int kc0 = kb_lo + c * CK;
+    store(c & 1);
+    __syncthreads();  // chunk c staged; every wave is past its reads of chunk c - 2
+    if (c + 1 < nch) load(kc0 + CK);
+    const int k0 = kc0;
+    if (!live || k0 > wk_hi || k0 + KB - 1 < wk_lo) continue;
+    const float* Kt = lds + (c & 1) * STAGE;
+    const float* Vt = Kt + CK * PK;
+    floatx4 sc[2][2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int par = 0; par < 2; ++par) sc[kt][par] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const floatx4 a4 = *reinterpret_cast<const floatx4*>(Kt + (16 * kt + i) * PK + 16 * g + 4 * t);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[kt][t & 1] = fm_mfma16(a4[e], qv[4 * t + e], sc[kt][t & 1]);
+      }
+    float sv[2][4];
+    float cmax = -INFINITY;
+    const bool full = q0w + QT <= T && k0 + KB - 1 <= wk_hi && k0 + KB - 1 <= q0w &&
+                      k0 > q0w + QT - 1 - window;
+    if (full) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          sv[kt][r] = (sc[kt][0][r] + sc[kt][1][r]) * scale2;
+          cmax = fmaxf(cmax, sv[kt][r]);
+        }
+    } else {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = k0 + 16 * kt + 4 * g + r;
+          const bool ok = q < T && key <= kb_hi && key <= q && key > q - window;
+          const float v = sc[kt][0][r] + sc[kt][1][r];
+          sv[kt][r] = ok ? v * scale2 : -INFINITY;
+          cmax = fmaxf(cmax, sv[kt][r]);
+        }
+    }
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+    const float m_new = fmaxf(m_run, cmax);
+    const float m_sub = m_new == -INFINITY ? 0.0f : m_new;
+    float psum = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(sv[kt][r] - m_sub);
+        sv[kt][r] = pv;
+        psum += pv;
+      }
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);
+    const float corr = __builtin_amdgcn_exp2f(m_run - m_sub);
+    l_run = l_run * corr + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[dt][r] *= corr;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float* vrow = Vt + (16 * kt + 4 * g + r) * PV + i;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt] = fm_mfma16(vrow[16 * dt], sv[kt][r], o[dt]);
+      }
+  }
+  if (!live || q >= T) return;
+  float* orow = out + (b * (long)(T - q_start) + q - q_start) * ld_out + head * D;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) orow[16 * dt + 4 * g + r] = o[dt][r] / l_run;
+}
+
 // Whole-sequence attention for head_dim 64 and sequences of at most 256
 // frames (the batched 12.5-25 Hz transformers): one block per (half, head,
 // sequence) stages the head's K (rotated when ROPE) and V for every frame in
@@ -1379,6 +1575,20 @@ int fm_window_attention_rows(const float* qkv, int ld_qkv, int q_offset, int k_o
       hipLaunchKernelGGL((window_attention_seq_kernel<false>), gs, dim3(512), 0, stream, qkv,
                          ld_qkv, q_offset, k_offset, v_offset, cos_table, sin_table, length, heads,
                          kv_heads, window, scale, out, ld_out);
+    return (int)hipGetLastError();
+  }
+  if (head_dim == 64 && length - query_start >= 512 && (long)batch * heads < 128) {
+    // Long sequences, few sequence-heads: query blocks sharing each key chunk.
+    constexpr int NWQ = 2;
+    const dim3 gf((length - query_start + 16 * NWQ - 1) / (16 * NWQ), heads, batch);
+    if (cos_table)
+      hipLaunchKernelGGL((window_attention_flash_kernel<true, NWQ>), gf, dim3(64 * NWQ), 0, stream, qkv, ld_qkv,
+                         q_offset, k_offset, v_offset, cos_table, sin_table, length, query_start,
+                         heads, kv_heads, window, scale, out, ld_out);
+    else
+      hipLaunchKernelGGL((window_attention_flash_kernel<false, NWQ>), gf, dim3(64 * NWQ), 0, stream, qkv, ld_qkv,
+                         q_offset, k_offset, v_offset, cos_table, sin_table, length, query_start,
+                         heads, kv_heads, window, scale, out, ld_out);
     return (int)hipGetLastError();
   }
   if (head_dim == 64) {

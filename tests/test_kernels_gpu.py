@@ -400,7 +400,9 @@ def attention_reference(qkv, B, T, H, D, window, cos, sin):
                                             (16, 125, 8, 64, 250), (8, 300, 8, 64, 250), (2, 18, 2, 8, 8),
                                             # whole-sequence kernel (>= 128 sequence-heads, T <= 256)
                                             (16, 250, 8, 64, 250), (16, 256, 8, 64, 250),
-                                            (20, 200, 8, 64, 64), (32, 97, 8, 64, 250), (128, 1, 8, 64, 250)])
+                                            (20, 200, 8, 64, 64), (32, 97, 8, 64, 250), (128, 1, 8, 64, 250),
+                                            # 64-query chunked kernel (>= 512 queries, < 128 sequence-heads)
+                                            (1, 2500, 8, 64, 250), (1, 1000, 8, 64, 64), (3, 513, 8, 64, 250)])
 def test_window_attention(B, T, H, D, window):
     g = torch.Generator().manual_seed(T + H)
     qkv = torch.randn(B * T, 3 * H * D, generator=g)
@@ -573,7 +575,8 @@ def test_conv1d_valid(B, L, ci, co, k, s, flags, ws):
 
 
 @pytest.mark.parametrize("B,T,q_start,window", [(1, 260, 249, 250), (2, 300, 249, 250),
-                                                (1, 10, 9, 250), (3, 12, 4, 8), (1, 64, 0, 250)])
+                                                (1, 10, 9, 250), (3, 12, 4, 8), (1, 64, 0, 250),
+                                                (1, 1100, 300, 250), (2, 700, 150, 100)])
 def test_window_attention_rows_with_cached_keys(B, T, q_start, window):
     """Queries at rows q_start.. over all rows as keys (a KV cache in front)."""
     H, D = 8, 64
