@@ -20,6 +20,7 @@
 namespace {
 
 constexpr int RB = 32;  // query rows per block
+constexpr int kQt2MaxChunkEntries = 2048;  // codebook entries per block with 64-row blocks
 constexpr int kMaxChunks = 64;  // entry chunks per step (partials per row)
 
 FM_DEVICE bool better(float v, int i, float bv, int bi) {
@@ -260,9 +261,13 @@ __global__ __launch_bounds__(256) void rvq_step_kernel(StepArgs a) {
 // sub-tile and one k-part; partial dot products are summed through LDS in
 // k-part order before the distances.  The prologue resolves step j-1 (eight
 // lanes per row, shuffle-reduced) and forms residual_j and |residual_j|^2.
-template <int DIM, int KP>
+template <int DIM, int KP, int QTN = 1>
 __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a0, const float* __restrict__ e0,
                                                             StepArgs a1, const float* __restrict__ e1) {
+  // QTN = 2: 64 query rows per block as two 32-query MFMA column tiles that
+  // share every codebook fragment (half the codebook reads per query).
+  static_assert(QTN == 1 || (QTN == 2 && KP == 1), "two query tiles only without k-parts");
+  constexpr int RBT = RB * QTN;
   // blockIdx.z picks the branch (semantic / acoustic chains share launches).
   const StepArgs a = blockIdx.z ? a1 : a0;
   const float* __restrict__ embed = blockIdx.z ? e1 : e0;
@@ -273,18 +278,22 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a0, const f
   constexpr int EG = 4 / KP, KW = DIM / KP, NPC = KW / 64, PX = DIM + 4, PR = RB + 1;
   constexpr int CH = DIM / 32;  // float4 chunks per lane in the prologue (8 lanes per row)
   static_assert(KW % 64 == 0, "k-part of whole 64-dim pieces");
-  extern __shared__ __attribute__((aligned(16))) float smem[];
-  float* Xs = smem;                      // [RB][PX]
-  float* xnS = Xs + RB * PX;             // [RB]
-  float* bestv = xnS + RB;               // [EG][RB]
-  int* besti = reinterpret_cast<int*>(bestv + EG * RB);
-  float* red = reinterpret_cast<float*>(besti + EG * RB);  // [KP-1][EG][32 * PR]
+  // QTN = 2 needs more than the 64 KB of dynamic LDS a launch gets: a static
+  // array sized for 64 rows and up to kQt2MaxChunkEntries codebook norms.
+  extern __shared__ __attribute__((aligned(16))) float smem_dyn[];
+  __shared__ __attribute__((aligned(16))) float smem_qt2[QTN == 2 ? RBT * PX + RBT + 2 * 4 * RBT + kQt2MaxChunkEntries : 4];
+  float* smem = QTN == 2 ? smem_qt2 : smem_dyn;
+  float* Xs = smem;                      // [RBT][PX]
+  float* xnS = Xs + RBT * PX;            // [RBT]
+  float* bestv = xnS + RBT;              // [EG][RBT]
+  int* besti = reinterpret_cast<int*>(bestv + EG * RBT);
+  float* red = reinterpret_cast<float*>(besti + EG * RBT);  // [KP-1][EG][32 * PR]
   float* normS = red + (KP - 1) * EG * 32 * PR;            // [chunk_entries]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = wave % EG, p = wave / EG;
   const int h = lane >> 5, col = lane & 31;
-  const long m0 = (long)blockIdx.x * RB;
+  const long m0 = (long)blockIdx.x * RBT;
   const int chunk = blockIdx.y;
   const int e_begin = chunk * a.chunk_entries;
   const int e_end = min(a.entries, e_begin + a.chunk_entries);
@@ -307,91 +316,118 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a0, const f
   const bool has_work = !fin && (KP == 1 ? items > 0 : g < nsub);
   if (has_work) load_piece(cur, 0);
 
-  // ---- prologue: row r = tid / 8, lane part pt = tid % 8.
+  // ---- prologue: rows r = 32 * pass + tid / 8, lane part pt = tid % 8.
   {
-    const int r = tid >> 3, pt = tid & 7;
-    const long m = m0 + r;
-    const long mc = min(m, (long)a.M - 1);
-    const bool valid = m < a.M;
+    const int pt = tid & 7;
     // The residual rows do not depend on the previous code: issue them first.
-    floatx4 xv[CH], ev[CH];
+    floatx4 xv[QTN][CH];
     if (!fin) {
 #pragma unroll
-      for (int u = 0; u < CH; ++u)
-        xv[u] = *reinterpret_cast<const floatx4*>(a.resid_in + mc * a.ld_in + 4 * (pt + 8 * u));
+      for (int ps = 0; ps < QTN; ++ps) {
+        const long mc = min(m0 + 32 * ps + (tid >> 3), (long)a.M - 1);
+#pragma unroll
+        for (int u = 0; u < CH; ++u)
+          xv[ps][u] = *reinterpret_cast<const floatx4*>(a.resid_in + mc * a.ld_in + 4 * (pt + 8 * u));
+      }
     }
-    int code = 0;
-    if (a.prev_embed) {
-      float bv;
-      int bi;
-      resolve8(a.prev_val, a.prev_idx, a.chunks, a.M, mc, pt, bv, bi);
-      code = bi;
-      if (chunk == 0 && pt == 0 && valid) {
-        const long b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
-        a.prev_codes[b * a.batch_stride + t] = code;
+    int code[QTN];
+#pragma unroll
+    for (int ps = 0; ps < QTN; ++ps) {
+      code[ps] = 0;
+      const long m = m0 + 32 * ps + (tid >> 3);
+      const long mc = min(m, (long)a.M - 1);
+      if (a.prev_embed) {
+        float bv;
+        int bi;
+        resolve8(a.prev_val, a.prev_idx, a.chunks, a.M, mc, pt, bv, bi);
+        code[ps] = bi;
+        if (chunk == 0 && pt == 0 && m < a.M) {
+          const long b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
+          a.prev_codes[b * a.batch_stride + t] = bi;
+        }
       }
     }
     if (fin) return;
-    if (a.prev_embed) {
-#pragma unroll
-      for (int u = 0; u < CH; ++u)
-        ev[u] = *reinterpret_cast<const floatx4*>(a.prev_embed + (long)code * DIM + 4 * (pt + 8 * u));
-    }
     for (int c = tid; c < e_end - e_begin; c += 256) normS[c] = a.norms[e_begin + c];
-    float xn = 0.0f;
 #pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      floatx4 x = xv[u];
+    for (int ps = 0; ps < QTN; ++ps) {
+      const int r = 32 * ps + (tid >> 3);
+      const long m = m0 + r;
+      const bool valid = m < a.M;
+      floatx4 ev[CH];
       if (a.prev_embed) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = __fsub_rn(x[e], ev[u][e]);
-        if (chunk == 0 && valid && a.resid_out)
-          *reinterpret_cast<floatx4*>(a.resid_out + m * DIM + 4 * (pt + 8 * u)) = x;
+        for (int u = 0; u < CH; ++u)
+          ev[u] = *reinterpret_cast<const floatx4*>(a.prev_embed + (long)code[ps] * DIM + 4 * (pt + 8 * u));
       }
-      if (!valid) x = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      float xn = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) xn = fmaf(x[e], x[e], xn);
-      *reinterpret_cast<floatx4*>(Xs + r * PX + 4 * (pt + 8 * u)) = x;
+      for (int u = 0; u < CH; ++u) {
+        floatx4 x = xv[ps][u];
+        if (a.prev_embed) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[e] = __fsub_rn(x[e], ev[u][e]);
+          if (chunk == 0 && valid && a.resid_out)
+            *reinterpret_cast<floatx4*>(a.resid_out + m * DIM + 4 * (pt + 8 * u)) = x;
+        }
+        if (!valid) x = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xn = fmaf(x[e], x[e], xn);
+        *reinterpret_cast<floatx4*>(Xs + r * PX + 4 * (pt + 8 * u)) = x;
+      }
+#pragma unroll
+      for (int o = 1; o < 8; o <<= 1) xn += __shfl_xor(xn, o, 64);
+      if (pt == 0) xnS[r] = xn;
     }
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) xn += __shfl_xor(xn, o, 64);
-    if (pt == 0) xnS[r] = xn;
   }
   __syncthreads();
 
   // ---- distance tiles.
-  const float xq = xnS[col];
-  float best_v = INFINITY;
-  int best_i = 0x7fffffff;
-  floatx16 acc;
+  float xq[QTN], best_vq[QTN];
+  int best_iq[QTN];
+  floatx16 accq[QTN];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  for (int qt = 0; qt < QTN; ++qt) {
+    xq[qt] = xnS[col + 32 * qt];
+    best_vq[qt] = INFINITY;
+    best_iq[qt] = 0x7fffffff;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) accq[qt][r] = 0.0f;
+  }
   for (int it = 0; it < (has_work ? items : 0); ++it) {
     if (it + 1 < items) load_piece(nxt, it + 1);
     const int pc = it % NPC;
-    const float* xrow = Xs + col * PX + kbase + 64 * pc + 32 * h;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const floatx4 b4 = *reinterpret_cast<const floatx4*>(xrow + 4 * j);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc = fm_mfma32(cur[j][e], b4[e], acc);
+      for (int qt = 0; qt < QTN; ++qt) {
+        const floatx4 b4 =
+            *reinterpret_cast<const floatx4*>(Xs + (col + 32 * qt) * PX + kbase + 64 * pc + 32 * h + 4 * j);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) accq[qt] = fm_mfma32(cur[j][e], b4[e], accq[qt]);
+      }
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) cur[j] = nxt[j];
     if (KP == 1 && pc == NPC - 1) {
       const int n0 = e_begin + 32 * (g + EG * (it / NPC));
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int entry = n0 + fm_mfma32_row(r, lane);
-        if (entry < e_end) {
-          const float d = __fadd_rn(__fadd_rn(__fmul_rn(-2.0f, acc[r]), xq), normS[entry - e_begin]);
-          const float dist = sqrtf(fmaxf(d, 0.0f));
-          if (better(dist, entry, best_v, best_i)) best_v = dist, best_i = entry;
+      for (int qt = 0; qt < QTN; ++qt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int entry = n0 + fm_mfma32_row(r, lane);
+          if (entry < e_end) {
+            const float d = __fadd_rn(__fadd_rn(__fmul_rn(-2.0f, accq[qt][r]), xq[qt]), normS[entry - e_begin]);
+            const float dist = sqrtf(fmaxf(d, 0.0f));
+            if (better(dist, entry, best_vq[qt], best_iq[qt])) best_vq[qt] = dist, best_iq[qt] = entry;
+          }
+          accq[qt][r] = 0.0f;
         }
-        acc[r] = 0.0f;
-      }
     }
   }
+  float best_v = best_vq[0];
+  int best_i = best_iq[0];
+  floatx16 acc = accq[0];
   if (KP > 1) {
     if (p > 0) {
       float* dst = red + ((p - 1) * EG + g) * 32 * PR;
@@ -409,27 +445,30 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a0, const f
         for (int pp = 1; pp < KP; ++pp) v = __fadd_rn(v, red[((pp - 1) * EG + g) * 32 * PR + row * PR + col]);
         const int entry = n0 + row;
         if (entry < e_end) {
-          const float d = __fadd_rn(__fadd_rn(__fmul_rn(-2.0f, v), xq), normS[entry - e_begin]);
+          const float d = __fadd_rn(__fadd_rn(__fmul_rn(-2.0f, v), xq[0]), normS[entry - e_begin]);
           const float dist = sqrtf(fmaxf(d, 0.0f));
           if (better(dist, entry, best_v, best_i)) best_v = dist, best_i = entry;
         }
       }
     }
   }
-  {
-    const float ov = __shfl_xor(best_v, 32, 64);
-    const int oi = __shfl_xor(best_i, 32, 64);
-    if (better(ov, oi, best_v, best_i)) best_v = ov, best_i = oi;
+  best_vq[0] = best_v;
+  best_iq[0] = best_i;
+#pragma unroll
+  for (int qt = 0; qt < QTN; ++qt) {
+    const float ov = __shfl_xor(best_vq[qt], 32, 64);
+    const int oi = __shfl_xor(best_iq[qt], 32, 64);
+    if (better(ov, oi, best_vq[qt], best_iq[qt])) best_vq[qt] = ov, best_iq[qt] = oi;
+    if (p == 0 && h == 0) bestv[g * RBT + col + 32 * qt] = best_vq[qt], besti[g * RBT + col + 32 * qt] = best_iq[qt];
   }
-  if (p == 0 && h == 0) bestv[g * RB + col] = best_v, besti[g * RB + col] = best_i;
   __syncthreads();
-  if (tid < RB) {
+  if (tid < RBT) {
     const long m = m0 + tid;
     float v = bestv[tid];
     int i = besti[tid];
 #pragma unroll
     for (int gg = 1; gg < EG; ++gg)
-      if (better(bestv[gg * RB + tid], besti[gg * RB + tid], v, i)) v = bestv[gg * RB + tid], i = besti[gg * RB + tid];
+      if (better(bestv[gg * RBT + tid], besti[gg * RBT + tid], v, i)) v = bestv[gg * RBT + tid], i = besti[gg * RBT + tid];
     if (m < a.M) {
       a.val[(long)chunk * a.M + m] = v;
       a.idx[(long)chunk * a.M + m] = i;
@@ -508,7 +547,7 @@ size_t step_lds_bytes(int dim) {
 // the launch has 512 blocks, multiples of NT entries.
 struct RvqPlan {
   bool fast;
-  int kp, chunks, ce, row_blocks;
+  int kp, qt, chunks, ce, row_blocks;
   size_t lds;
 };
 
@@ -518,6 +557,7 @@ RvqPlan rvq_plan(int rows, int dim, int entries) {
   pl.fast = (dim == 64 || dim == 128 || dim == 256);
   pl.chunks = 1;
   pl.kp = 1;
+  pl.qt = 1;
   constexpr int blocks_cap = 1024;
   if (pl.fast) {
     const int sub = (entries + 31) / 32;
@@ -526,6 +566,11 @@ RvqPlan rvq_plan(int rows, int dim, int entries) {
     } else if (dim >= 128 && (sub + 1) / 2 <= kMaxChunks && pl.row_blocks * ((sub + 1) / 2) <= blocks_cap) {
       pl.kp = 2, pl.chunks = (sub + 1) / 2;
     } else {
+      // Many rows: 64-row blocks (two query tiles per codebook fragment).
+      if (rows >= 1024 && entries <= kQt2MaxChunkEntries) {
+        pl.qt = 2;
+        pl.row_blocks = (rows + 2 * RB - 1) / (2 * RB);
+      }
       int per = 128;
       while ((entries + per - 1) / per > kMaxChunks || pl.row_blocks * ((entries + per - 1) / per) > blocks_cap) {
         if (per >= entries) break;
@@ -539,7 +584,8 @@ RvqPlan rvq_plan(int rows, int dim, int entries) {
   const int chunk_entries = pl.fast ? (pl.kp == 4 ? 32 : pl.kp == 2 ? 64 : (entries + pl.chunks - 1) / pl.chunks)
                                     : ((entries + pl.chunks - 1) / pl.chunks + NT - 1) / NT * NT;
   pl.ce = pl.fast && pl.kp == 1 ? (chunk_entries + 31) / 32 * 32 : chunk_entries;
-  pl.lds = pl.fast ? ((size_t)RB * (dim + 4) + RB + 2 * 4 * RB + 3 * 32 * (RB + 1) + pl.ce) * 4
+  // Dynamic LDS (64-row blocks use a static array instead).
+  pl.lds = pl.fast ? (pl.qt == 2 ? 0 : ((size_t)RB * (dim + 4) + RB + 2 * 4 * RB + 3 * 32 * (RB + 1) + pl.ce) * 4)
                    : step_lds_bytes(dim);
   return pl;
 }
@@ -602,7 +648,14 @@ int launch_fast_step(const RvqPlan& pl, int dim, dim3 grid, const StepArgs& a0, 
                      const StepArgs& a1, const float* e1, hipStream_t stream) {
 #define FM_RVQ(D, K) \
   hipLaunchKernelGGL((rvq_step_mfma_kernel<D, K>), grid, dim3(256), pl.lds, stream, a0, e0, a1, e1)
-  if (dim == 256 && pl.kp == 4) FM_RVQ(256, 4);
+#define FM_RVQ2(D) \
+  hipLaunchKernelGGL((rvq_step_mfma_kernel<D, 1, 2>), grid, dim3(256), 0, stream, a0, e0, a1, e1)
+  if (pl.qt == 2) {
+    if (dim == 256) FM_RVQ2(256);
+    else if (dim == 128) FM_RVQ2(128);
+    else FM_RVQ2(64);
+#undef FM_RVQ2
+  } else if (dim == 256 && pl.kp == 4) FM_RVQ(256, 4);
   else if (dim == 256 && pl.kp == 2) FM_RVQ(256, 2);
   else if (dim == 256) FM_RVQ(256, 1);
   else if (dim == 128 && pl.kp == 2) FM_RVQ(128, 2);

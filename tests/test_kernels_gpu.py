@@ -678,6 +678,10 @@ def rvq_encode_oracle(x, embeds, T):
     (3, 100, 3, 1000, 128),    # ragged last chunk
     (2, 70, 3, 100, 64),
     (2, 40, 3, 48, 8),         # general kernel (dim not in {64, 128, 256})
+    # 64-row blocks (>= 1024 rows): two query tiles per codebook fragment
+    (16, 125, 8, 2048, 256),
+    (11, 100, 5, 1000, 128),   # ragged last chunk
+    (17, 61, 3, 2048, 64),     # partial last row block
 ])
 def test_rvq_encode_matches_reference_loop(B, T, nq, e, d):
     g = torch.Generator().manual_seed(B * T + nq + e + d)
