@@ -417,6 +417,30 @@ def test_window_attention(B, T, H, D, window):
     close(out.cpu(), attention_reference(qkv, B, T, H, D, window, cos, sin), rel=5e-5)
 
 
+@pytest.mark.parametrize("B,T", [(1, 300), (16, 250), (1, 700)])
+def test_window_attention_grouped_kv_heads(B, T):
+    """kv_heads < heads: head h reads K/V head h // (heads / kv_heads), for the
+    16-query, whole-sequence and long-sequence kernels."""
+    H, KV, D, window = 8, 2, 64, 250
+    g = torch.Generator().manual_seed(B * 7 + T)
+    ld = (H + 2 * KV) * D
+    qkv = torch.randn(B * T, ld, generator=g)
+    cfg = MimiConfig()
+    cos, sin = rope_tables(cfg, T)
+    # Expanded to one K/V per query head, the reference formulas apply unchanged.
+    q = qkv[:, :H * D].view(B * T, H, D)
+    k = qkv[:, H * D:(H + KV) * D].view(B * T, KV, D).repeat_interleave(H // KV, dim=1)
+    v = qkv[:, (H + KV) * D:].view(B * T, KV, D).repeat_interleave(H // KV, dim=1)
+    full = torch.cat([q, k, v], 1).reshape(B * T, 3 * H * D)
+    out = torch.empty(B * T, H * D, device=DEV)
+    qkv_d, cos_d, sin_d = qkv.to(DEV), cos.to(DEV), sin.to(DEV)
+    nat.call("fm_window_attention", qkv_d.data_ptr(), ld, 0, H * D, (H + KV) * D, cos_d.data_ptr(),
+             sin_d.data_ptr(), B, T, H, KV, D, window, 1.0 / math.sqrt(D), out.data_ptr(), H * D,
+             stream())
+    torch.cuda.synchronize()
+    close(out.cpu(), attention_reference(full, B, T, H, D, window, cos, sin), rel=5e-5)
+
+
 @pytest.mark.parametrize("B,T", [(1, 300), (16, 250)])
 def test_window_attention_prerotated(B, T):
     """NULL RoPE tables: q/k are consumed as given (rotated by their producer)."""
