@@ -755,32 +755,35 @@ __global__ __launch_bounds__(64 * NWQ) void window_attention_flash_kernel(
     for (int r = 0; r < 4; ++r) orow[16 * dt + 4 * g + r] = o[dt][r] / l_run;
 }
 
+constexpr int SEQ_MAX = 256;
 // Whole-sequence attention for head_dim 64 and sequences of at most 256
 // frames (the batched 12.5-25 Hz transformers): one block per (half, head,
 // sequence) stages the head's K (rotated when ROPE) and V for every frame in
 // LDS once, so no key row is fetched twice by a block.  The 16 query tiles of
 // 16 frames are paired (j, 15 - j) so that every pair costs the same number
 // of key tiles under the causal mask; block half s owns pairs 4s .. 4s+3.
-// Waves w and w + 4 share pair w and split its key tiles (even / odd 32-key
-// tiles), then merge their (max, sum, O) through LDS after each query tile.
-// The inner step is the one of window_attention16_kernel: S^T = K Q^T on
-// 16x16x4 MFMA with K from 16-byte LDS reads and Q^T from registers, an
-// online softmax in base-2 units, and O^T += V^T P^T with P^T from the S^T
-// registers.  A key tile may run up to 31 rows past the staged frames; those
-// rows are masked, and the LDS layout (V, then K, then the merge area) keeps
-// such reads inside the array on finite values (V overruns read K rows).
-constexpr int SEQ_MAX = 256;
-template <bool ROPE>
-__global__ __launch_bounds__(512) void window_attention_seq_kernel(
+// NKS waves share a pair and take its key tiles round-robin; each keeps both
+// of its query tiles' (max, sum, O) in registers and the pair merges once at
+// the end, parking the states over the staged K/V.  The inner step is the one
+// of window_attention16_kernel: S^T = K Q^T on 16x16x4 MFMA with K from
+// 16-byte LDS reads and Q^T from registers, an online softmax in base-2
+// units, and O^T += V^T P^T with P^T from the S^T registers.  A key tile may
+// run up to 31 rows past the staged frames; those rows are masked.
+// Measured at C3 (B 16, 250 frames): 25.8 us per layer with NKS = 2; 27.2 us
+// with NKS = 3; 28.6 us when the pair merged after each query tile.
+template <bool ROPE, int NKS>
+__global__ __launch_bounds__(256 * NKS) void window_attention_seq_kernel(
     const float* __restrict__ qkv, int ld, int q_off, int k_off, int v_off,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, int T, int heads,
     int kv_heads, int window, float scale, float* __restrict__ out, int ld_out) {
-  constexpr int D = 64, QT = 16, PK = D + 4, PV = D + 4, P = QT + 1;
-  constexpr int PARK = D * P + 2 * QT;  // one wave pair's parked O^T, max and sum
-  __shared__ __attribute__((aligned(16))) float lds[SEQ_MAX * (PV + PK) + 4 * PARK];
-  float* Vs = lds;                       // [SEQ_MAX][PV]
-  float* Ks = Vs + SEQ_MAX * PV;          // [SEQ_MAX][PK]
-  float* park = Ks + SEQ_MAX * PK;        // [4][PARK]
+  constexpr int D = 64, QT = 16, PK = D + 4, PV = D + 4, P = QT + 1, NTH = 256 * NKS;
+  constexpr int PARK = D * P + 2 * QT;  // one parked (O^T, max, sum)
+  static_assert(4 * (NKS - 1) * 2 * PARK <= SEQ_MAX * (PV + PK), "states park over K/V");
+  // V, then K, then 32 rows that absorb the masked reads of a key tile that
+  // runs past the staged frames (V overruns read K rows).
+  __shared__ __attribute__((aligned(16))) float lds[SEQ_MAX * (PV + PK) + KB * PK];
+  float* Vs = lds;                 // [SEQ_MAX][PV]
+  float* Ks = Vs + SEQ_MAX * PV;    // [SEQ_MAX][PK]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, i = lane & 15;
@@ -790,13 +793,13 @@ __global__ __launch_bounds__(512) void window_attention_seq_kernel(
   const long b = blockIdx.z;
   const float* seq = qkv + b * (long)T * ld;
 
-  // Stage every frame's K (rotated) and V; rows T .. SEQ_MAX-1 are zero.
   {
-    constexpr int PAIRS = SEQ_MAX * D / 8, KN = PAIRS / 512;
+    constexpr int PAIRS = SEQ_MAX * D / 8, KN = (PAIRS + NTH - 1) / NTH;
     const float* kcol = seq + k_off + hk * D;
 #pragma unroll
     for (int u = 0; u < KN; ++u) {
-      const int e = tid + u * 512;
+      const int e = tid + u * NTH;
+      if (PAIRS % NTH && e >= PAIRS) break;
       const int r = e / (D / 8), d = (e % (D / 8)) * 4;
       const int t = min(r, T - 1);
       floatx4 lo = *reinterpret_cast<const floatx4*>(kcol + (long)t * ld + d);
@@ -804,17 +807,18 @@ __global__ __launch_bounds__(512) void window_attention_seq_kernel(
       if (r >= T) lo = hi = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
       if (ROPE) {
         const floatx4 c = *reinterpret_cast<const floatx4*>(cos_t + (long)t * D + d);
-        const floatx4 s = *reinterpret_cast<const floatx4*>(sin_t + (long)t * D + d);
-        rope_pair(lo, hi, c, s);
+        const floatx4 sn = *reinterpret_cast<const floatx4*>(sin_t + (long)t * D + d);
+        rope_pair(lo, hi, c, sn);
       }
       *reinterpret_cast<floatx4*>(Ks + r * PK + d) = lo;
       *reinterpret_cast<floatx4*>(Ks + r * PK + d + D / 2) = hi;
     }
-    constexpr int CH = SEQ_MAX * D / 4, VN = CH / 512;
+    constexpr int CH = SEQ_MAX * D / 4, VN = (CH + NTH - 1) / NTH;
     const float* vcol = seq + v_off + hk * D;
 #pragma unroll
     for (int u = 0; u < VN; ++u) {
-      const int e = tid + u * 512;
+      const int e = tid + u * NTH;
+      if (CH % NTH && e >= CH) break;
       const int r = e / (D / 4), d = (e % (D / 4)) * 4;
       floatx4 v = *reinterpret_cast<const floatx4*>(vcol + (long)min(r, T - 1) * ld + d);
       if (r >= T) v = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -824,9 +828,10 @@ __global__ __launch_bounds__(512) void window_attention_seq_kernel(
   __syncthreads();
 
   const float scale2 = scale * 1.44269504088896341f;
-  float* pk = park + pair * PARK;
   const int jp = blockIdx.x * 4 + pair;
-#pragma unroll 1
+  float m_st[2], l_st[2];
+  floatx4 o_st[2][4];
+#pragma unroll
   for (int half = 0; half < 2; ++half) {
     const int qt = half == 0 ? jp : 15 - jp;
     const int q0 = qt * QT;
@@ -837,7 +842,6 @@ __global__ __launch_bounds__(512) void window_attention_seq_kernel(
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     if (live) {
-      // Query i, dims 16g .. 16g+15, rotated in registers (RoPE pairs d, d +- 32).
       float qv[16];
       const float* qrow = seq + (long)min(q, T - 1) * ld + q_off + head * D;
 #pragma unroll
@@ -845,12 +849,12 @@ __global__ __launch_bounds__(512) void window_attention_seq_kernel(
         const int d = 16 * g + 4 * t4;
         floatx4 x = *reinterpret_cast<const floatx4*>(qrow + d);
         if (ROPE) {
-          const int dl = d & (D / 2 - 1);  // the pair's lower dim
+          const int dl = d & (D / 2 - 1);
           const floatx4 y = *reinterpret_cast<const floatx4*>(qrow + (d ^ (D / 2)));
           const floatx4 c = *reinterpret_cast<const floatx4*>(cos_t + (long)min(q, T - 1) * D + dl);
-          const floatx4 s = *reinterpret_cast<const floatx4*>(sin_t + (long)min(q, T - 1) * D + dl);
+          const floatx4 sn = *reinterpret_cast<const floatx4*>(sin_t + (long)min(q, T - 1) * D + dl);
           floatx4 lo = d < D / 2 ? x : y, hi = d < D / 2 ? y : x;
-          rope_pair(lo, hi, c, s);
+          rope_pair(lo, hi, c, sn);
           x = d < D / 2 ? lo : hi;
         }
 #pragma unroll
@@ -859,7 +863,7 @@ __global__ __launch_bounds__(512) void window_attention_seq_kernel(
       const int k_lo = max(0, q0 - window + 1);
       const int k_hi = min(T, q0 + QT) - 1;
       const int ntiles = (k_hi - k_lo + KB) / KB;
-      for (int tile = kh; tile < ntiles; tile += 2) {
+      for (int tile = kh; tile < ntiles; tile += NKS) {
         const int k0 = k_lo + tile * KB;
         const float* Kt = Ks + k0 * PK;
         const float* Vt = Vs + k0 * PV;
@@ -932,34 +936,57 @@ __global__ __launch_bounds__(512) void window_attention_seq_kernel(
           }
       }
     }
-    // Merge the pair: the odd-tile wave parks its state, the even-tile wave
-    // forms O = (O_0 f_0 + O_1 f_1) / (l_0 f_0 + l_1 f_1), f_w = 2^(m_w - M).
-    if (kh == 1) {
-      if (g == 0) pk[D * P + i] = m_run, pk[D * P + QT + i] = l_run;
+    m_st[half] = m_run;
+    l_st[half] = l_run;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o_st[half][dt] = o[dt];
+  }
+  // Merge: waves kh > 0 park their two states over the K/V (every wave is
+  // done reading them after this barrier); wave kh = 0 of each pair combines
+  // O = sum_w O_w f_w / sum_w l_w f_w, f_w = 2^(m_w - M), in key-split order.
+  __syncthreads();
+  if (kh > 0) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      float* pk = lds + ((pair * (NKS - 1) + kh - 1) * 2 + half) * PARK;
+      if (g == 0) pk[D * P + i] = m_st[half], pk[D * P + QT + i] = l_st[half];
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pk[(16 * dt + 4 * g + r) * P + i] = o[dt][r];
+        for (int r = 0; r < 4; ++r) pk[(16 * dt + 4 * g + r) * P + i] = o_st[half][dt][r];
     }
-    __syncthreads();
-    if (kh == 0 && live) {
-      const float m1 = pk[D * P + i], l1 = pk[D * P + QT + i];
-      const float M = fmaxf(m_run, m1);
-      const float f0 = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
-      const float f1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - M);
-      const float den = l_run * f0 + l1 * f1;
-      if (q < T) {
-        float* orow = out + (b * (long)T + q) * ld_out + head * D;
+  }
+  __syncthreads();
+  if (kh > 0) return;
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
+  for (int half = 0; half < 2; ++half) {
+    const int qt = half == 0 ? jp : 15 - jp;
+    const int q = qt * QT + i;
+    if (qt * QT >= T || q >= T) continue;
+    float M = m_st[half];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int d = 16 * dt + 4 * g + r;
-            orow[d] = (o[dt][r] * f0 + pk[d * P + i] * f1) / den;
-          }
+    for (int w = 1; w < NKS; ++w) M = fmaxf(M, lds[((pair * (NKS - 1) + w - 1) * 2 + half) * PARK + D * P + i]);
+    const float f0 = m_st[half] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_st[half] - M);
+    float den = l_st[half] * f0;
+    float fw[NKS];
+#pragma unroll
+    for (int w = 1; w < NKS; ++w) {
+      const float* pk = lds + ((pair * (NKS - 1) + w - 1) * 2 + half) * PARK;
+      const float mw = pk[D * P + i];
+      fw[w] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+      den += pk[D * P + QT + i] * fw[w];
+    }
+    float* orow = out + (b * (long)T + q) * ld_out + head * D;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = 16 * dt + 4 * g + r;
+        float num = o_st[half][dt][r] * f0;
+#pragma unroll
+        for (int w = 1; w < NKS; ++w) num += lds[((pair * (NKS - 1) + w - 1) * 2 + half) * PARK + d * P + i] * fw[w];
+        orow[d] = num / den;
       }
-    }
-    __syncthreads();  // the park area is free again
   }
 }
 
@@ -1567,12 +1594,13 @@ int fm_window_attention_rows(const float* qkv, int ld_qkv, int q_offset, int k_o
   if (head_dim == 64 && query_start == 0 && length <= SEQ_MAX && (long)batch * heads >= 128) {
     // Enough (sequence, head) pairs to fill the GPU with two blocks each.
     const dim3 gs(2, heads, batch);
+    constexpr int NKS = 2;
     if (cos_table)
-      hipLaunchKernelGGL((window_attention_seq_kernel<true>), gs, dim3(512), 0, stream, qkv,
+      hipLaunchKernelGGL((window_attention_seq_kernel<true, NKS>), gs, dim3(256 * NKS), 0, stream, qkv,
                          ld_qkv, q_offset, k_offset, v_offset, cos_table, sin_table, length, heads,
                          kv_heads, window, scale, out, ld_out);
     else
-      hipLaunchKernelGGL((window_attention_seq_kernel<false>), gs, dim3(512), 0, stream, qkv,
+      hipLaunchKernelGGL((window_attention_seq_kernel<false, NKS>), gs, dim3(256 * NKS), 0, stream, qkv,
                          ld_qkv, q_offset, k_offset, v_offset, cos_table, sin_table, length, heads,
                          kv_heads, window, scale, out, ld_out);
     return (int)hipGetLastError();
