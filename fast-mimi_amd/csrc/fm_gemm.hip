@@ -596,7 +596,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
 template <int BM, int BN, int WN, int BK, int NST, int WPE>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void gemm_dl_kernel(GemmArgs p) {
   constexpr int NTH = 512, WM = 2;
-  static_assert((BK == 16 || BK == 32) && (NST == 2 || NST == 3), "ring shape");
+  static_assert((BK == 16 || BK == 32 || BK == 64) && (NST == 2 || NST == 3), "ring shape");
   constexpr int CPR = BK / 4, RPI = 64 / CPR;  // chunks per row, rows per load instruction
   constexpr int SWR = 64 / BK;                 // rows per full sweep of the 64 banks
   static_assert(WM * WN == 8, "eight waves");
@@ -1161,7 +1161,8 @@ constexpr TileCfg kBig64 = {64, 128, 1, 32, 11, 0};    // double-buffered, 32x32
 // operands allow, see gemm_dl_kernel).
 constexpr TileCfg kDl128 = {128, 128, 1, 32, 13, 0};
 constexpr TileCfg kDl192 = {192, 128, 1, 32, 14, 0};
-constexpr TileCfg kDl64 = {64, 128, 1, 32, 15, 0};
+// 64x128 runs one block per CU: 64-deep k-tiles (96 KB ring) halve its barriers.
+constexpr TileCfg kDl64 = {64, 128, 1, 64, 15, 0};
 #ifndef FM_DL_MODE
 #define FM_DL_MODE 2
 #endif
@@ -1296,7 +1297,7 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
   if (FM_DL_MODE && dl_ok) {
     if (cfg.id == 9) cfg = kDl128;
     if (FM_DL_MODE >= 2 && cfg.id == 10) cfg = kDl192;
-    if (FM_DL_MODE >= 2 && cfg.id == 11) cfg = kDl64;
+    if (FM_DL_MODE >= 2 && cfg.id == 11 && p.C_in % 64 == 0 && p.K % 64 == 0) cfg = kDl64;
   }
   if (splits > 1) {
     const size_t per = (size_t)M * p.N * sizeof(float);
@@ -1328,7 +1329,7 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
 #undef FM_BIG
     case 13: hipLaunchKernelGGL((gemm_dl_kernel<128, 128, 4, 32, 2, 4>), grid, dim3(512), 0, s, p); break;
     case 14: hipLaunchKernelGGL((gemm_dl_kernel<192, 128, 4, 32, 2, 4>), grid, dim3(512), 0, s, p); break;
-    case 15: hipLaunchKernelGGL((gemm_dl_kernel<64, 128, 4, 32, 2, 4>), grid, dim3(512), 0, s, p); break;
+    case 15: hipLaunchKernelGGL((gemm_dl_kernel<64, 128, 4, 64, 2, 4>), grid, dim3(512), 0, s, p); break;
     case 7: hipLaunchKernelGGL((gemm_mid_kernel<64, 64, 1>), grid, dim3(NTHREADS), 0, s, p); break;
     case 8: hipLaunchKernelGGL((gemm_mid_kernel<32, 32, 4>), grid, dim3(NTHREADS), 0, s, p); break;
     default: hipLaunchKernelGGL(gemm_generic_kernel, grid, dim3(256), 0, s, p); break;

@@ -112,6 +112,7 @@ DL_CASES = [
     (16, 512, 512, 1, 1, 250, None),
     (1, 256, 512, 12, 6, 12003, None),
     (1, 2048, 512, 1, 1, 4000, None),   # long K, one 64x128 tile per CU, unsplit
+    (1, 480, 512, 1, 1, 4000, None),    # 64x128 pick with C_in % 64 == 32 (32-deep tile)
 ]
 
 
