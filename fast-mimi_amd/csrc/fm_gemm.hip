@@ -582,8 +582,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_big_kernel(GemmArgs p) {
 // lane * 16 bytes of the wave's 1 KB window), so the k-loop holds no prefetch
 // registers and issues no vector instructions to stage operands.  An NST-deep
 // LDS ring of BK-deep k-tiles is refilled NST - 1 k-tiles ahead, with one
-// barrier per k-tile (the shipped tiles: BK = 32, two stages; BK = 16 with
-// three stages measured slower).  Each lane picks the global chunk that
+// barrier per k-tile (the shipped tiles: two stages, BK = 32, or BK = 64 for
+// the one-block-per-CU 64x128 tile; BK = 16 with three stages measured
+// slower).  Each lane picks the global chunk that
 // belongs in its LDS slot: slot (row r, position cp) holds chunk
 // cp ^ ((r / SWR) % CPR) of row r, so the MFMA fragment reads (eight rows per
 // 16-byte read phase) spread over all 64 banks.  Loads that fall outside the
