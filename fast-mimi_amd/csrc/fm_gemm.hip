@@ -1164,9 +1164,6 @@ constexpr TileCfg kDl128 = {128, 128, 1, 32, 13, 0};
 constexpr TileCfg kDl192 = {192, 128, 1, 32, 14, 0};
 // 64x128 runs one block per CU: 64-deep k-tiles (96 KB ring) halve its barriers.
 constexpr TileCfg kDl64 = {64, 128, 1, 64, 15, 0};
-#ifndef FM_DL_MODE
-#define FM_DL_MODE 2
-#endif
 
 
 long tile_count(long M, int N, const TileCfg& t) {
@@ -1295,10 +1292,10 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
   // The direct-load tiles need every k-tile (32 deep) inside one tap.
   const bool dl_ok = big_ok && !(p.flags & (FM_REPLICATE | FM_ELU_IN)) && p.C_in % 32 == 0 &&
                      p.K % 32 == 0;
-  if (FM_DL_MODE && dl_ok) {
+  if (dl_ok) {
     if (cfg.id == 9) cfg = kDl128;
-    if (FM_DL_MODE >= 2 && cfg.id == 10) cfg = kDl192;
-    if (FM_DL_MODE >= 2 && cfg.id == 11 && p.C_in % 64 == 0 && p.K % 64 == 0) cfg = kDl64;
+    if (cfg.id == 10) cfg = kDl192;
+    if (cfg.id == 11 && p.C_in % 64 == 0 && p.K % 64 == 0) cfg = kDl64;
   }
   if (splits > 1) {
     const size_t per = (size_t)M * p.N * sizeof(float);

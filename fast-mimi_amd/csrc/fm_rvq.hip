@@ -27,6 +27,21 @@ FM_DEVICE bool better(float v, int i, float bv, int bi) {
   return v < bv || (v == bv && i < bi);
 }
 
+// cdist value of one mm-form distance as an argmin key.  torch's clamp_min
+// keeps a NaN and its argmin returns the first NaN, so a NaN maps to -inf:
+// it then beats every real distance (all >= 0) and ties between NaNs go to
+// the lowest index.  Non-finite input rows therefore still yield a valid code.
+FM_DEVICE float dist_key(float d) {
+  return d != d ? -INFINITY : sqrtf(fmaxf(d, 0.0f));
+}
+
+// A resolved code used as a gather index.  Every resolve visits at least one
+// entry, so the index is in range; the clamp keeps a gather inside the
+// codebook whatever the partials hold.
+FM_DEVICE int code_index(int code, int entries) {
+  return (unsigned)code < (unsigned)entries ? code : 0;
+}
+
 struct StepArgs {
   const float* resid_in;   // rows entering step j-1 (or step 0), row pitch ld_in
   int ld_in;
@@ -110,6 +125,7 @@ __global__ __launch_bounds__(256) void rvq_step_kernel(StepArgs a) {
     if (m < a.M) {
       float bv;
       resolve(a.prev_val, a.prev_idx, a.chunks, a.M, m, bv, code);
+      code = code_index(code, a.entries);
       if (chunk == 0) {
         const long b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
         a.prev_codes[b * a.batch_stride + t] = code;
@@ -213,7 +229,7 @@ __global__ __launch_bounds__(256) void rvq_step_kernel(StepArgs a) {
       for (int r = 0; r < 16; ++r) {
         const int row = fm_mfma32_row(r, lane);
         const float d = __fadd_rn(__fadd_rn(__fmul_rn(-2.0f, acc[r]), xn[row]), en);
-        const float dist = sqrtf(fmaxf(d, 0.0f));
+        const float dist = dist_key(d);
         if (better(dist, col, best_v[r], best_i[r])) best_v[r] = dist, best_i[r] = col;
       }
     }
@@ -340,6 +356,7 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a0, const f
         float bv;
         int bi;
         resolve8(a.prev_val, a.prev_idx, a.chunks, a.M, mc, pt, bv, bi);
+        bi = code_index(bi, a.entries);
         code[ps] = bi;
         if (chunk == 0 && pt == 0 && m < a.M) {
           const long b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
@@ -418,7 +435,7 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a0, const f
           const int entry = n0 + fm_mfma32_row(r, lane);
           if (entry < e_end) {
             const float d = __fadd_rn(__fadd_rn(__fmul_rn(-2.0f, accq[qt][r]), xq[qt]), normS[entry - e_begin]);
-            const float dist = sqrtf(fmaxf(d, 0.0f));
+            const float dist = dist_key(d);
             if (better(dist, entry, best_vq[qt], best_iq[qt])) best_vq[qt] = dist, best_iq[qt] = entry;
           }
           accq[qt][r] = 0.0f;
@@ -446,7 +463,7 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a0, const f
         const int entry = n0 + row;
         if (entry < e_end) {
           const float d = __fadd_rn(__fadd_rn(__fmul_rn(-2.0f, v), xq[0]), normS[entry - e_begin]);
-          const float dist = sqrtf(fmaxf(d, 0.0f));
+          const float dist = dist_key(d);
           if (better(dist, entry, best_v, best_i)) best_v = dist, best_i = entry;
         }
       }
@@ -479,7 +496,8 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a0, const f
 // Resolves the last step: 8 lanes per row (32 rows per block).
 __global__ __launch_bounds__(256) void rvq_finalize_kernel(const float* val, const int* idx,
                                                            int chunks, int M, int64_t* codes,
-                                                           int rows_per_batch, int batch_stride) {
+                                                           int rows_per_batch, int batch_stride,
+                                                           int entries) {
   const long m = (long)blockIdx.x * 32 + (threadIdx.x >> 3);
   const int pt = threadIdx.x & 7;
   float bv;
@@ -487,7 +505,7 @@ __global__ __launch_bounds__(256) void rvq_finalize_kernel(const float* val, con
   resolve8(val, idx, chunks, M, min(m, (long)M - 1), pt, bv, bi);
   if (m >= M || pt != 0) return;
   const long b = m / rows_per_batch, t = m - b * rows_per_batch;
-  codes[b * batch_stride + t] = bi;
+  codes[b * batch_stride + t] = code_index(bi, entries);
 }
 
 // embed = embed_sum / max(usage, eps); transposed copy; squared norms.
@@ -725,7 +743,7 @@ int fm_rvq_encode(const float* x, int ld_x, int rows, int rows_per_batch, int di
   const int last = (count - 1) & 1;
   hipLaunchKernelGGL(rvq_finalize_kernel, dim3((rows + 31) / 32), dim3(256), 0, stream,
                      br.val[last], br.idx[last], pl.chunks, rows,
-                     codes + (size_t)(count - 1) * rows_per_batch, rows_per_batch, batch_stride);
+                     codes + (size_t)(count - 1) * rows_per_batch, rows_per_batch, batch_stride, entries);
   return (int)hipGetLastError();
 }
 

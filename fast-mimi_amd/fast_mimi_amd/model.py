@@ -14,11 +14,12 @@ Differences, by design:
     it raises ``RuntimeError``;
   * ``MimiModel(config)`` initialises from a portable seeded generator
     (``weights.seeded_state_dict``) instead of the torch global RNG;
-  * checkpoints load from a local directory (``config.json`` +
-    ``model.safetensors``); there is no Hub download;
-  * streaming caches (``encoder_past_key_values``, ``padding_cache``,
-    ``use_streaming``, ``decoder_past_key_values``) are not implemented and
-    raise ``NotImplementedError`` when supplied.
+  * a Hub model id resolves only through an existing local Hugging Face cache
+    (``cache_dir`` / ``local_files_only``); nothing is downloaded;
+  * stateful calls (``encoder_past_key_values``, ``padding_cache``,
+    ``use_streaming``, ``decoder_past_key_values``) run eagerly, since their
+    cache lengths change from call to call; every other call replays a
+    captured hipGraph per input shape.
 """
 
 from __future__ import annotations
@@ -84,6 +85,20 @@ class MimiEncoderOutput(_OutputMixin):
 class MimiDecoderOutput(_OutputMixin):
     audio_values: torch.Tensor | None = None
     decoder_past_key_values: Any = None
+
+
+# Architecture fields the declared checkpoint must keep (``model.py:76-81``).
+DECLARED_MIMI_CONFIG = {"sampling_rate": 24_000, "frame_rate": 12.5, "audio_channels": 1,
+                        "codebook_size": 2_048}
+
+
+def assert_declared_mimi_config(config: MimiConfig) -> None:
+    """Reject architecture drift of the identity-locked checkpoint
+    (``_assert_declared_mimi_config``, ``model.py:92-100``)."""
+    for name, expected in DECLARED_MIMI_CONFIG.items():
+        actual = getattr(config, name)
+        if actual != expected:
+            raise RuntimeError(f"declared checkpoint config {name!r} changed: {actual!r} != {expected!r}")
 
 
 def _file_sha256(path: Path) -> str:
@@ -205,9 +220,17 @@ class MimiModel:
                         revision: str = KYUTAI_MIMI_REVISION, cache_dir=None,
                         local_files_only: bool = False, attention_backend: str = "sdpa",
                         device=None, dtype=None) -> "MimiModel":
-        """Load ``config.json`` + ``model.safetensors`` from a local directory,
-        strictly, with the reference's identity locks for the declared
-        checkpoint (revision, SHA-256, parameter count; ``model.py:2852-2941``)."""
+        """Load ``config.json`` + ``model.safetensors`` strictly
+        (``model.py:2852-2941``).
+
+        ``model_id`` is a local directory, or a Hub repository id resolved by
+        ``huggingface_hub.hf_hub_download(..., revision, cache_dir,
+        local_files_only)`` exactly as the reference does (``:2898-2920``); with
+        ``local_files_only=True`` that reads an existing cache and never touches
+        the network.  The declared ``kyutai/mimi`` checkpoint keeps the
+        reference's identity locks, in its order: revision, declared config
+        fields (``_assert_declared_mimi_config``, ``:92-100``), weights SHA-256,
+        parameter count."""
         from safetensors.torch import load_file
 
         declared = str(model_id) == KYUTAI_MIMI_MODEL_ID
@@ -215,23 +238,32 @@ class MimiModel:
             raise ValueError(
                 f"declared kyutai/mimi revision changed: {revision!r} != {KYUTAI_MIMI_REVISION!r}")
         path = Path(model_id)
-        if not path.is_dir():
-            raise OSError(f"{model_id!r} is not a local checkpoint directory (no Hub access)")
-        config = MimiConfig.from_json_file(path / "config.json")
-        weights = path / "model.safetensors"
+        if path.exists():
+            config_path, weights = path / "config.json", path / "model.safetensors"
+        else:
+            from huggingface_hub import hf_hub_download
+
+            config_path, weights = (
+                Path(hf_hub_download(str(model_id), name, revision=revision, cache_dir=cache_dir,
+                                     local_files_only=local_files_only))
+                for name in ("config.json", "model.safetensors"))
+        config = MimiConfig.from_json_file(config_path)
         if declared:
+            assert_declared_mimi_config(config)
             digest = _file_sha256(weights)
             if digest != KYUTAI_MIMI_WEIGHTS_SHA256:
-                raise RuntimeError(f"declared kyutai/mimi checkpoint digest changed: {digest}")
+                raise RuntimeError(
+                    f"declared kyutai/mimi checkpoint digest changed: {digest} != {KYUTAI_MIMI_WEIGHTS_SHA256}")
         model = cls(config, attention_backend=attention_backend)
         model.load_state_dict(load_file(str(weights), device="cpu"), strict=True)
         if declared:
             count = sum(p.numel() for p in model.parameters())
             if count != KYUTAI_MIMI_PARAMETER_COUNT:
-                raise RuntimeError(f"declared kyutai/mimi parameter count changed: {count}")
+                raise RuntimeError(
+                    f"declared kyutai/mimi parameter count changed: {count} != {KYUTAI_MIMI_PARAMETER_COUNT}")
         if device is not None or dtype is not None:
             model.to(device=device, dtype=dtype)
-        return model
+        return model.eval()
 
     def save_pretrained(self, directory: str | Path) -> None:
         from safetensors.torch import save_file
@@ -340,8 +372,11 @@ class MimiModel:
             raise ValueError(f"audio_codes must hold 1..{self.config.num_quantizers} codebooks")
         rt = self.runtime()
         codes = self._on_device(audio_codes, torch.int64)
-        if codes.numel() and (int(codes.min()) < 0 or int(codes.max()) >= self.config.codebook_size):
-            raise IndexError("audio code out of range of the codebook")
+        if codes.numel():
+            lo, hi = torch.aminmax(codes)
+            lo, hi = torch.stack((lo, hi)).tolist()  # one device->host sync
+            if lo < 0 or hi >= self.config.codebook_size:
+                raise IndexError("audio code out of range of the codebook")
         out_len = None if padding_mask is None else padding_mask.shape[-1]
         frames = codes.shape[-1]
         kv = decoder_past_key_values
@@ -420,10 +455,11 @@ class MimiModel:
         return n
 
     def get_audio_codes_mask(self, padding_mask: torch.Tensor, padding_side: str = "right") -> torch.Tensor:
-        """Sample mask -> frame mask (``model.py:3026-3045``)."""
+        """Sample mask -> frame mask (``model.py:3026-3045``), with the
+        reference's broadcasting: a 2-D ``[B, S]`` mask gives ``[B, T]``; a
+        3-D ``[B, C, S]`` mask gives ``[B, B, T]`` (the per-row lengths
+        ``[B, C]`` gain a trailing axis and broadcast against ``[B, T]``)."""
         lengths = self.get_encoded_length(padding_mask.sum(dim=-1))
-        if lengths.ndim > 1:
-            lengths = lengths.reshape(lengths.shape[0], -1)[:, 0]
         mask = torch.arange(int(lengths.max()), device=lengths.device).expand(len(lengths), -1)
         mask = mask < lengths.unsqueeze(1)
         return mask if padding_side == "right" else mask.flip(-1)

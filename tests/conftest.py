@@ -42,5 +42,12 @@ def golden():
     return np.load(GOLDEN / "reference_golden.npz")
 
 
+@pytest.fixture(scope="session")
+def golden_large():
+    """Reference outputs of the larger benchmark configurations (C3, C4, C5 clips)
+    and of ``get_audio_codes_mask``."""
+    return np.load(GOLDEN / "reference_golden_large.npz")
+
+
 def gpu_available() -> bool:
     return torch.cuda.is_available()

@@ -7,7 +7,12 @@ as small ``.npz`` fixtures next to this script.  Nothing at test time imports
 the reference; the fixtures are data: inputs, codes, waveforms (full or
 decimated plus a SHA-256 of the full float32 bytes) and the checkpoint layout.
 
-Usage:  python tests/golden/make_golden.py [/root/reference/src]
+Usage:  python tests/golden/make_golden.py [/root/reference/src] [--large-only]
+
+``reference_golden.npz`` holds the small configurations; the larger
+benchmark configurations (batch 16 with a padded tail, the 100 s clip, the
+32-codebook clips) and ``get_audio_codes_mask`` outputs go to
+``reference_golden_large.npz``.
 """
 
 from __future__ import annotations
@@ -23,7 +28,8 @@ import torch
 HERE = Path(__file__).resolve().parent
 REPO = HERE.parents[1]
 sys.path.insert(0, str(REPO / "fast-mimi_amd"))
-sys.path.insert(0, sys.argv[1] if len(sys.argv) > 1 else "/root/reference/src")
+ARGS = [a for a in sys.argv[1:] if not a.startswith("--")]
+sys.path.insert(0, ARGS[0] if ARGS else "/root/reference/src")
 
 import fast_mimi as reference  # noqa: E402  (the reference package)
 from fast_mimi_amd import synthetic  # noqa: E402
@@ -59,8 +65,46 @@ def sha(a: np.ndarray) -> str:
     return hashlib.sha256(np.ascontiguousarray(a, dtype=np.float32).tobytes()).hexdigest()
 
 
+def large(full) -> None:
+    """Benchmark configurations C3-C5 and the frame-mask helper."""
+    out: dict[str, np.ndarray] = {}
+    # C3: the whole padded batch of 16 in one reference call.
+    a, m, nq = synthetic.config_inputs("c3")
+    codes, wave = run(full, a, m, nq)
+    out["c3_codes"] = codes
+    for c in (0, 12, 15):
+        out[f"c3_clip{c}_values_dec10"] = wave[c:c + 1, :, ::10]
+    out["c3_values_sha256"] = np.array([sha(wave[c]) for c in range(wave.shape[0])])
+    # C4: one 100 s clip.
+    a, m, nq = synthetic.config_inputs("c4")
+    codes, wave = run(full, a, m, nq)
+    out["c4_codes"], out["c4_values_dec100"] = codes, wave[..., ::100]
+    out["c4_values_sha256"] = np.array(sha(wave))
+    # C5 (32 codebooks): its first and last clips, each as a batch of one.
+    a, m, nq = synthetic.config_inputs("c5")
+    for c in (0, 63):
+        codes, wave = run(full, a[c:c + 1], m[c:c + 1], nq)
+        out[f"c5_clip{c}_codes"], out[f"c5_clip{c}_values_dec10"] = codes, wave[..., ::10]
+        out[f"c5_clip{c}_values_sha256"] = np.array(sha(wave))
+    # get_audio_codes_mask on 2-D and 3-D sample masks, both padding sides.
+    lengths = [24_000, 1_921, 17, 0]
+    mask2 = np.zeros((len(lengths), 24_000), dtype=bool)
+    for i, n in enumerate(lengths):
+        mask2[i, :n] = True
+    out["codes_mask_in_2d"] = mask2
+    for side in ("right", "left"):
+        out[f"codes_mask_2d_{side}"] = full.get_audio_codes_mask(torch.from_numpy(mask2), side).numpy()
+        out[f"codes_mask_3d_{side}"] = full.get_audio_codes_mask(
+            torch.from_numpy(mask2[:, None]), side).numpy()
+    np.savez_compressed(HERE / "reference_golden_large.npz", **out)
+    print("wrote", len(out), "large arrays")
+
+
 def main() -> None:
     torch.manual_seed(0)
+    if "--large-only" in sys.argv:
+        large(build({}, 0))
+        return
     out: dict[str, np.ndarray] = {}
 
     # ---- tiny config (the reference's own test config) ----
@@ -111,6 +155,7 @@ def main() -> None:
             [wave.min(), wave.max(), float(np.sqrt(np.mean(wave.astype(np.float64) ** 2)))])
 
     np.savez_compressed(HERE / "reference_golden.npz", **out)
+    large(full)
 
     layout = [[k, list(v.shape)] for k, v in full.state_dict().items()]
     (HERE / "reference_state_layout.json").write_text(json.dumps(layout) + "\n")

@@ -130,3 +130,62 @@ def test_strict_load_rejects_missing_and_mismatched() -> None:
     bad["encoder.layers.0.conv.bias"] = torch.zeros(3)
     with pytest.raises(RuntimeError, match="size mismatch"):
         model.load_state_dict(bad)
+
+
+@pytest.mark.parametrize("side", ["right", "left"])
+@pytest.mark.parametrize("ndim", [2, 3])
+def test_audio_codes_mask_matches_reference(golden_large, ndim, side) -> None:
+    """2-D masks give [B, T]; 3-D [B, 1, S] masks broadcast to [B, B, T] as the
+    reference's do (model.py:3040-3044); fixtures from the reference itself."""
+    model = MimiModel(MimiConfig())
+    mask = torch.from_numpy(golden_large["codes_mask_in_2d"])
+    if ndim == 3:
+        mask = mask[:, None]
+    got = model.get_audio_codes_mask(mask, side)
+    want = torch.from_numpy(golden_large[f"codes_mask_{ndim}d_{side}"])
+    assert got.dtype == torch.bool and torch.equal(got, want)
+
+
+def _hub_cache(root: Path, repo_id: str, commit: str, config: MimiConfig, weights: bytes | None,
+               model: MimiModel | None = None) -> None:
+    """The huggingface_hub cache layout: refs/main -> commit, snapshots/<commit>/files."""
+    repo = root / ("models--" + repo_id.replace("/", "--"))
+    snap = repo / "snapshots" / commit
+    snap.mkdir(parents=True)
+    (repo / "refs").mkdir()
+    (repo / "refs" / "main").write_text(commit)
+    config.save_pretrained(snap)
+    if model is not None:
+        model.save_pretrained(snap)
+    else:
+        (snap / "model.safetensors").write_bytes(weights)
+
+
+def test_hub_id_resolves_through_local_cache(tmp_path) -> None:
+    """A Hub repository id loads from an existing cache with local_files_only
+    (model.py:2898-2920); no network access is attempted."""
+    cfg = MimiConfig(**TINY)
+    model = MimiModel(cfg, seed=9)
+    commit = "0123456789abcdef0123456789abcdef01234567"
+    _hub_cache(tmp_path, "someone/mimi-tiny", commit, cfg, None, model)
+    for rev in ("main", commit):
+        loaded = MimiModel.from_pretrained("someone/mimi-tiny", revision=rev, cache_dir=tmp_path,
+                                           local_files_only=True)
+        assert loaded.config == cfg
+        sa, sb = model.state_dict(), loaded.state_dict()
+        assert all(torch.equal(sa[k], sb[k]) for k in sa)
+    with pytest.raises(OSError):  # not cached, and the network may not be used
+        MimiModel.from_pretrained("someone/absent", revision="main", cache_dir=tmp_path,
+                                  local_files_only=True)
+
+
+def test_declared_checkpoint_config_and_digest_are_locked(tmp_path) -> None:
+    """kyutai/mimi keeps its identity locks through the cache: drifted declared
+    config fields fail first (model.py:92-100), then a changed weights digest."""
+    drifted = MimiConfig(frame_rate_override=25.0)
+    _hub_cache(tmp_path / "a", KYUTAI_MIMI_MODEL_ID, KYUTAI_MIMI_REVISION, drifted, b"not the weights")
+    with pytest.raises(RuntimeError, match="declared checkpoint config 'frame_rate' changed"):
+        MimiModel.from_pretrained(KYUTAI_MIMI_MODEL_ID, cache_dir=tmp_path / "a", local_files_only=True)
+    _hub_cache(tmp_path / "b", KYUTAI_MIMI_MODEL_ID, KYUTAI_MIMI_REVISION, MimiConfig(), b"not the weights")
+    with pytest.raises(RuntimeError, match="digest changed"):
+        MimiModel.from_pretrained(KYUTAI_MIMI_MODEL_ID, cache_dir=tmp_path / "b", local_files_only=True)

@@ -1,14 +1,19 @@
 """End-to-end parity of ``MimiModel`` on the GPU against the CPU oracle and the
 reference's golden vectors.
 
-Bar: RVQ codes equal the reference's (a mismatch is only tolerated when the
-float64 re-evaluation certifies a near-tie, and is reported); decoded audio
-from the *same* codes within max-abs 1e-4 and SNR >= 60 dB of the reference.
+Bar: RVQ codes bit-exact with the reference's at every configuration the
+fixtures pin (1 s, batch 2 at 32 codebooks, C1, C2, the batch-16 padded C3).
+Only the 100 s clip (C4) and the 32-codebook clips (C5) may hold certified
+near-ties, at most as many as recorded and no wider (``rvq_check``).  Decoded
+audio from the *same* codes within max-abs 1e-4 and SNR >= 60 dB of the
+reference.
 """
 
 from __future__ import annotations
 
+import json
 import math
+import os
 
 import numpy as np
 import pytest
@@ -16,11 +21,16 @@ import torch
 
 from conftest import TINY, torch_state, tiny_config
 from fast_mimi_amd import MimiConfig, MimiKVCache, MimiModel, synthetic
+from fast_mimi_amd import _native as nat
 from oracle.mimi_oracle import MimiOracle, Trace
-from rvq_check import certify
+from rvq_check import check_codes, first_divergence, reference_rvq_rows
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
+
+# Certified near-ties recorded per configuration against the reference fixtures:
+# (code rows, widest relative gap); C5 is per clip.
+NEAR_TIE_BOUND = {"c4": (1, 3e-8), "c5": (1, 1.1e-7)}
 
 
 def snr_db(got: torch.Tensor, want: torch.Tensor) -> float:
@@ -30,10 +40,65 @@ def snr_db(got: torch.Tensor, want: torch.Tensor) -> float:
 
 
 def assert_audio(got: torch.Tensor, want: torch.Tensor, max_abs=1e-4, min_snr=60.0):
-    assert got.shape == want.shape
+    assert got.shape == want.shape, (got.shape, want.shape)
     err = (got.double() - want.double()).abs().max().item()
     snr = snr_db(got, want)
     assert err <= max_abs and snr >= min_snr, f"max-abs {err:.3e}, SNR {snr:.1f} dB"
+
+
+def record(what: str, **fields) -> None:
+    """Parity figures of a test, printed and (with PARITY_LOG set) kept as JSON lines."""
+    line = json.dumps({"test": what, **fields})
+    print(line)
+    path = os.environ.get("PARITY_LOG")
+    if path:
+        with open(path, "a") as f:
+            f.write(line + "\n")
+
+
+def gpu_rerun(model):
+    """The GPU chain of codebooks j0 .. j0+count-1 (global codebook order) on rows x."""
+    rt = model.runtime()
+    lib = nat.library()
+
+    def rerun(x, j0, count):
+        R, d = x.shape
+        e = model.config.codebook_size
+        xd = x.to(DEV).contiguous()
+        codes = torch.empty(count, R, dtype=torch.int64, device=DEV)
+        wsb = lib.fm_rvq_workspace_bytes(R, d, e)
+        ws = torch.empty((wsb + 3) // 4, device=DEV)
+        nat.call("fm_rvq_encode", xd.data_ptr(), d, R, R, d, e, count, rt.embeds[j0].data_ptr(),
+                 rt.embeds_t[j0].data_ptr(), rt.norms[j0].data_ptr(), codes.data_ptr(), count * R,
+                 ws.data_ptr(), wsb, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        return codes.cpu()
+
+    return rerun
+
+
+def chain_rows(oracle, trace, want, n_semantic):
+    """Residual rows entering each codebook along the code chain ``want``,
+    starting from the oracle's projected RVQ inputs.  Equal to the oracle's own
+    rows where its codes are ``want``; needed where ``want`` comes from a
+    reference run on another host CPU, whose ulp-level differences can resolve
+    a near-tie the other way."""
+    embeds = [oracle.embed(f"{p}.codebook") for p, _ in trace.rvq_inputs]
+    nq = want.shape[1]
+    flat = want.transpose(0, 1).reshape(nq, -1)
+    rows = reference_rvq_rows(trace.rvq_inputs[0][1], embeds[:n_semantic], flat[:n_semantic])
+    if nq > n_semantic:
+        rows += reference_rvq_rows(trace.rvq_inputs[n_semantic][1], embeds[n_semantic:], flat[n_semantic:])
+    return rows, embeds
+
+
+def compare_codes(model, oracle, trace, got, want, what, allow=None):
+    rows, embeds = chain_rows(oracle, trace, want, model.config.num_semantic_quantizers)
+    report = check_codes(got, want, rows, embeds, model.config.num_semantic_quantizers,
+                         gpu_rerun(model), allow)
+    record(what, near_ties=report.count, worst_gap=report.worst_gap,
+           codes_bit_exact=bool(torch.equal(got, want)))
+    return report
 
 
 @pytest.fixture(scope="module")
@@ -50,18 +115,16 @@ def full():
     return model, MimiOracle(cfg, torch_state(cfg, 0))
 
 
-def check_against_oracle(model, oracle, audio, mask, nq):
+def check_against_oracle(model, oracle, audio, mask, nq, what, allow=None):
+    """GPU round trip vs the oracle: codes bit-exact (or near-ties within
+    ``allow``), audio of the same codes within max-abs 1e-4 / 60 dB."""
     out = model(audio.to(DEV), mask.to(DEV) if mask is not None else None, num_quantizers=nq)
     trace = Trace()
     ref_codes, ref_audio = oracle.forward(audio, mask, nq, trace=trace)
     got_codes = out.audio_codes.cpu()
     assert got_codes.shape == ref_codes.shape and got_codes.dtype == torch.int64
+    compare_codes(model, oracle, trace, got_codes, ref_codes, what, allow)
     if not torch.equal(got_codes, ref_codes):
-        rows = [r for _, r in trace.rvq_inputs]
-        embeds = [oracle.embed(f"{p}.codebook") for p, _ in trace.rvq_inputs]
-        # The trace holds the reference's rows per codebook in chain order.
-        n, worst = certify(rows, embeds, got_codes, ref_codes)
-        print(f"{n} certified near-tie code rows (worst gap {worst:.2e})")
         # Decode the GPU's codes on both sides so audio compares like for like.
         ref_audio = oracle.decode(got_codes, mask if mask is not None else torch.ones_like(audio, dtype=torch.bool))
     assert_audio(out.audio_values.cpu(), ref_audio)
@@ -89,7 +152,7 @@ def test_tiny_padding_boundaries_and_window(tiny, golden, length):
 def test_full_one_second_matches_reference_golden(full, golden):
     model, oracle = full
     audio, mask = synthetic.batch(1, 24_000)
-    out = check_against_oracle(model, oracle, torch.from_numpy(audio), torch.from_numpy(mask), 8)
+    out = check_against_oracle(model, oracle, torch.from_numpy(audio), torch.from_numpy(mask), 8, "full_1s")
     assert torch.equal(out.audio_codes.cpu(), torch.from_numpy(golden["full_1s_codes"]).long())
     assert_audio(out.audio_values.cpu(), torch.from_numpy(golden["full_1s_values"]))
 
@@ -97,53 +160,87 @@ def test_full_one_second_matches_reference_golden(full, golden):
 def test_full_batch_padded_32_codebooks(full, golden):
     model, oracle = full
     audio, mask = synthetic.batch(2, 48_000, padded_tail=1, padded_length=28_800)
-    out = check_against_oracle(model, oracle, torch.from_numpy(audio), torch.from_numpy(mask), 32)
-    print("codes equal golden:", torch.equal(out.audio_codes.cpu(), torch.from_numpy(golden["full_b2_codes"]).long()))
+    out = check_against_oracle(model, oracle, torch.from_numpy(audio), torch.from_numpy(mask), 32, "full_b2_nq32")
+    assert torch.equal(out.audio_codes.cpu(), torch.from_numpy(golden["full_b2_codes"]).long())
+    assert_audio(out.audio_values.cpu()[..., ::10], torch.from_numpy(golden["full_b2_values_dec10"]))
 
 
 @pytest.mark.parametrize("name", ["c1", "c2"])
-def test_benchmark_configs_match_oracle(full, golden, name):
+def test_benchmark_configs_match_reference(full, golden, name):
     model, oracle = full
     audio, mask, nq = synthetic.config_inputs(name)
-    out = check_against_oracle(model, oracle, torch.from_numpy(audio), torch.from_numpy(mask), nq)
-    same = torch.equal(out.audio_codes.cpu(), torch.from_numpy(golden[f"full_{name}_codes"]).long())
-    print(f"{name}: codes bit-exact vs reference golden: {same}")
+    out = check_against_oracle(model, oracle, torch.from_numpy(audio), torch.from_numpy(mask), nq, name)
+    assert torch.equal(out.audio_codes.cpu(), torch.from_numpy(golden[f"full_{name}_codes"]).long())
+    assert_audio(out.audio_values.cpu()[..., ::10], torch.from_numpy(golden[f"full_{name}_values_dec10"]))
 
 
-@pytest.mark.parametrize("name,clips", [("c3", [0, 5, 12, 15]), ("c4", [0]), ("c5", [0, 31, 63])])
-def test_large_configs_match_oracle_per_clip(full, name, clips):
-    """Batch-16 (padded tail), 100 s and batch-64 / 32-codebook configurations at full size.
-
-    Clips are independent through the whole round trip, so the GPU batch is
-    checked clip by clip against the oracle run on those clips alone.
-    """
+def test_c3_padded_batch_matches_reference(full, golden_large):
+    """Batch 16, last four clips zero-padded from 6 s: every clip's codes
+    bit-exact with the reference's batched call; audio of clips 0, 12, 15
+    against the reference's (decimated) and of clips 0 and 12 against the
+    oracle at full resolution."""
     model, oracle = full
-    audio, mask, nq = synthetic.config_inputs(name)
+    audio, mask, nq = synthetic.config_inputs("c3")
     a, m = torch.from_numpy(audio), torch.from_numpy(mask)
     out = model(a.to(DEV), m.to(DEV), num_quantizers=nq)
     codes, values = out.audio_codes.cpu(), out.audio_values.cpu()
     model.release_graphs()
-    assert codes.shape == (audio.shape[0], nq, int(model.get_encoded_length(audio.shape[-1])))
-    for c in clips:
-        trace = Trace()
-        ref_codes, ref_audio = oracle.forward(a[c:c + 1], m[c:c + 1], nq, trace=trace)
-        got = codes[c:c + 1]
-        if not torch.equal(got, ref_codes):
-            rows = [r for _, r in trace.rvq_inputs]
-            embeds = [oracle.embed(f"{p}.codebook") for p, _ in trace.rvq_inputs]
-            n, worst = certify(rows, embeds, got, ref_codes)
-            print(f"{name} clip {c}: {n} certified near-tie code rows (worst gap {worst:.2e})")
-            ref_audio = oracle.decode(got, m[c:c + 1])
+    want = torch.from_numpy(golden_large["c3_codes"]).long()
+    record("c3", codes_bit_exact=bool(torch.equal(codes, want)),
+           differing_codes=int((codes != want).sum()))
+    assert torch.equal(codes, want)
+    for c in (0, 12, 15):
+        assert_audio(values[c:c + 1, :, ::10], torch.from_numpy(golden_large[f"c3_clip{c}_values_dec10"]))
+    for c in (0, 12):
+        _, ref_audio = oracle.forward(a[c:c + 1], m[c:c + 1], nq)
         assert_audio(values[c:c + 1], ref_audio)
 
 
-def _codes_match_or_near_tie(oracle, trace, got, want, what):
-    if torch.equal(got, want):
-        return
-    rows = [r for _, r in trace.rvq_inputs]
-    embeds = [oracle.embed(f"{p}.codebook") for p, _ in trace.rvq_inputs]
-    n, worst = certify(rows, embeds, got, want)
-    print(f"{what}: {n} certified near-tie code rows (worst gap {worst:.2e})")
+def test_c4_long_clip_matches_reference(full, golden_large):
+    """100 s clip: codes against the reference's, certified near-ties within the
+    recorded bound; audio of the GPU's codes against the oracle's decode."""
+    model, oracle = full
+    audio, mask, nq = synthetic.config_inputs("c4")
+    a, m = torch.from_numpy(audio), torch.from_numpy(mask)
+    out = model(a.to(DEV), m.to(DEV), num_quantizers=nq)
+    codes, values = out.audio_codes.cpu(), out.audio_values.cpu()
+    model.release_graphs()
+    trace = Trace()
+    ref_codes = oracle.encode(a, nq, trace)
+    want = torch.from_numpy(golden_large["c4_codes"]).long()
+    # The oracle on this host's CPU may resolve a near-tie unlike the reference
+    # run that wrote the fixture (the CPU test pins them equal on that host).
+    record("c4_host_oracle_vs_reference", differing_rows=len(first_divergence(ref_codes, want)))
+    compare_codes(model, oracle, trace, codes, want, "c4", NEAR_TIE_BOUND["c4"])
+    if torch.equal(codes, want):
+        assert_audio(values[..., ::100], torch.from_numpy(golden_large["c4_values_dec100"]))
+    assert_audio(values, oracle.decode(codes, m))
+
+
+def test_c5_32_codebooks_matches_reference(full, golden_large):
+    """Batch 64 at 32 codebooks: clips 0 and 63 against the reference's codes
+    (certified near-ties within the recorded bound) and audio."""
+    model, oracle = full
+    audio, mask, nq = synthetic.config_inputs("c5")
+    a, m = torch.from_numpy(audio), torch.from_numpy(mask)
+    out = model(a.to(DEV), m.to(DEV), num_quantizers=nq)
+    codes, values = out.audio_codes.cpu(), out.audio_values.cpu()
+    model.release_graphs()
+    assert codes.shape == (64, 32, 125)
+    for c in (0, 63):
+        trace = Trace()
+        ref_codes = oracle.encode(a[c:c + 1], nq, trace)
+        want = torch.from_numpy(golden_large[f"c5_clip{c}_codes"]).long()
+        record(f"c5_clip{c}_host_oracle_vs_reference", differing_rows=len(first_divergence(ref_codes, want)))
+        got = codes[c:c + 1]
+        compare_codes(model, oracle, trace, got, want, f"c5_clip{c}", NEAR_TIE_BOUND["c5"])
+        if torch.equal(got, want):
+            assert_audio(values[c:c + 1, :, ::10], torch.from_numpy(golden_large[f"c5_clip{c}_values_dec10"]))
+        assert_audio(values[c:c + 1], oracle.decode(got, m[c:c + 1]))
+
+
+def _codes_match_or_near_tie(model, oracle, trace, got, want, what):
+    compare_codes(model, oracle, trace, got, want, what, allow=(2, 1e-6))
 
 
 @pytest.mark.parametrize("batch,samples,chunk", [(1, 40, 8), (2, 96, 16), (1, 200, 24), (1, 72, 12)])
@@ -161,7 +258,7 @@ def test_streaming_encode_tiny(tiny, batch, samples, chunk):
         kv, pc = out.encoder_past_key_values, out.padding_cache
         trace = Trace()
         want = oracle.encode_stream(piece, 4, state, trace)
-        _codes_match_or_near_tie(oracle, trace, out.audio_codes.cpu(), want, "tiny stream")
+        _codes_match_or_near_tie(model, oracle, trace, out.audio_codes.cpu(), want, "tiny stream")
         assert kv.get_seq_length() == state.encoder_kv.length
 
 
@@ -178,7 +275,7 @@ def test_streaming_encode_full_config(full):
         kv, pc = out.encoder_past_key_values, out.padding_cache
         trace = Trace()
         want = oracle.encode_stream(piece, 8, state, trace)
-        _codes_match_or_near_tie(oracle, trace, out.audio_codes.cpu(), want, "full stream")
+        _codes_match_or_near_tie(model, oracle, trace, out.audio_codes.cpu(), want, "full stream")
     assert kv.get_seq_length() == state.encoder_kv.length == 15_360 // 960
 
 
@@ -220,6 +317,11 @@ def test_decode_only_and_encode_only(full):
     a = torch.from_numpy(audio)
     enc = model.encode(a.to(DEV), num_quantizers=8)
     codes = enc.audio_codes
+    # encode() runs its own captured graph: its codes against the oracle's.
+    trace = Trace()
+    want = oracle.encode(a, 8, trace)
+    compare_codes(model, oracle, trace, codes.cpu(), want, "encode_only")
+    assert torch.equal(model.encode(a.to(DEV), num_quantizers=8).audio_codes, codes)  # replay
     dec = model.decode(codes)
     ref = oracle.decode(codes.cpu())
     assert dec.audio_values.shape == (1, 1, 48_000)
@@ -262,3 +364,16 @@ def test_errors(full):
         model(torch.zeros(1, 3, 1920, device=DEV))
     with pytest.raises(IndexError):
         model.decode(torch.full((1, 8, 2), 2048, dtype=torch.int64, device=DEV))
+
+
+def test_checkpoint_round_trip_runs_on_gpu(full, golden, tmp_path):
+    """save_pretrained -> from_pretrained(device=cuda) of the full model gives
+    the reference's codes and audio for the 1 s clip."""
+    model, _ = full
+    model.save_pretrained(tmp_path)
+    loaded = MimiModel.from_pretrained(tmp_path, device=DEV)
+    audio, mask = synthetic.batch(1, 24_000)
+    out = loaded(torch.from_numpy(audio).to(DEV), torch.from_numpy(mask).to(DEV), num_quantizers=8)
+    assert torch.equal(out.audio_codes.cpu(), torch.from_numpy(golden["full_1s_codes"]).long())
+    assert_audio(out.audio_values.cpu(), torch.from_numpy(golden["full_1s_values"]))
+    loaded.release_graphs()

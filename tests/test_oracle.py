@@ -95,6 +95,49 @@ def test_benchmark_c1_matches_reference(full_oracle, golden):
     assert digest == str(golden["full_c1_values_sha256"])
 
 
+def _sha(values: torch.Tensor) -> str:
+    return hashlib.sha256(values.numpy().astype(np.float32).tobytes()).hexdigest()
+
+
+def test_benchmark_c2_matches_reference(full_oracle, golden):
+    audio, mask, nq = synthetic.config_inputs("c2")
+    codes, values = full_oracle.forward(torch.from_numpy(audio), torch.from_numpy(mask), nq)
+    assert torch.equal(codes, torch.from_numpy(golden["full_c2_codes"]).long())
+    assert torch.equal(values[..., ::10], torch.from_numpy(golden["full_c2_values_dec10"]))
+    assert _sha(values) == str(golden["full_c2_values_sha256"])
+    stats = golden["full_c2_values_stats"]
+    assert float(values.min()) == stats[0] and float(values.max()) == stats[1]
+
+
+def test_benchmark_c3_padded_batch_matches_reference(full_oracle, golden_large):
+    """Batch 16, last four clips zero-padded from 6 s (one reference call)."""
+    audio, mask, nq = synthetic.config_inputs("c3")
+    codes, values = full_oracle.forward(torch.from_numpy(audio), torch.from_numpy(mask), nq)
+    assert torch.equal(codes, torch.from_numpy(golden_large["c3_codes"]).long())
+    assert [_sha(values[c]) for c in range(16)] == golden_large["c3_values_sha256"].tolist()
+    for c in (0, 12, 15):
+        assert torch.equal(values[c:c + 1, :, ::10], torch.from_numpy(golden_large[f"c3_clip{c}_values_dec10"]))
+
+
+def test_benchmark_c4_long_clip_matches_reference(full_oracle, golden_large):
+    """100 s clip: 2,500 transformer frames through the 250-frame window."""
+    audio, mask, nq = synthetic.config_inputs("c4")
+    codes, values = full_oracle.forward(torch.from_numpy(audio), torch.from_numpy(mask), nq)
+    assert torch.equal(codes, torch.from_numpy(golden_large["c4_codes"]).long())
+    assert torch.equal(values[..., ::100], torch.from_numpy(golden_large["c4_values_dec100"]))
+    assert _sha(values) == str(golden_large["c4_values_sha256"])
+
+
+@pytest.mark.parametrize("clip", [0, 63])
+def test_benchmark_c5_32_codebooks_matches_reference(full_oracle, golden_large, clip):
+    audio, mask, nq = synthetic.config_inputs("c5")
+    a, m = torch.from_numpy(audio[clip:clip + 1]), torch.from_numpy(mask[clip:clip + 1])
+    codes, values = full_oracle.forward(a, m, nq)
+    assert codes.shape == (1, 32, 125)
+    assert torch.equal(codes, torch.from_numpy(golden_large[f"c5_clip{clip}_codes"]).long())
+    assert _sha(values) == str(golden_large[f"c5_clip{clip}_values_sha256"])
+
+
 def test_encoded_length_closed_form(full_oracle, golden):
     assert full_oracle.encoded_length(golden["encoded_length_in"]) == golden["encoded_length_out"].tolist()
     # Reference tests/test_config.py:45-48.
