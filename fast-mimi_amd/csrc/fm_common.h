@@ -5,6 +5,7 @@
 #include <stdint.h>
 #include <climits>
 #include <algorithm>
+#include <mutex>
 
 #define FM_DEVICE __device__ __forceinline__
 
@@ -17,6 +18,7 @@ enum FmStatus {
   FM_BAD_ARGUMENT = 1000,
   FM_WORKSPACE_TOO_SMALL = 1001,
   FM_UNSUPPORTED = 1002,
+  FM_SCRATCH_LIMIT = 1003,  // input larger than an allocation-free entry point's fixed scratch
 };
 
 // Epilogue / loader flags of the implicit-GEMM kernel.

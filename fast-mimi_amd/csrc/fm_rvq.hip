@@ -830,3 +830,71 @@ int fm_rvq_decode(const int64_t* codes, int batch, int num_codebooks, int frames
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free split encode.  The step partials and residual ping-pong
+// buffers live in a fixed device array instead of a caller workspace, so the
+// entry point makes no allocation of any kind (for hipGraph capture, serving
+// loops and harnesses that forbid hipMalloc).  Each GPU the library runs on
+// holds its own copy of the array until the process ends.  Every call on a
+// GPU shares that GPU's array: calls that overlap on one GPU (two streams, two
+// threads) race and must be serialised by the caller.  Nothing in the array
+// needs clearing between calls: every step writes all the partials and
+// residual rows the next step reads before it reads them.
+
+namespace {
+constexpr size_t kNoAllocScratchBytes = size_t(48) << 20;  // 8,190 rows of 256-dim codebooks
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of ``scratch`` on the current device (looked up once per
+// device; the host-side name is only a stand-in for it).
+int scratch_on_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return FM_UNSUPPORTED;
+  std::lock_guard<std::mutex> guard(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!ptr) return FM_UNSUPPORTED;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return FM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t fm_rvq_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+int fm_rvq_encode_split_noalloc(const float* x, int ld_x, int rows, int rows_per_batch, int dim,
+                                int entries, int n_semantic, int n_acoustic, const float* embeds,
+                                const float* embeds_t, const float* norms, int64_t* codes,
+                                int batch_stride, hipStream_t stream) {
+  if (!rvq_args_ok(x, ld_x, rows, rows_per_batch, dim, entries, embeds, embeds_t, norms, codes) ||
+      n_semantic < 0 || n_acoustic < 0 || n_semantic + n_acoustic <= 0 || ld_x < 2 * dim)
+    return FM_BAD_ARGUMENT;
+  if (rows == 0) return FM_OK;
+  if (fm_rvq_split_workspace_bytes(rows, dim, entries) > kNoAllocScratchBytes)
+    return FM_SCRATCH_LIMIT;
+  void* ptr = nullptr;
+  const int e = scratch_on_current_device(&ptr);
+  if (e != FM_OK) return e;
+  return fm_rvq_encode_split(x, ld_x, rows, rows_per_batch, dim, entries, n_semantic, n_acoustic,
+                             embeds, embeds_t, norms, codes, batch_stride, ptr,
+                             kNoAllocScratchBytes, stream);
+}
+
+}  // extern "C"

@@ -26,7 +26,8 @@ EPI_GELU = 8
 EPI_RES_ADD = 16
 EPI_RES_SCALE = 32
 
-_STATUS = {1000: "bad argument", 1001: "workspace too small", 1002: "unsupported shape"}
+_STATUS = {1000: "bad argument", 1001: "workspace too small", 1002: "unsupported shape",
+           1003: "input larger than the fixed scratch of an allocation-free entry point"}
 
 
 class NativeLibraryError(RuntimeError):
@@ -62,6 +63,8 @@ _SIGNATURES = {
     "fm_rvq_encode": ([_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _S, _P], _I),
     "fm_rvq_split_workspace_bytes": ([_I, _I, _I], _S),
     "fm_rvq_encode_split": ([_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _S, _P], _I),
+    "fm_rvq_noalloc_scratch_bytes": ([], _S),
+    "fm_rvq_encode_split_noalloc": ([_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P], _I),
     "fm_rvq_decode": ([_P, _I, _I, _I, _I, _P, _I, _I, _P, _P], _I),
     "fm_upsample_depthwise": ([_P, _I, _I, _I, _P, _I, _I, _P, _P], _I),
     "fm_resblock_supported": ([_I], _I),

@@ -11,7 +11,8 @@
  *   - Work is enqueued on `stream`; nothing synchronizes.  Calls sharing a
  *     `workspace` must be ordered on one stream.
  *   - Return value: 0 on success, 1000 bad argument, 1001 workspace too small,
- *     1002 unsupported shape, otherwise the hipError_t of the launch.
+ *     1002 unsupported shape, 1003 input larger than the fixed scratch of an
+ *     allocation-free entry point, otherwise the hipError_t of the launch.
  *   - Packed weights ("W^T layout") are [N][K] row-major with K contiguous:
  *       Conv1d weight [C_out][C_in][k]     -> [C_out][k * C_in], k-major:
  *                                             element (co, tap*C_in + ci) = w[co][ci][tap]
@@ -278,6 +279,23 @@ int fm_rvq_encode_split(const float* x, int ld_x, int rows, int rows_per_batch, 
                         int n_semantic, int n_acoustic, const float* embeds, const float* embeds_t,
                         const float* norms, int64_t* codes, int batch_stride, void* workspace,
                         size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * fm_rvq_encode_split without a workspace argument: it allocates nothing.
+ * No counterpart in the reference; it is for callers that cannot allocate
+ * (code under hipGraph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The step partials and residuals live in a fixed device array of
+ * fm_rvq_noalloc_scratch_bytes() bytes (48 MiB: up to 8,190 rows of 256-dim
+ * codebooks) that each GPU holds until the process ends.  Larger inputs
+ * return 1003 (scratch limit).  All calls on one GPU share its array: calls
+ * that overlap on one GPU race, so the caller serialises them.  Same
+ * arguments, codes and rounding as fm_rvq_encode_split otherwise.
+ */
+size_t fm_rvq_noalloc_scratch_bytes(void);
+int fm_rvq_encode_split_noalloc(const float* x, int ld_x, int rows, int rows_per_batch, int dim,
+                                int entries, int n_semantic, int n_acoustic, const float* embeds,
+                                const float* embeds_t, const float* norms, int64_t* codes,
+                                int batch_stride, hipStream_t stream);
 
 /*
  * Split-RVQ decode gather-sum: out[(b*frames + t)][0:dim] = 0 + E_0[c_0]
