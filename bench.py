@@ -7,6 +7,10 @@ timed region.  ``value`` is audio-seconds per second; ``ms_per_step`` the mean
 and ``median_ms`` the median round-trip latency.  The batch-16 configuration
 (configs[2]: 10 s clips, last 4 zero-padded from 6 s) is reported beside it.
 
+``parity`` compares each configuration's codes from the timed model with
+the reference's (committed fixtures under ``tests/golden``) and reports the
+float64 top-2 distance margins along the GPU's code chain.
+
 ``roofline`` describes the dominant kernel: its algorithmic FLOPs per launch
 over its mean launch time, timed with HIP events on the stream it runs on.
 ``cpu_baseline`` times the repository's CPU oracle (the reference's portable
@@ -43,6 +47,7 @@ sys.path.insert(0, str(REPO / "fast-mimi_amd"))
 
 from fast_mimi_amd import MimiConfig, MimiModel, synthetic  # noqa: E402
 from fast_mimi_amd import _native as nat  # noqa: E402
+from fast_mimi_amd.diagnostics import code_margins  # noqa: E402
 from fast_mimi_amd.flops import layer_table, roundtrip_flops  # noqa: E402
 
 PEAK_FP32_TFLOPS = 157.3  # MI355X dense FP32 (matrix) peak
@@ -159,6 +164,32 @@ def cpu_baseline(audio: np.ndarray, mask: np.ndarray, nq: int, runs: int) -> dic
                       f"after 2 warm-ups ({total_s:.1f} s of timed CPU work), {cores} threads"}
 
 
+GOLDEN = REPO / "tests" / "golden"
+
+
+def reference_codes(name: str) -> dict[int, np.ndarray]:
+    """The reference's codes for a configuration, per clip index (committed fixtures)."""
+    if name == "c2":
+        return {0: np.load(GOLDEN / "reference_golden.npz")["full_c2_codes"][0]}
+    large = np.load(GOLDEN / "reference_golden_large.npz")
+    if name == "c3":
+        return dict(enumerate(large["c3_codes"]))
+    if name == "c4":
+        return {0: large["c4_codes"][0]}
+    return {c: large[f"c5_clip{c}_codes"][0] for c in (0, 63)}
+
+
+def parity(model, name: str, audio: torch.Tensor, codes: torch.Tensor) -> dict:
+    """Codes of the timed run against the reference's, plus float64 near-tie margins."""
+    got = codes.cpu().numpy()
+    ref = reference_codes(name)
+    differing = {c: int((got[c] != want.astype(np.int64)).sum()) for c, want in ref.items()}
+    out = {"clips_checked": len(ref), "codes_differing_from_reference": sum(differing.values()),
+           "codes_checked": int(sum(w.size for w in ref.values()))}
+    out.update(code_margins(model, audio, codes))
+    return out
+
+
 def cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -201,6 +232,7 @@ def main() -> None:
     audio, mask, nq = synthetic.config_inputs("c2")
     a, m = torch.from_numpy(audio).to(dev), torch.from_numpy(mask).to(dev)
     times = time_steps(lambda: model(a, m, num_quantizers=nq), args.steps, args.warmup)
+    checks = {"c2": parity(model, "c2", a, model(a, m, num_quantizers=nq).audio_codes)}
     mean_ms = statistics.fmean(times)
     med_ms = statistics.median(times)
     seconds = audio.shape[0] * audio.shape[-1] / 24_000
@@ -237,6 +269,7 @@ def main() -> None:
         a16, m16, nq16 = synthetic.config_inputs("c3")
         a16d, m16d = torch.from_numpy(a16).to(dev), torch.from_numpy(m16).to(dev)
         t16 = time_steps(lambda: model(a16d, m16d, num_quantizers=nq16), max(5, args.steps // 5), 2)
+        checks["c3"] = parity(model, "c3", a16d, model(a16d, m16d, num_quantizers=nq16).audio_codes)
         med16 = statistics.median(t16)
         f16 = roundtrip_flops(cfg, 16, a16.shape[-1], nq16)
         result["batch16"] = {"audio_sec_per_sec": round(16 * 10 / (med16 / 1e3), 2),
@@ -247,6 +280,7 @@ def main() -> None:
             ax, mx, nqx = synthetic.config_inputs(cfg_name)
             axd, mxd = torch.from_numpy(ax).to(dev), torch.from_numpy(mx).to(dev)
             tx = time_steps(lambda: model(axd, mxd, num_quantizers=nqx), steps, 2)
+            checks[cfg_name] = parity(model, cfg_name, axd, model(axd, mxd, num_quantizers=nqx).audio_codes)
             medx = statistics.median(tx)
             fx = roundtrip_flops(cfg, ax.shape[0], ax.shape[-1], nqx)
             result[key] = {"batch": int(ax.shape[0]), "samples": int(ax.shape[-1]),
@@ -255,6 +289,7 @@ def main() -> None:
                            "pipeline_tflops": round(fx / (medx * 1e-3) / 1e12, 3)}
             del axd, mxd
         model.release_graphs()
+    result["parity"] = checks
     result["roofline"] = dominant_kernel(model, DOMINANT, 1, audio.shape[-1], nq, 50)
     tr = recorded_traffic()
     if tr is not None:

@@ -29,6 +29,7 @@ import threading
 import torch
 
 from . import _native as nat
+from . import ops
 from .config import MimiConfig
 from .weights import decoder_layer_indices, encoder_layer_indices
 
@@ -40,10 +41,6 @@ _WORKSPACE_BYTES = 64 << 20
 _ROW_LINEAR_MAX_ROWS = 1024
 # Up to this many rows the 16-row kernels on fragment-packed weights are used.
 _ROW16_MAX_ROWS = 512
-
-
-def _ptr(t: torch.Tensor | None) -> int | None:
-    return None if t is None else t.data_ptr()
 
 
 class _Conv:
@@ -165,12 +162,11 @@ class MimiRuntime:
         self.embeds = torch.empty((len(prefixes), e, d), device=device)
         self.embeds_t = torch.empty((len(prefixes), d, e), device=device)
         self.norms = torch.empty((len(prefixes), e), device=device)
-        stream = torch.cuda.current_stream(device).cuda_stream
         for j, p in enumerate(prefixes):
-            nat.call("fm_rvq_prepare_codebook", st[f"{p}.embed_sum"].contiguous().data_ptr(),
-                     st[f"{p}.cluster_usage"].contiguous().data_ptr(), e, d, 1e-5,
-                     self.embeds[j].data_ptr(), self.embeds_t[j].data_ptr(),
-                     self.norms[j].data_ptr(), stream)
+            ops.call("fm_rvq_prepare_codebook", st[f"{p}.embed_sum"].contiguous(),
+                     st[f"{p}.cluster_usage"].contiguous(), e, d, 1e-5,
+                     self.embeds[j], self.embeds_t[j],
+                     self.norms[j])
         # Fragment-packed copies of the projection weights for the few-row kernels,
         # keyed by the row-major weight's device address.
         self._packed: dict[int, torch.Tensor] = {}
@@ -180,7 +176,7 @@ class MimiRuntime:
             n, k = w.shape
             if lib.fm_row_linear_supported(k, n):
                 pw = torch.empty_like(w)
-                nat.call("fm_pack_row_weights", w.data_ptr(), n, k, pw.data_ptr(), stream)
+                ops.call("fm_pack_row_weights", w, n, k, pw)
                 self._packed[w.data_ptr()] = pw
         self.workspace = torch.empty(_WORKSPACE_BYTES // 4, device=device)
         self._rope: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
@@ -190,17 +186,16 @@ class MimiRuntime:
         torch.cuda.synchronize(device)
 
     # ------------------------------------------------------------------ ops
-    def _stream(self) -> int:
-        return torch.cuda.current_stream(self.device).cuda_stream
-
     def _call(self, name: str, *args) -> None:
+        """Run C-ABI entry point ``name`` through its ``torch.ops.fast_mimi_amd``
+        operator on the current stream (tensors in place of device pointers)."""
         if self.profile is None:
-            nat.call(name, *args)
+            ops.call(name, *args)
             return
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
         start.record()
-        nat.call(name, *args)
+        ops.call(name, *args)
         stop.record()
         self.profile.append((f"{self._tag}:{name}", start, stop))
 
@@ -215,24 +210,23 @@ class MimiRuntime:
         rows = -(-L // layer.stride)
         y_len = rows if y_len is None else y_len
         y = torch.empty((B, y_len, layer.c_out), device=self.device)
-        self._call("fm_conv1d", x.data_ptr(), B, L, layer.c_in, layer.w.data_ptr(), _ptr(layer.b),
-                 layer.c_out, layer.k, layer.stride, layer.replicate, flags, _ptr(residual),
-                 y.data_ptr(), y_len, self.workspace.data_ptr(), _WORKSPACE_BYTES, self._stream())
+        self._call("fm_conv1d", x, B, L, layer.c_in, layer.w, layer.b,
+                 layer.c_out, layer.k, layer.stride, layer.replicate, flags, residual,
+                 y, y_len, self.workspace, _WORKSPACE_BYTES)
         return y, rows
 
     def _convt(self, x, B, L, layer: _ConvT):
         y = torch.empty((B, L * layer.stride, layer.c_out), device=self.device)
-        self._call("fm_conv_transpose1d", x.data_ptr(), B, L, layer.c_in, layer.w.data_ptr(),
-                 _ptr(layer.b), layer.c_out, layer.k, layer.stride, 0, None, y.data_ptr(),
-                 self.workspace.data_ptr(), _WORKSPACE_BYTES, self._stream())
+        self._call("fm_conv_transpose1d", x, B, L, layer.c_in, layer.w,
+                 layer.b, layer.c_out, layer.k, layer.stride, 0, None, y,
+                 self.workspace, _WORKSPACE_BYTES)
         return y, L * layer.stride
 
     def _linear(self, x, rows, w, flags=0, residual=None, scale=None, out=None):
         n, k = w.shape
         y = torch.empty((rows, n), device=self.device) if out is None else out
-        self._call("fm_linear", x.data_ptr(), rows, k, w.data_ptr(), n, flags, _ptr(residual),
-                 _ptr(scale), y.data_ptr(), self.workspace.data_ptr(), _WORKSPACE_BYTES,
-                 self._stream())
+        self._call("fm_linear", x, rows, k, w, n, flags, residual,
+                 scale, y, self.workspace, _WORKSPACE_BYTES)
         return y
 
     def _proj(self, x, rows, w, flags=0, residual=None, scale=None, out=None):
@@ -247,13 +241,13 @@ class MimiRuntime:
         """Transformer projection with LayerNorm prologue / RoPE epilogue fused."""
         n, k = w.shape
         y = torch.empty((rows, n), device=self.device) if out is None else out
-        g, b = (ln[0].data_ptr(), ln[1].data_ptr()) if ln is not None else (None, None)
+        g, b = (ln[0], ln[1]) if ln is not None else (None, None)
         cos, sin, rope_cols, per_seq = rope if rope is not None else (None, None, 0, 1)
         packed = self._packed.get(w.data_ptr()) if rows <= _ROW16_MAX_ROWS else None
         name, wp = ("fm_row_linear_packed", packed) if packed is not None else ("fm_row_linear", w)
-        self._call(name, x.data_ptr(), rows, k, g, b, self.config.norm_eps,
-                   wp.data_ptr(), n, flags, _ptr(residual), _ptr(scale), _ptr(cos), _ptr(sin),
-                   rope_cols, per_seq, y.data_ptr(), self._stream())
+        self._call(name, x, rows, k, g, b, self.config.norm_eps,
+                   wp, n, flags, residual, scale, cos, sin,
+                   rope_cols, per_seq, y)
         return y
 
     def _fuse_last(self, block) -> bool:
@@ -272,9 +266,8 @@ class MimiRuntime:
         if fused:
             self._tag = tag
             y = torch.empty_like(x)
-            self._call("fm_resblock", x.data_ptr(), B, L, c2.c_out, c1.w.data_ptr(), c1.b.data_ptr(),
-                       c2.w.data_ptr(), c2.b.data_ptr(), 1 if elu_after else 0, y.data_ptr(),
-                       self._stream())
+            self._call("fm_resblock", x, B, L, c2.c_out, c1.w, c1.b,
+                       c2.w, c2.b, 1 if elu_after else 0, y)
             return y
         self._tag = f"{tag}.c1"
         h, _ = self._conv(x, B, L, c1, nat.ELU_IN | nat.EPI_ELU)
@@ -306,7 +299,6 @@ class MimiRuntime:
         h = h.reshape(M, C)
         xln = torch.empty((M, C), device=self.device)
         att = torch.empty((M, nh * hd), device=self.device)
-        s = self._stream()
         lib = nat.library()
         fused = (M <= _ROW_LINEAR_MAX_ROWS and hd == 64 and lib.fm_row_linear_supported(C, layers[0].wqkv.shape[0])
                  and lib.fm_row_linear_supported(C, layers[0].w1.shape[0])
@@ -318,16 +310,16 @@ class MimiRuntime:
                 qkv = self._row_linear(h, M, lay.wqkv, ln=lay.ln1, rope=(cos, sin, rope_cols, T))
             else:
                 self._tag = f"{tag}{li}.ln1"
-                self._call("fm_layer_norm", h.data_ptr(), lay.ln1[0].data_ptr(),
-                           lay.ln1[1].data_ptr(), M, C, cfg.norm_eps, xln.data_ptr(), s)
+                self._call("fm_layer_norm", h, lay.ln1[0],
+                           lay.ln1[1], M, C, cfg.norm_eps, xln)
                 self._tag = f"{tag}{li}.qkv"
                 qkv = self._linear(xln, M, lay.wqkv)
             ld = qkv.shape[1]
             self._tag = f"{tag}{li}.attn"
-            tabs = (None, None) if fused else (cos.data_ptr(), sin.data_ptr())
-            self._call("fm_window_attention", qkv.data_ptr(), ld, 0, nh * hd, (nh + nkv) * hd,
+            tabs = (None, None) if fused else (cos, sin)
+            self._call("fm_window_attention", qkv, ld, 0, nh * hd, (nh + nkv) * hd,
                        tabs[0], tabs[1], B, T, nh, nkv, hd, cfg.sliding_window,
-                       1.0 / (hd ** 0.5), att.data_ptr(), nh * hd, s)
+                       1.0 / (hd ** 0.5), att, nh * hd)
             self._tag = f"{tag}{li}.o"
             if fused:
                 self._row_linear(att, M, lay.wo, nat.EPI_RES_SCALE, residual=h, scale=lay.ls1, out=h)
@@ -336,8 +328,8 @@ class MimiRuntime:
             else:
                 self._linear(att, M, lay.wo, nat.EPI_RES_SCALE, residual=h, scale=lay.ls1, out=h)
                 self._tag = f"{tag}{li}.ln2"
-                self._call("fm_layer_norm", h.data_ptr(), lay.ln2[0].data_ptr(),
-                           lay.ln2[1].data_ptr(), M, C, cfg.norm_eps, xln.data_ptr(), s)
+                self._call("fm_layer_norm", h, lay.ln2[0],
+                           lay.ln2[1], M, C, cfg.norm_eps, xln)
                 self._tag = f"{tag}{li}.fc1"
                 ff = self._linear(xln, M, lay.w1, nat.EPI_GELU)
             self._tag = f"{tag}{li}.fc2"
@@ -352,6 +344,11 @@ class MimiRuntime:
         With ``padding_cache`` the convolutions run on cached left context with
         no right padding (streaming); with ``kv_cache`` the transformer
         continues from cached keys/values (``model.py:2964-3005``)."""
+        h, B, L = self.embeddings(audio, padding_cache, kv_cache)
+        return self.quantize(h, B, L, num_quantizers)
+
+    def embeddings(self, audio: torch.Tensor, padding_cache=None, kv_cache=None):
+        """Encoder output entering the quantizer: ``(h [B, T12.5, C], B, T12.5)``."""
         B, C, S = audio.shape
         x = audio if C == 1 else audio.transpose(1, 2).contiguous()
         if padding_cache is None:
@@ -368,7 +365,12 @@ class MimiRuntime:
                 h, L = self._conv(h, B, L, self.down)
             else:
                 h, L = self._stream_conv(h, self.down, padding_cache, len(padding_cache.padding_cache) - 1)
-        return self.quantize(h, B, L, num_quantizers)
+        return h, B, L
+
+    def quantizer_inputs(self, h, B, T) -> torch.Tensor:
+        """Both branches' projected RVQ inputs ``[B*T, 2*dim]`` (semantic | acoustic)."""
+        self._tag = "rvq.in"
+        return self._proj(h.reshape(B * T, self.config.hidden_size), B * T, self.w_in)
 
     def _encoder_seanet(self, x, B, S):
         n = len(self.enc_stages)
@@ -378,9 +380,9 @@ class MimiRuntime:
             # The first conv is formed inside the first residual block.
             self._tag = "enc.first+res64"
             h = torch.empty((B, S, 64), device=self.device)
-            self._call("fm_conv_resblock64", x.data_ptr(), B, S, first.w.data_ptr(),
-                       first.b.data_ptr(), c1.w.data_ptr(), c1.b.data_ptr(), c2.w.data_ptr(),
-                       c2.b.data_ptr(), 1, h.data_ptr(), self._stream())
+            self._call("fm_conv_resblock64", x, B, S, first.w,
+                       first.b, c1.w, c1.b, c2.w,
+                       c2.b, 1, h)
             L, start = S, 1
         else:
             self._tag = "enc.first"
@@ -419,9 +421,9 @@ class MimiRuntime:
             raise RuntimeError(f"streaming chunk too short: {total} rows for a kernel of {layer.k}")
         rows = (total - layer.k) // layer.stride + 1
         y = torch.empty((B, rows, layer.c_out), device=self.device)
-        self._call("fm_conv1d_valid", buf.data_ptr(), B, total, layer.c_in, layer.w.data_ptr(),
-                   _ptr(layer.b), layer.c_out, layer.k, layer.stride, flags, _ptr(residual),
-                   y.data_ptr(), self.workspace.data_ptr(), _WORKSPACE_BYTES, self._stream())
+        self._call("fm_conv1d_valid", buf, B, total, layer.c_in, layer.w,
+                   layer.b, layer.c_out, layer.k, layer.stride, flags, residual,
+                   y, self.workspace, _WORKSPACE_BYTES)
         return y, rows
 
     def _encoder_seanet_stream(self, x, B, cache):
@@ -460,17 +462,16 @@ class MimiRuntime:
         h = h.reshape(M, C)
         att = torch.empty((M, nh * hd), device=self.device)
         qd, kd = nh * hd, nkv * hd
-        s = self._stream()
         xln = None if fused else torch.empty((M, C), device=self.device)
         for li, lay in enumerate(layers):
             if fused:
                 qkv = self._row_linear(h, M, lay.wqkv, ln=lay.ln1, rope=(cos, sin, qd + kd, T))
             else:
-                self._call("fm_layer_norm", h.data_ptr(), lay.ln1[0].data_ptr(), lay.ln1[1].data_ptr(),
-                           M, C, cfg.norm_eps, xln.data_ptr(), s)
+                self._call("fm_layer_norm", h, lay.ln1[0], lay.ln1[1],
+                           M, C, cfg.norm_eps, xln)
                 qkv = self._linear(xln, M, lay.wqkv)
-                self._call("fm_apply_rope", qkv.data_ptr(), M, qkv.shape[1], qd + kd, hd,
-                           cos.data_ptr(), sin.data_ptr(), T, s)
+                self._call("fm_apply_rope", qkv, M, qkv.shape[1], qd + kd, hd,
+                           cos, sin, T)
             ld = qkv.shape[1]
             q3 = qkv.view(B, T, ld)
             keys, values = kv.update(q3[:, :, qd:qd + kd], q3[:, :, qd + kd:], li)
@@ -479,16 +480,16 @@ class MimiRuntime:
             comb[:, :, qd:qd + kd] = keys
             comb[:, :, qd + kd:] = values
             comb[:, n:, :qd] = q3[:, :, :qd]
-            self._call("fm_window_attention_rows", comb.data_ptr(), ld, 0, qd, qd + kd, None, None,
+            self._call("fm_window_attention_rows", comb, ld, 0, qd, qd + kd, None, None,
                        B, n + T, n, nh, nkv, hd, cfg.sliding_window, 1.0 / (hd ** 0.5),
-                       att.data_ptr(), qd, s)
+                       att, qd)
             if fused:
                 self._row_linear(att, M, lay.wo, nat.EPI_RES_SCALE, residual=h, scale=lay.ls1, out=h)
                 ff = self._row_linear(h, M, lay.w1, nat.EPI_GELU, ln=lay.ln2)
             else:
                 self._linear(att, M, lay.wo, nat.EPI_RES_SCALE, residual=h, scale=lay.ls1, out=h)
-                self._call("fm_layer_norm", h.data_ptr(), lay.ln2[0].data_ptr(), lay.ln2[1].data_ptr(),
-                           M, C, cfg.norm_eps, xln.data_ptr(), s)
+                self._call("fm_layer_norm", h, lay.ln2[0], lay.ln2[1],
+                           M, C, cfg.norm_eps, xln)
                 ff = self._linear(xln, M, lay.w1, nat.EPI_GELU)
             self._proj(ff, M, lay.w2, nat.EPI_RES_SCALE, residual=h, scale=lay.ls2, out=h)
         return h.reshape(B, T, C)
@@ -497,18 +498,16 @@ class MimiRuntime:
         cfg = self.config
         M = B * T
         vq = self.vq
-        self._tag = "rvq.in"
-        proj = self._proj(h.reshape(M, cfg.hidden_size), M, self.w_in)
+        proj = self.quantizer_inputs(h, B, T)
         self._tag = "rvq.encode"
         codes = torch.empty((B, nq, T), dtype=torch.int64, device=self.device)
         ws_bytes = nat.library().fm_rvq_split_workspace_bytes(M, vq, cfg.codebook_size)
         n_sem = min(cfg.num_semantic_quantizers, nq)
         # Both chains in shared launches (step s of each branch in one grid).
         ws = torch.empty((ws_bytes + 3) // 4, device=self.device)
-        self._call("fm_rvq_encode_split", proj.data_ptr(), 2 * vq, M, T, vq, cfg.codebook_size,
-                   n_sem, nq - n_sem, self.embeds.data_ptr(), self.embeds_t.data_ptr(),
-                   self.norms.data_ptr(), codes.data_ptr(), nq * T, ws.data_ptr(), ws_bytes,
-                   self._stream())
+        self._call("fm_rvq_encode_split", proj, 2 * vq, M, T, vq, cfg.codebook_size,
+                   n_sem, nq - n_sem, self.embeds, self.embeds_t,
+                   self.norms, codes, nq * T, ws, ws_bytes)
         return codes
 
     def decode(self, codes: torch.Tensor, out_length: int | None = None, kv_cache=None) -> torch.Tensor:
@@ -521,16 +520,16 @@ class MimiRuntime:
         vq = self.vq
         q = torch.empty((M, 2 * vq), device=self.device)
         self._tag = "rvq.decode"
-        self._call("fm_rvq_decode", codes.data_ptr(), B, nq, T, cfg.num_semantic_quantizers,
-                 self.embeds.data_ptr(), cfg.codebook_size, vq, q.data_ptr(), self._stream())
+        self._call("fm_rvq_decode", codes, B, nq, T, cfg.num_semantic_quantizers,
+                 self.embeds, cfg.codebook_size, vq, q)
         self._tag = "rvq.out"
         h = self._proj(q, M, self.w_out).reshape(B, T, cfg.hidden_size)
         self._tag = "up"
         L = T
         if self.bottleneck:
             up = torch.empty((B, L * 2, cfg.hidden_size), device=self.device)
-            self._call("fm_upsample_depthwise", h.data_ptr(), B, L, cfg.hidden_size,
-                     self.up_w.data_ptr(), self.up_k, 2, up.data_ptr(), self._stream())
+            self._call("fm_upsample_depthwise", h, B, L, cfg.hidden_size,
+                     self.up_w, self.up_k, 2, up)
             h, L = up, 2 * L
         if kv_cache is None:
             h = self.transformer(h, B, L, self.dec_tf, "dec.tf")
@@ -552,9 +551,9 @@ class MimiRuntime:
                 d = torch.empty((lib.fm_resblock64_conv_workspace_bytes(B, L) + 3) // 4, device=self.device)
                 y = torch.empty((B, out_length), device=self.device)
                 last = self.dec_last
-                self._call("fm_resblock64_conv", h.data_ptr(), B, L, c1.w.data_ptr(), c1.b.data_ptr(),
-                           c2.w.data_ptr(), c2.b.data_ptr(), 1, last.w.data_ptr(), _ptr(last.b),
-                           out_length, y.data_ptr(), d.data_ptr(), d.numel() * 4, self._stream())
+                self._call("fm_resblock64_conv", h, B, L, c1.w, c1.b,
+                           c2.w, c2.b, 1, last.w, last.b,
+                           out_length, y, d, d.numel() * 4)
                 return y.view(B, 1, out_length)
             h = self._resblock(h, B, L, block, elu_after=True, tag=f"dec.res{convt.c_out}")
         full = L

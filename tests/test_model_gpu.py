@@ -377,3 +377,72 @@ def test_checkpoint_round_trip_runs_on_gpu(full, golden, tmp_path):
     assert torch.equal(out.audio_codes.cpu(), torch.from_numpy(golden["full_1s_codes"]).long())
     assert_audio(out.audio_values.cpu(), torch.from_numpy(golden["full_1s_values"]))
     loaded.release_graphs()
+
+
+def test_runtime_calls_go_through_torch_ops(full):
+    """Every kernel of an eager round trip is dispatched as a
+    torch.ops.fast_mimi_amd operator (no other device compute op runs)."""
+    from torch.utils._python_dispatch import TorchDispatchMode
+
+    model, _ = full
+    eager = MimiModel(model.config, device=DEV, use_graphs=False)
+    eager.load_state_dict(model.state_dict())
+    eager.runtime()
+    seen = []
+
+    class Record(TorchDispatchMode):
+        def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+            out = func(*args, **(kwargs or {}))
+            tensors = [t for t in torch.utils._pytree.tree_leaves((args, kwargs, out))
+                       if isinstance(t, torch.Tensor)]
+            if any(t.is_cuda for t in tensors):  # host-side table set-up is not device compute
+                seen.append(func.name())
+            return out
+
+    audio, _ = synthetic.batch(1, 24_000, base_seed=2)
+    a = torch.from_numpy(audio).to(DEV)
+    with Record():
+        eager(a, num_quantizers=8)
+    ours = [n for n in seen if n.startswith("fast_mimi_amd::")]
+    assert {"fast_mimi_amd::conv_resblock64", "fast_mimi_amd::row_linear_packed",
+            "fast_mimi_amd::window_attention", "fast_mimi_amd::rvq_encode_split",
+            "fast_mimi_amd::rvq_decode", "fast_mimi_amd::resblock64_conv"} <= set(ours)
+    compute = [n for n in seen if not n.startswith("fast_mimi_amd::") and n.split("::")[1].split(".")[0]
+               not in ("empty", "empty_like", "view", "reshape", "_reshape_alias", "transpose", "t",
+                       "contiguous", "clone", "copy_", "slice", "select", "detach", "alias",
+                       "_to_copy", "to", "new_empty", "as_strided", "expand", "unsqueeze",
+                       "squeeze", "zeros", "zero_", "fill_", "lift_fresh", "unbind")]
+    assert not compute, sorted(set(compute))
+
+
+def test_torch_ops_round_trip_in_captured_graph(full):
+    """The runtime's operator calls recorded under torch.cuda.graph replay to
+    the eager result, with other eager work and syncs between replays."""
+    model, _ = full
+    rt = model.runtime()
+    audio, _ = synthetic.batch(1, 24_000, base_seed=4)
+    a = torch.from_numpy(audio).to(DEV)
+
+    def roundtrip(x):
+        codes = rt.encode(x, 8)
+        return codes, rt.decode(codes, x.shape[-1])
+
+    with torch.inference_mode():
+        rt.prepare(model._frames_25(a.shape[-1]))
+        want_codes, want_audio = roundtrip(a)
+        static = a.clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            roundtrip(static)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            g_codes, g_audio = roundtrip(static)
+        other, _ = synthetic.batch(1, 24_000, base_seed=8)
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(g_codes, want_codes) and torch.equal(g_audio, want_audio)
+            roundtrip(torch.from_numpy(other).to(DEV))  # eager work between replays
+            torch.cuda.synchronize()

@@ -51,3 +51,44 @@ def test_status_codes_map_to_errors():
     with pytest.raises(nat.NativeError, match="hipError_t 700"):
         nat.check(700, "fm_x")
     nat.check(0, "fm_x")
+
+
+def test_torch_ops_mirror_the_header():
+    """Every stream-taking entry point is a torch.ops.fast_mimi_amd operator
+    whose schema follows the C signature (stream dropped; const pointers
+    read-only, other pointers mutated)."""
+    import torch
+
+    from fast_mimi_amd import ops
+
+    text = HEADER.read_text()
+    for ret, name, args in re.findall(r"^\s*(int|size_t)\s+(fm_\w+)\s*\(([^)]*)\)", text, re.M):
+        params = [a.strip() for a in args.replace("\n", " ").split(",") if a.strip() not in ("", "void")]
+        if not params or not params[-1].startswith("hipStream_t"):
+            continue
+        schema = getattr(torch.ops.fast_mimi_amd, name[3:]).default._schema
+        assert len(schema.arguments) == len(params) - 1, name
+        for arg, param in zip(schema.arguments, params[:-1]):
+            cname = re.split(r"[\s*]+", param)[-1]
+            assert arg.name == cname, (name, arg.name, cname)
+            if "*" in param:
+                assert str(arg.type) == "Optional[Tensor]", (name, cname)
+                mutable = arg.alias_info is not None and arg.alias_info.is_write
+                assert mutable == (not param.startswith("const")), (name, cname)
+        assert name in ops.SPECS
+
+
+def test_torch_ops_trace_as_opaque_mutating_calls():
+    """The fake implementations let FX trace the operators without a GPU."""
+    import torch
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    from fast_mimi_amd import ops  # noqa: F401  (registers the operators)
+
+    def decode(codes, embeds, out):
+        torch.ops.fast_mimi_amd.rvq_decode(codes, 1, 8, 125, 1, embeds, 2048, 256, out)
+        return out
+
+    gm = make_fx(decode, tracing_mode="fake")(torch.zeros(1, 8, 125, dtype=torch.int64),
+                                              torch.zeros(8, 2048, 256), torch.zeros(125, 512))
+    assert "fast_mimi_amd.rvq_decode" in gm.code
