@@ -80,14 +80,22 @@ def dominant_kernel(model: MimiModel, name: str, batch: int, samples: int, nq: i
     for _ in range(3):
         op()
     torch.cuda.synchronize()
+    # The launches are captured in one hipGraph and replayed, so the events
+    # bracket back-to-back kernels on the capture stream, not host launch gaps.
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(iters):
+            op()
+    graph.replay()
+    torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     start.record()
-    for _ in range(iters):
-        op()
+    graph.replay()
     stop.record()
     stop.synchronize()
     ms = start.elapsed_time(stop) / iters
+    del graph
     achieved = flops / (ms * 1e-3) / 1e12
     return {"bound": "mfma", "kernel": f"gemm_kernel ({name}: {row[1]} rows={row[3]} K={row[4]} N={row[5]})",
             "flops_per_launch": flops, "avg_launch_ms": ms, "achieved": round(achieved, 3),

@@ -1270,8 +1270,10 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
                         : *reinterpret_cast<const floatx4*>(xs + 64 * piece + 4 * t);
   };
 
-  // The input rows are the critical path (LayerNorm, then the A operand):
-  // their loads go out first, the weight fragments right after.
+  // The input rows are the critical path (LayerNorm, then the A operand).
+  // With staging, the weight fragments are issued once the rows are in LDS:
+  // issued earlier they queue ahead of the LayerNorm parameters and the
+  // other waves' rows (measured 0.2-0.6 us faster per launch at 250 rows).
   if (!STAGE) load_b(0, 0);
   if (STAGE) {
     // 32 lanes per row, float4 chunks p, p + 32, ...
@@ -1282,7 +1284,6 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
     floatx4 v[CH];
 #pragma unroll
     for (int u = 0; u < CH; ++u) v[u] = *reinterpret_cast<const floatx4*>(xr + 4 * (p + TPR * u));
-    load_b(0, 0);
     if (gamma) {
       floatx4 gv[CH], bv[CH];
 #pragma unroll
@@ -1317,6 +1318,7 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
     for (int u = 0; u < CH; ++u)
       *reinterpret_cast<floatx4*>(As + r * PA + 4 * (p + TPR * u)) =
           valid ? v[u] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    load_b(0, 0);
     __syncthreads();
   }
   load_a(0, 0);
