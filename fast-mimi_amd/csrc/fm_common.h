@@ -28,7 +28,8 @@ enum FmGemmFlags {
   FM_EPI_ELU = 4,       // ELU on the output
   FM_EPI_GELU = 8,      // exact-erf GELU on the output
   FM_EPI_RES_ADD = 16,  // y = res + (acc + bias)
-  FM_EPI_RES_SCALE = 32 // y = res + scale[n] * acc
+  FM_EPI_RES_SCALE = 32, // y = res + scale[n] * acc
+  FM_WEIGHTS_X6 = 64     // weight_packed is followed by its three bf16 planes (fm_split_weights)
 };
 
 // e^x - 1 for x <= 0, branch-free.  Near zero (x > -1/4) x * q(x), q a

@@ -1033,6 +1033,239 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int spli
 }
 
 // ---------------------------------------------------------------------------
+// FP32 contraction on the bf16 matrix cores ("bf16x6").  Every FP32 operand
+// is the sum of three round-to-nearest bf16 pieces, v = v0 + v1 + v2, exact to
+// within 2^-24 |v| (each piece holds the next 8 significant bits of what the
+// previous ones left).  A product a*b is then the six cross terms whose
+// pieces' orders sum to at most 2 (a2b0 + a1b1 + a0b2 + a1b0 + a0b1 + a0b0,
+// smallest first); the three dropped terms are below 2^-24 |a b|.  Each
+// bf16 x bf16 product is exact in FP32 and the MFMA accumulates in FP32, so
+// the result carries FP32 rounding error (measured against float64 on the
+// SEANet shapes: rms 2-3e-7 of the output scale, as the FP32 MFMA path) while
+// v_mfma_f32_32x32x16_bf16 delivers 16x the FP32 MFMA rate: six of them cost
+// 0.375 of the FP32 instruction time per k.
+// Weights are split once (fm_split_weights) into planes [3][N][K] stored
+// right after the FP32 W^T; A tiles are split as they are staged: each
+// thread loads one float4 of the 128 x 16 k-tile, splits it and writes the
+// three 8-byte pieces, so each A element is split once per block.  B planes
+// travel global -> LDS directly (global_load_lds_dwordx4).  LDS rows are 32
+// bytes (16 k of bf16) and a wave's fragment read is 1 KB contiguous
+// (row l % 32, k half l / 32), so neither the 8-byte writes nor the 16-byte
+// reads conflict.  Two stages of 24 KB, one barrier per 16-deep k-tile; the
+// epilogue is the direct-load kernel's.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+FM_DEVICE floatx16 fm_mfma32_bf16(bf16x8 a, bf16x8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// v = h0 + h1 + h2 (+ a residual below 2^-24 |v|), each a round-to-nearest bf16.
+FM_DEVICE void split3(floatx4 v, bf16x4& h0, bf16x4& h1, bf16x4& h2) {
+  h0 = __builtin_convertvector(v, bf16x4);
+  const floatx4 r1 = v - __builtin_convertvector(h0, floatx4);
+  h1 = __builtin_convertvector(r1, bf16x4);
+  const floatx4 r2 = r1 - __builtin_convertvector(h1, floatx4);
+  h2 = __builtin_convertvector(r2, bf16x4);
+}
+
+// W^T [N][K] fp32 -> three bf16 planes [3][N][K].
+__global__ __launch_bounds__(256) void split_weights_kernel(const float* __restrict__ w, long n4, bf16x4* __restrict__ out) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  bf16x4 h0, h1, h2;
+  split3(*reinterpret_cast<const floatx4*>(w + 4 * i), h0, h1, h2);
+  out[i] = h0;
+  out[n4 + i] = h1;
+  out[2 * n4 + i] = h2;
+}
+
+template <int BM, int BN, int WN>
+__global__ __launch_bounds__(512) void gemm_x6_kernel(GemmArgs p, const __bf16* __restrict__ w3) {
+  constexpr int NTH = 512, WM = 8 / WN, BK = 16;
+  constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
+  static_assert(FM >= 1 && FN >= 1 && BM * 4 == NTH && BN % 32 == 0, "tiling");
+  constexpr int PLANE_A = BM * BK * 2, PLANE_B = BN * BK * 2;  // bytes
+  constexpr int STAGE_B = 3 * (PLANE_A + PLANE_B);
+  constexpr int HM = BM / 2, PC = BN + 4, TILE_B = HM * PC * 4;
+  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE_B > TILE_B ? 2 * STAGE_B : TILE_B];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave / WN;
+  const int wm0 = wr * WTM, wn0 = (wave % WN) * WTN;
+  const long M = (long)p.batch * p.rows;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int tile = tile_index();
+  const long m0 = (long)(tile / tiles_n) * BM;
+  const int n0 = (tile % tiles_n) * BN;
+  const int k_begin = blockIdx.y * p.k_split;
+  const int k_end = min(p.K, k_begin + p.k_split);
+
+  // A: thread -> (row tid / 4, 4-wide k chunk tid % 4) of each k-tile.
+  const int ar = tid >> 2, ac = tid & 3;
+  const float* a_row;
+  int a_p0;
+  {
+    const long mm = m0 + ar;
+    const int m = (int)min(mm, M - 1);
+    const int b = (int)fm_div((unsigned)m, p.rows_div);
+    const int t = m - b * p.rows;
+    a_p0 = mm < M ? t * p.rs - p.padL : INT_MIN / 2;
+    a_row = p.x + (long)b * p.L_in * p.C_in + (long)a_p0 * p.C_in + 4 * ac;
+  }
+  // B: waves 0 .. BN/32 - 1 move 32 rows x 3 planes each, direct to LDS.
+  const bool b_loader = wave < BN / 32;
+  const int brow = wave * 32 + (lane >> 1);
+  const long KN = (long)p.K * p.N;
+  const __bf16* b_src = (n0 + brow < p.N) ? w3 + (long)(n0 + brow) * p.K + 8 * (lane & 1) : nullptr;
+
+  auto issue_b = [&](int stage, int k0) {
+    if (!b_loader) return;
+    char* Bs = smem + stage * STAGE_B + 3 * PLANE_A;
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) {
+      const void* src = b_src ? (const void*)(b_src + pl * KN + k0) : (const void*)g_zero16;
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(Bs + pl * PLANE_B + wave * 32 * BK * 2),
+                                       16, 0, 0);
+    }
+  };
+  floatx4 areg;
+  auto load_a = [&](int k0) {
+    const int tap = k0 / p.C_in;
+    const bool ok = (unsigned)(a_p0 + tap) < (unsigned)p.L_in;
+    areg = *reinterpret_cast<const floatx4*>(ok ? a_row + k0 : g_zero16);
+  };
+  auto store_a = [&](int stage) {
+    bf16x4 h0, h1, h2;
+    split3(areg, h0, h1, h2);
+    char* As = smem + stage * STAGE_B + ar * (BK * 2) + ac * 8;
+    *reinterpret_cast<bf16x4*>(As) = h0;
+    *reinterpret_cast<bf16x4*>(As + PLANE_A) = h1;
+    *reinterpret_cast<bf16x4*>(As + 2 * PLANE_A) = h2;
+  };
+
+  floatx16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int lrow = lane & 31, lk = lane >> 5;
+  const int nkt = (k_end - k_begin) / BK;
+  if (nkt > 0) {
+    issue_b(0, k_begin);
+    load_a(k_begin);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    store_a(0);
+  }
+  for (int kt = 0; kt < nkt; ++kt) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const bool more = kt + 1 < nkt;
+    if (more) {
+      issue_b((kt + 1) & 1, k_begin + (kt + 1) * BK);
+      load_a(k_begin + (kt + 1) * BK);
+    }
+    const char* As = smem + (kt & 1) * STAGE_B;
+    const char* Bs = As + 3 * PLANE_A;
+    bf16x8 a[3][FM], b[3][FN];
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        a[pl][i] = *reinterpret_cast<const bf16x8*>(As + pl * PLANE_A + (wm0 + 32 * i + lrow) * (BK * 2) + lk * 16);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        b[pl][j] = *reinterpret_cast<const bf16x8*>(Bs + pl * PLANE_B + (wn0 + 32 * j + lrow) * (BK * 2) + lk * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        acc[i][j] = fm_mfma32_bf16(a[2][i], b[0][j], acc[i][j]);
+        acc[i][j] = fm_mfma32_bf16(a[1][i], b[1][j], acc[i][j]);
+        acc[i][j] = fm_mfma32_bf16(a[0][i], b[2][j], acc[i][j]);
+        acc[i][j] = fm_mfma32_bf16(a[1][i], b[0][j], acc[i][j]);
+        acc[i][j] = fm_mfma32_bf16(a[0][i], b[1][j], acc[i][j]);
+        acc[i][j] = fm_mfma32_bf16(a[0][i], b[0][j], acc[i][j]);
+      }
+    if (more) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      store_a((kt + 1) & 1);
+    }
+  }
+  lds_barrier();
+
+  // Epilogue: as the direct-load kernel (two halves of BM / 2 rows through LDS).
+  float* fsm = reinterpret_cast<float*>(smem);
+  const int h = lane >> 5, lcol = lane & 31;
+  const bool crop = p.y_rows != p.rows;
+  const bool has_res = p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE);
+  float* part = p.partial ? p.partial + (long)blockIdx.y * M * p.N : nullptr;
+  constexpr int CG = BN / 4, RSTEP = NTH / CG, NRUN = HM / RSTEP, RB = NRUN < 2 ? NRUN : 2;
+  const int c = (tid % CG) * 4, r0 = tid / CG;
+  const int n = n0 + c;
+  const bool n_ok = n < p.N;
+  const int ncl = n_ok ? n : 0;
+  const floatx4 bias = (p.bias && !part) ? *reinterpret_cast<const floatx4*>(p.bias + ncl % p.bias_len)
+                                         : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  const floatx4 scale = ((p.flags & FM_EPI_RES_SCALE) && !part)
+                            ? *reinterpret_cast<const floatx4*>(p.scale + ncl)
+                            : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    if (wr * WTM / HM == hf) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            fsm[(wm0 - hf * HM + i * 32 + fm_mfma32_row(r, lane)) * PC + wn0 + j * 32 + lcol] = acc[i][j][r];
+    }
+    lds_barrier();
+    const long mh = m0 + hf * HM;
+#pragma unroll
+    for (int u0 = 0; u0 < NRUN; u0 += RB) {
+      floatx4 v[RB], res[RB];
+#pragma unroll
+      for (int u = 0; u < RB; ++u) {
+        const int r = r0 + (u0 + u) * RSTEP;
+        const long m = min(mh + r, M - 1);
+        v[u] = *reinterpret_cast<const floatx4*>(fsm + r * PC + c);
+        res[u] = (has_res && !part) ? *reinterpret_cast<const floatx4*>(p.res + m * p.N + ncl)
+                                    : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (int u = 0; u < RB; ++u) {
+        const long m = mh + r0 + (u0 + u) * RSTEP;
+        if (m >= M || !n_ok) continue;
+        if (part) {
+          *reinterpret_cast<floatx4*>(part + m * p.N + n) = v[u];
+          continue;
+        }
+        floatx4 o = v[u];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = epilogue_v(o[e], bias[e], res[u][e], scale[e], p.flags);
+        long dst = m * p.N + n;
+        if (crop) {
+          const int b = (int)(m / p.rows);
+          const int t = (int)(m - (long)b * p.rows);
+          if (t >= p.y_rows) continue;
+          dst = ((long)b * p.y_rows + t) * p.N + n;
+        }
+        *reinterpret_cast<floatx4*>(p.y + dst) = o;
+      }
+    }
+    if (hf == 0) lds_barrier();
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Single-input-channel causal conv (the waveform -> num_filters first layer):
 // y[b, t, c] = bias[c] + sum_j w[c, j] * x[b, t - pad + j].  HBM-bound on the
 // output; a block stages its 256 positions plus the causal halo in LDS and
@@ -1161,6 +1394,7 @@ constexpr TileCfg kBig64 = {64, 128, 1, 32, 11, 0};    // double-buffered, 32x32
 // Direct-load forms of the three double-buffered tiles (taken when the
 // operands allow, see gemm_dl_kernel).
 constexpr TileCfg kDl128 = {128, 128, 1, 32, 13, 0};
+constexpr TileCfg kX6 = {128, 128, 1, 32, 16, 0};  // bf16x6 tile (k-tile 16; splits stay 32-aligned)
 constexpr TileCfg kDl192 = {192, 128, 1, 32, 14, 0};
 // 64x128 runs one block per CU: 64-deep k-tiles (96 KB ring) halve its barriers.
 constexpr TileCfg kDl64 = {64, 128, 1, 64, 15, 0};
@@ -1296,6 +1530,11 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     if (cfg.id == 9) cfg = kDl128;
     if (cfg.id == 10) cfg = kDl192;
     if (cfg.id == 11 && p.C_in % 64 == 0 && p.K % 64 == 0) cfg = kDl64;
+    // With split weights the direct-load tiles become the bf16x6 tile.
+    if ((p.flags & FM_WEIGHTS_X6) && (cfg.id == 13 || cfg.id == 14 || cfg.id == 15)) {
+      cfg = kX6;
+      tiles = tile_count(M, p.N, cfg);
+    }
   }
   if (splits > 1) {
     const size_t per = (size_t)M * p.N * sizeof(float);
@@ -1328,6 +1567,10 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     case 13: hipLaunchKernelGGL((gemm_dl_kernel<128, 128, 4, 32, 2, 4>), grid, dim3(512), 0, s, p); break;
     case 14: hipLaunchKernelGGL((gemm_dl_kernel<192, 128, 4, 32, 2, 4>), grid, dim3(512), 0, s, p); break;
     case 15: hipLaunchKernelGGL((gemm_dl_kernel<64, 128, 4, 64, 2, 4>), grid, dim3(512), 0, s, p); break;
+    case 16:
+      hipLaunchKernelGGL((gemm_x6_kernel<128, 128, 4>), grid, dim3(512), 0, s, p,
+                         reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
+      break;
     case 7: hipLaunchKernelGGL((gemm_mid_kernel<64, 64, 1>), grid, dim3(NTHREADS), 0, s, p); break;
     case 8: hipLaunchKernelGGL((gemm_mid_kernel<32, 32, 4>), grid, dim3(NTHREADS), 0, s, p); break;
     default: hipLaunchKernelGGL(gemm_generic_kernel, grid, dim3(256), 0, s, p); break;
@@ -1361,7 +1604,7 @@ int fm_conv1d(const float* x, int batch, int length, int in_channels, const floa
   p.y_rows = y_length; p.bias_len = out_channels;
   p.flags = (flags & ~FM_REPLICATE) | (pad_mode == 1 ? FM_REPLICATE : 0);
   if (p.flags & FM_EPI_RES_SCALE) return FM_BAD_ARGUMENT;
-  const int plain = p.flags & ~(FM_EPI_ELU | FM_ELU_IN);
+  const int plain = p.flags & ~(FM_EPI_ELU | FM_ELU_IN | FM_WEIGHTS_X6);
   if (x && weight_packed && y && batch > 0 && length > 0 && stride == 1 && plain == 0 &&
       y_length >= 0 && y_length <= length) {
     // The packed layout W^T[c_out][(tap, c_in)] doubles as [C][k] / [k*C] here.
@@ -1398,6 +1641,17 @@ int fm_conv1d_valid(const float* x, int batch, int length, int in_channels,
   p.rs = stride; p.padL = 0; p.K = kernel * in_channels; p.N = out_channels;
   p.y_rows = p.rows; p.bias_len = out_channels; p.flags = flags;
   return run_gemm(p, workspace, workspace_bytes, stream);
+}
+
+// Appends the bf16x6 planes of a packed weight: planes [3][count] bf16
+// (count = N * K, a multiple of 4).  Callers store them right after the
+// FP32 weight and pass FM_WEIGHTS_X6 in flags.
+int fm_split_weights(const float* weight_packed, long count, void* planes, hipStream_t stream) {
+  if (!weight_packed || !planes || count <= 0 || count % 4) return FM_BAD_ARGUMENT;
+  const long n4 = count / 4;
+  hipLaunchKernelGGL(split_weights_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream,
+                     weight_packed, n4, reinterpret_cast<bf16x4*>(planes));
+  return (int)hipGetLastError();
 }
 
 int fm_conv_transpose1d(const float* x, int batch, int length, int in_channels,

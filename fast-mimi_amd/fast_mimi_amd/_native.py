@@ -25,6 +25,7 @@ EPI_ELU = 4
 EPI_GELU = 8
 EPI_RES_ADD = 16
 EPI_RES_SCALE = 32
+WEIGHTS_X6 = 64
 
 _STATUS = {1000: "bad argument", 1001: "workspace too small", 1002: "unsupported shape",
            1003: "input larger than the fixed scratch of an allocation-free entry point"}
@@ -46,6 +47,7 @@ _S = ctypes.c_size_t
 
 _SIGNATURES = {
     "fm_abi_version": ([], _I),
+    "fm_split_weights": ([_P, _L, _P, _P], _I),
     "fm_conv1d": ([_P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _S, _P], _I),
     "fm_conv1d_valid": ([_P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _S, _P], _I),
     "fm_conv_transpose1d": ([_P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _S, _P], _I),

@@ -53,6 +53,7 @@ class _Conv:
         self.replicate = 1 if pad_mode == "replicate" else 0
         self.w = weight.permute(0, 2, 1).reshape(c_out, k * c_in).contiguous()
         self.b = None if bias is None else bias.contiguous()
+        self.flags = 0  # nat.WEIGHTS_X6 once the runtime appends the bf16 planes
 
 
 class _ConvT:
@@ -71,6 +72,7 @@ class _ConvT:
         w = weight.reshape(c_in, c_out, taps, stride).flip(2)  # [ci, co, jj, r]
         self.w = w.permute(3, 1, 2, 0).reshape(stride * c_out, taps * c_in).contiguous()
         self.b = None if bias is None else bias.contiguous()
+        self.flags = 0
 
 
 class _Layer:
@@ -178,12 +180,42 @@ class MimiRuntime:
                 pw = torch.empty_like(w)
                 ops.call("fm_pack_row_weights", w, n, k, pw)
                 self._packed[w.data_ptr()] = pw
+        # Convolution and large-row projection weights carry their bf16x6
+        # planes: W^T followed by [3][N][K] bf16 in one buffer.
+        self._x6: dict[int, torch.Tensor] = {}
+        for layer in self._conv_layers():
+            layer.w = self._with_planes(layer.w)
+            layer.flags = nat.WEIGHTS_X6
+        for w in [m for lay in self.enc_tf + self.dec_tf for m in (lay.wqkv, lay.wo, lay.w1, lay.w2)]:
+            self._x6[w.data_ptr()] = self._with_planes(w)
         self.workspace = torch.empty(_WORKSPACE_BYTES // 4, device=device)
         self._rope: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
         # Optional per-op timing: a list of (tag, start_event, end_event).
         self.profile: list | None = None
         self._tag = ""
         torch.cuda.synchronize(device)
+
+    def _conv_layers(self):
+        layers = [self.enc_first, self.enc_last, self.dec_first, self.dec_last]
+        for (c1, c2), down in self.enc_stages:
+            layers += [c1, c2, down]
+        for convt, (c1, c2) in self.dec_stages:
+            layers += [convt, c1, c2]
+        if self.bottleneck:
+            layers.append(self.down)
+        return layers
+
+    def _with_planes(self, w: torch.Tensor) -> torch.Tensor:
+        """``w`` [N, K] (FP32 W^T) as the first N*K floats of a buffer that
+        continues with its three bf16 planes (``fm_split_weights``)."""
+        n = w.numel()
+        if n % 4:
+            return w
+        buf = torch.empty(n + (3 * n * 2 + 3) // 4, device=self.device)
+        buf[:n].copy_(w.reshape(-1))
+        nat.call("fm_split_weights", buf.data_ptr(), n, buf.data_ptr() + 4 * n,
+                 torch.cuda.current_stream(self.device).cuda_stream)
+        return buf[:n].view(w.shape)
 
     # ------------------------------------------------------------------ ops
     def _call(self, name: str, *args) -> None:
@@ -211,20 +243,23 @@ class MimiRuntime:
         y_len = rows if y_len is None else y_len
         y = torch.empty((B, y_len, layer.c_out), device=self.device)
         self._call("fm_conv1d", x, B, L, layer.c_in, layer.w, layer.b,
-                 layer.c_out, layer.k, layer.stride, layer.replicate, flags, residual,
+                 layer.c_out, layer.k, layer.stride, layer.replicate, flags | layer.flags, residual,
                  y, y_len, self.workspace, _WORKSPACE_BYTES)
         return y, rows
 
     def _convt(self, x, B, L, layer: _ConvT):
         y = torch.empty((B, L * layer.stride, layer.c_out), device=self.device)
         self._call("fm_conv_transpose1d", x, B, L, layer.c_in, layer.w,
-                 layer.b, layer.c_out, layer.k, layer.stride, 0, None, y,
+                 layer.b, layer.c_out, layer.k, layer.stride, layer.flags, None, y,
                  self.workspace, _WORKSPACE_BYTES)
         return y, L * layer.stride
 
     def _linear(self, x, rows, w, flags=0, residual=None, scale=None, out=None):
         n, k = w.shape
         y = torch.empty((rows, n), device=self.device) if out is None else out
+        wx = self._x6.get(w.data_ptr())
+        if wx is not None:
+            w, flags = wx, flags | nat.WEIGHTS_X6
         self._call("fm_linear", x, rows, k, w, n, flags, residual,
                  scale, y, self.workspace, _WORKSPACE_BYTES)
         return y
@@ -422,7 +457,7 @@ class MimiRuntime:
         rows = (total - layer.k) // layer.stride + 1
         y = torch.empty((B, rows, layer.c_out), device=self.device)
         self._call("fm_conv1d_valid", buf, B, total, layer.c_in, layer.w,
-                   layer.b, layer.c_out, layer.k, layer.stride, flags, residual,
+                   layer.b, layer.c_out, layer.k, layer.stride, flags | layer.flags, residual,
                    y, self.workspace, _WORKSPACE_BYTES)
         return y, rows
 

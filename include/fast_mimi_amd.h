@@ -44,11 +44,26 @@ enum {
   FM_EPI_ELU = 4,       /* ELU on the output                                   */
   FM_EPI_GELU = 8,      /* exact-erf GELU on the output                        */
   FM_EPI_RES_ADD = 16,  /* y = residual + (acc + bias)                         */
-  FM_EPI_RES_SCALE = 32 /* y = residual + scale[n] * acc   (fm_linear only)    */
+  FM_EPI_RES_SCALE = 32, /* y = residual + scale[n] * acc   (fm_linear only)    */
+  FM_WEIGHTS_X6 = 64     /* weight is followed by its bf16 planes (fm_split_weights) */
 };
 
 /* ABI version of the library (bumped when a contract changes). */
 int fm_abi_version(void);
+
+/*
+ * bf16x6 weights: writes the three round-to-nearest bf16 pieces of each of
+ * the `count` floats of a packed weight (count = N * K, a multiple of 4) as
+ * planes [3][count] into `planes`.  A caller that stores the planes directly
+ * after the FP32 weight (one buffer of count * 4 + count * 6 bytes) and adds
+ * FM_WEIGHTS_X6 (64) to `flags` of fm_conv1d / fm_conv1d_valid /
+ * fm_conv_transpose1d / fm_linear lets the large direct-load tiles run the
+ * FP32 contraction as six bf16 MFMA products per operand pair (FP32-accurate,
+ * see csrc/fm_gemm.hip); every other kernel reads the FP32 part only.
+ * No reference counterpart: it prepares the operands of the convolutions the
+ * entry points below replace.
+ */
+int fm_split_weights(const float* weight_packed, long count, void* planes, hipStream_t stream);
 
 /*
  * Causal Conv1d, dilation 1: left zero (pad_mode 0) or edge (pad_mode 1)

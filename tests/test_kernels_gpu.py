@@ -44,9 +44,39 @@ def close(got, want, rel=2e-5):
     assert err <= rel * scale, f"max err {err:.3e} vs scale {scale:.3e}"
 
 
-def run_conv(x_ncl, w, b, stride, pad_mode, flags, ws, residual_ncl=None, y_len=None):
+def with_planes(w):
+    """A packed weight followed by its bf16x6 planes (fm_split_weights), as
+    the runtime stores it; returns the FP32 view at the buffer's start."""
+    n = w.numel()
+    buf = torch.empty(n + (6 * n + 3) // 4, device=DEV)
+    buf[:n].copy_(w.reshape(-1))
+    nat.call("fm_split_weights", buf.data_ptr(), n, buf.data_ptr() + 4 * n, stream())
+    torch.cuda.synchronize()
+    return buf[:n].view(w.shape)
+
+
+def test_split_weights_pieces_sum_to_the_weight():
+    """Each float is three round-to-nearest bf16 pieces whose sum is within
+    2^-24 of it, each piece at most half an ulp of the previous remainder."""
+    g = torch.Generator().manual_seed(3)
+    w = (torch.randn(4096, generator=g) * torch.logspace(-6, 3, 4096)).to(DEV)
+    buf = with_planes(w.view(64, 64))
+    planes = buf.reshape(-1).untyped_storage()
+    n = w.numel()
+    raw = torch.empty(0, dtype=torch.bfloat16, device=DEV).set_(planes, n * 2, (3, n))
+    h = raw.float().cpu().double()
+    wd = w.cpu().double()
+    assert torch.equal(raw[0].cpu(), w.cpu().to(torch.bfloat16))
+    assert torch.all((wd - h.sum(0)).abs() <= wd.abs() * 2.0 ** -24)
+    with pytest.raises(nat.NativeError, match="bad argument"):
+        nat.call("fm_split_weights", buf.data_ptr(), 6, buf.data_ptr(), stream())
+
+
+def run_conv(x_ncl, w, b, stride, pad_mode, flags, ws, residual_ncl=None, y_len=None, x6=False):
     B, C, L = x_ncl.shape
     layer = _Conv(w.to(DEV), None if b is None else b.to(DEV), stride, pad_mode)
+    if x6:
+        layer.w, flags = with_planes(layer.w), flags | nat.WEIGHTS_X6
     x = x_ncl.transpose(1, 2).contiguous().to(DEV)
     rows = -(-L // stride)
     y_len = rows if y_len is None else y_len
@@ -118,7 +148,8 @@ DL_CASES = [
 
 @pytest.mark.parametrize("B,cin,cout,k,stride,L,y_len", DL_CASES)
 @pytest.mark.parametrize("epi", ["plain", "res_elu"])
-def test_conv1d_direct_load_tiles(B, cin, cout, k, stride, L, y_len, epi, ws):
+@pytest.mark.parametrize("x6", [False, True], ids=["fp32", "bf16x6"])
+def test_conv1d_direct_load_tiles(B, cin, cout, k, stride, L, y_len, epi, x6, ws):
     g = torch.Generator().manual_seed(B * 31 + cin + cout + k + L)
     x = torch.randn(B, cin, L, generator=g)
     w = torch.randn(cout, cin, k, generator=g) / math.sqrt(cin * k)
@@ -126,11 +157,11 @@ def test_conv1d_direct_load_tiles(B, cin, cout, k, stride, L, y_len, epi, ws):
     rows = -(-L // stride)
     want = causal_conv1d(x.double(), w.double(), b.double(), stride)
     if epi == "plain":
-        got = run_conv(x, w, b, stride, "constant", 0, ws, y_len=y_len)
+        got = run_conv(x, w, b, stride, "constant", 0, ws, y_len=y_len, x6=x6)
     else:
         res = torch.randn(B, cout, rows, generator=g)
         got = run_conv(x, w, b, stride, "constant", nat.EPI_RES_ADD | nat.EPI_ELU, ws,
-                       residual_ncl=res, y_len=y_len)
+                       residual_ncl=res, y_len=y_len, x6=x6)
         want = F.elu(res.double() + want)
     want = want[..., :y_len] if y_len is not None else want
     assert got.shape == want.shape
@@ -319,16 +350,20 @@ def test_conv1d_crop(ws):
     (1, 1024, 512, 8, 250), (2, 512, 256, 6, 40), (1, 256, 128, 5, 300),
     (1, 128, 64, 4, 1000), (1, 4, 2, 2, 7), (2, 8, 4, 2, 1), (1, 128, 64, 4, 40000),
     (1, 128, 64, 4, 60000)])
-def test_conv_transpose1d(B, cin, cout, stride, L, ws):
+@pytest.mark.parametrize("x6", [False, True], ids=["fp32", "bf16x6"])
+def test_conv_transpose1d(B, cin, cout, stride, L, x6, ws):
     g = torch.Generator().manual_seed(cin + L)
     x = torch.randn(B, cin, L, generator=g)
     w = torch.randn(cin, cout, 2 * stride, generator=g) / math.sqrt(cin)
     b = torch.randn(cout, generator=g) * 0.1
     layer = _ConvT(w.to(DEV), b.to(DEV), stride)
+    flags = 0
+    if x6:
+        layer.w, flags = with_planes(layer.w), nat.WEIGHTS_X6
     xd = x.transpose(1, 2).contiguous().to(DEV)
     y = torch.empty((B, L * stride, cout), device=DEV)
     nat.call("fm_conv_transpose1d", xd.data_ptr(), B, L, cin, layer.w.data_ptr(), layer.b.data_ptr(),
-             cout, 2 * stride, stride, 0, None, y.data_ptr(), ws.data_ptr(), WS_BYTES, stream())
+             cout, 2 * stride, stride, flags, None, y.data_ptr(), ws.data_ptr(), WS_BYTES, stream())
     torch.cuda.synchronize()
     want = causal_conv_transpose1d(x.double(), w.double(), b.double(), stride)
     close(y.cpu().transpose(1, 2), want)
@@ -352,17 +387,23 @@ def run_linear(x, w, flags=0, res=None, scale=None, ws=None, out=None):
                                       (4000, 512, 1536), (4001, 512, 1536),  # 192x128 tiles
                                       (2500, 512, 512), (4001, 512, 512),    # 64x128 tiles
                                       (2500, 512, 2048)])
-def test_linear_epilogues(rows, k, n, ws):
+@pytest.mark.parametrize("x6", [False, True], ids=["fp32", "bf16x6"])
+def test_linear_epilogues(rows, k, n, x6, ws):
     g = torch.Generator().manual_seed(rows + k + n)
     x = torch.randn(rows, k, generator=g)
     w = torch.randn(n, k, generator=g) * 0.05
     xd, wd = x.to(DEV), w.to(DEV)
-    close(run_linear(xd, wd, ws=ws).cpu(), x.double() @ w.double().t())
-    close(run_linear(xd, wd, nat.EPI_GELU, ws=ws).cpu(), F.gelu(x.double() @ w.double().t()))
+    f = 0
+    if x6:
+        if (n * k) % 4:
+            pytest.skip("bf16x6 planes need N * K to be a multiple of 4")
+        wd, f = with_planes(wd), nat.WEIGHTS_X6
+    close(run_linear(xd, wd, f, ws=ws).cpu(), x.double() @ w.double().t())
+    close(run_linear(xd, wd, nat.EPI_GELU | f, ws=ws).cpu(), F.gelu(x.double() @ w.double().t()))
     res = torch.randn(rows, n, generator=g)
     scale = torch.rand(n, generator=g) * 0.1
     h = res.to(DEV)
-    run_linear(xd, wd, nat.EPI_RES_SCALE, res=h, scale=scale.to(DEV), ws=ws, out=h)  # in place
+    run_linear(xd, wd, nat.EPI_RES_SCALE | f, res=h, scale=scale.to(DEV), ws=ws, out=h)  # in place
     close(h.cpu(), res.double() + scale.double() * (x.double() @ w.double().t()))
 
 
