@@ -1144,11 +1144,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6_kernel(GemmArgs p, const
       areg[i] = *reinterpret_cast<const floatx4*>(ok ? a_row[i] + k0 : g_zero16);
     }
   };
+  const bool elu_in = p.flags & FM_ELU_IN;
   auto store_a = [&](int stage) {
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
       bf16x4 h0, h1, h2;
-      split3(areg[i], h0, h1, h2);
+      floatx4 v = areg[i];
+      if (elu_in) v = floatx4{fm_elu(v[0]), fm_elu(v[1]), fm_elu(v[2]), fm_elu(v[3])};
+      split3(v, h0, h1, h2);
       char* As = smem + stage * STAGE_B + a_off[i];
       *reinterpret_cast<bf16x4*>(As) = h0;
       *reinterpret_cast<bf16x4*>(As + PLANE_A) = h1;
@@ -1559,10 +1562,17 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     if (cfg.id == 10) cfg = kDl192;
     if (cfg.id == 11 && p.C_in % 64 == 0 && p.K % 64 == 0) cfg = kDl64;
     // With split weights the direct-load tiles become the bf16x6 tile.
-    if ((p.flags & FM_WEIGHTS_X6) && (cfg.id == 13 || cfg.id == 14 || cfg.id == 15)) {
-      cfg = tile_count(M, p.N, kX6Big) >= 384 ? kX6Big : kX6;
-      tiles = tile_count(M, p.N, cfg);
-    }
+  }
+  // With split weights the large tiles become bf16x6 tiles (which also take
+  // ELU on load: the A operand passes through registers) when that still
+  // gives most CUs a tile; the few-hundred-tile shapes keep the FP32 tile
+  // picked for them (measured: the 512-column projections at 2500-4000 rows,
+  // 64x128 FP32 tiles on all CUs against 80-128 bf16x6 tiles).
+  const bool x6_ok = (p.flags & FM_WEIGHTS_X6) && big_ok && !(p.flags & FM_REPLICATE) &&
+                     p.C_in % 16 == 0 && p.K % 16 == 0;
+  if (x6_ok && cfg.id >= 9 && cfg.id <= 15 && cfg.id != 12 && tile_count(M, p.N, kX6) >= 192) {
+    cfg = tile_count(M, p.N, kX6Big) >= 384 ? kX6Big : kX6;
+    tiles = tile_count(M, p.N, cfg);
   }
   if (splits > 1) {
     const size_t per = (size_t)M * p.N * sizeof(float);

@@ -169,6 +169,19 @@ def test_conv1d_direct_load_tiles(B, cin, cout, k, stride, L, y_len, epi, x6, ws
     close(got, want)
 
 
+@pytest.mark.parametrize("B,cin,cout,L", [(1, 512, 256, 2000), (16, 512, 256, 2000), (2, 256, 128, 9001)])
+def test_conv1d_bf16x6_elu_on_load(B, cin, cout, L, ws):
+    """bf16x6 tiles with ELU applied to the A operand as it is loaded (the
+    residual block's first conv, k = 3), ELU epilogue, vs float64."""
+    g = torch.Generator().manual_seed(B + cin + L)
+    x = torch.randn(B, cin, L, generator=g)
+    w = torch.randn(cout, cin, 3, generator=g) / math.sqrt(cin * 3)
+    b = torch.randn(cout, generator=g) * 0.1
+    got = run_conv(x, w, b, 1, "constant", nat.ELU_IN | nat.EPI_ELU, ws, x6=True)
+    want = F.elu(causal_conv1d(F.elu(x.double()), w.double(), b.double(), 1))
+    close(got, want)
+
+
 @pytest.mark.parametrize("B,L,y_len", [(1, 1, 1), (2, 2, 2), (1, 62, 62), (2, 63, 60), (3, 999, 999),
                                        (1, 240000, 240000), (2, 24001, 23995)])
 @pytest.mark.parametrize("elu_in", [0, 1])
