@@ -84,7 +84,9 @@ def dominant_kernel(model: MimiModel, name: str, batch: int, samples: int, nq: i
     # The launches are captured in one hipGraph and replayed, so the events
     # bracket back-to-back kernels on the capture stream, not host launch gaps.
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    # Captured in inference mode like the model's own graphs (they share the
+    # default generator's graph state, created as an inference tensor).
+    with torch.inference_mode(), torch.cuda.graph(graph):
         for _ in range(iters):
             op()
     graph.replay()
