@@ -1565,12 +1565,13 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
   }
   // With split weights the large tiles become bf16x6 tiles (which also take
   // ELU on load: the A operand passes through registers) when that still
-  // gives most CUs a tile; the few-hundred-tile shapes keep the FP32 tile
+  // gives most CUs a tile (K-split blocks included); the few-hundred-tile
+  // shapes keep the FP32 tile
   // picked for them (measured: the 512-column projections at 2500-4000 rows,
   // 64x128 FP32 tiles on all CUs against 80-128 bf16x6 tiles).
   const bool x6_ok = (p.flags & FM_WEIGHTS_X6) && big_ok && !(p.flags & FM_REPLICATE) &&
                      p.C_in % 16 == 0 && p.K % 16 == 0;
-  if (x6_ok && cfg.id >= 9 && cfg.id <= 15 && cfg.id != 12 && tile_count(M, p.N, kX6) >= 192) {
+  if (x6_ok && cfg.id >= 9 && cfg.id <= 15 && cfg.id != 12 && tile_count(M, p.N, kX6) * splits >= 192) {
     cfg = tile_count(M, p.N, kX6Big) >= 384 ? kX6Big : kX6;
     tiles = tile_count(M, p.N, cfg);
   }
