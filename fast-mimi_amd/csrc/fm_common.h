@@ -73,6 +73,25 @@ FM_DEVICE floatx16 fm_mfma32(float a, float b, floatx16 c) {
 
 FM_DEVICE int fm_mfma32_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
+// bf16x6 primitives: one v_mfma_f32_32x32x16_bf16 (lane l supplies row / column
+// l % 32, k = 8 (l / 32) .. +7, same result layout as fm_mfma32) and the
+// three-piece round-to-nearest bf16 split of an FP32 value.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+FM_DEVICE floatx16 fm_mfma32_bf16(bf16x8 a, bf16x8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// v = h0 + h1 + h2 (+ a residual below 2^-24 |v|), each a round-to-nearest bf16.
+FM_DEVICE void split3(floatx4 v, bf16x4& h0, bf16x4& h1, bf16x4& h2) {
+  h0 = __builtin_convertvector(v, bf16x4);
+  const floatx4 r1 = v - __builtin_convertvector(h0, floatx4);
+  h1 = __builtin_convertvector(r1, bf16x4);
+  const floatx4 r2 = r1 - __builtin_convertvector(h1, floatx4);
+  h2 = __builtin_convertvector(r2, bf16x4);
+}
+
 static inline int fm_ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
 
 // Division by a runtime constant d >= 1 for numerators n < 2^31:

@@ -1044,11 +1044,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int spli
 // SEANet shapes: rms 2-3e-7 of the output scale, as the FP32 MFMA path) while
 // v_mfma_f32_32x32x16_bf16 delivers 16x the FP32 MFMA rate: six of them cost
 // 0.375 of the FP32 instruction time per k.
-// Weights are split once (fm_split_weights) into planes [3][N][K] stored
-// right after the FP32 W^T; A tiles are split as they are staged: each
+// Weights are split once (fm_split_weights) into planes [3][K/16][N][16]
+// stored right after the FP32 W^T; A tiles are split as they are staged: each
 // thread loads one float4 of the 128 x 16 k-tile, splits it and writes the
 // three 8-byte pieces, so each A element is split once per block.  B planes
-// travel global -> LDS directly (global_load_lds_dwordx4).  LDS rows are 32
+// travel global -> LDS directly (global_load_lds_dwordx4; 32 rows of a k-tile
+// are one contiguous 1 KB run of the k16-tile ordered planes).  LDS rows are 32
 // bytes (16 k of bf16) and a wave's fragment read is 1 KB contiguous
 // (row l % 32, k half l / 32), so neither the 8-byte writes nor the 16-byte
 // reads conflict.  Two stages, one barrier per 16-deep k-tile; the epilogue
@@ -1057,31 +1058,22 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int spli
 // else 128 x 128 (waves of 64 x 32, 48 KB).  Measured against the FP32
 // direct-load tile on the SEANet shapes: 1.3-1.5x (dec.up4 at C2 55 vs 80 us,
 // at C3 0.81 vs 1.07 ms).
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-
-FM_DEVICE floatx16 fm_mfma32_bf16(bf16x8 a, bf16x8 b, floatx16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-// v = h0 + h1 + h2 (+ a residual below 2^-24 |v|), each a round-to-nearest bf16.
-FM_DEVICE void split3(floatx4 v, bf16x4& h0, bf16x4& h1, bf16x4& h2) {
-  h0 = __builtin_convertvector(v, bf16x4);
-  const floatx4 r1 = v - __builtin_convertvector(h0, floatx4);
-  h1 = __builtin_convertvector(r1, bf16x4);
-  const floatx4 r2 = r1 - __builtin_convertvector(h1, floatx4);
-  h2 = __builtin_convertvector(r2, bf16x4);
-}
-
-// W^T [N][K] fp32 -> three bf16 planes [3][N][K].
-__global__ __launch_bounds__(256) void split_weights_kernel(const float* __restrict__ w, long n4, bf16x4* __restrict__ out) {
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+// W^T [N][K] fp32 -> three bf16 planes in k16-tile order [3][K/16][N][16]:
+// the 16 k of one row are 32 contiguous bytes and the rows of a k-tile are
+// adjacent, so 32 rows of one k-tile are one 1 KB run.
+__global__ __launch_bounds__(256) void split_weights_kernel(const float* __restrict__ w, int N, int K,
+                                                            bf16x4* __restrict__ out) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;  // float4 index into W^T
+  const long n4 = (long)N * K / 4;
   if (i >= n4) return;
+  const long n = 4 * i / K;
+  const int k = (int)(4 * i - n * K);
   bf16x4 h0, h1, h2;
   split3(*reinterpret_cast<const floatx4*>(w + 4 * i), h0, h1, h2);
-  out[i] = h0;
-  out[n4 + i] = h1;
-  out[2 * n4 + i] = h2;
+  const long o = (((long)(k >> 4) * N + n) * 16 + (k & 15)) / 4;
+  out[o] = h0;
+  out[n4 + o] = h1;
+  out[2 * n4 + o] = h2;
 }
 
 template <int BM, int BN, int WM, int WN, int NST>
@@ -1128,7 +1120,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6_kernel(GemmArgs p, const
     for (int i = wave; i < NBI; i += NW) {
       const int pl = i / (BN / 32), rg = i % (BN / 32);
       const int row = rg * 32 + (lane >> 1);
-      const void* src = (n0 + row < p.N) ? (const void*)(w3 + pl * KN + (long)(n0 + row) * p.K + k0 + 8 * (lane & 1))
+      const void* src = (n0 + row < p.N) ? (const void*)(w3 + pl * KN + ((long)(k0 >> 4) * p.N + n0 + row) * 16 + 8 * (lane & 1))
                                          : (const void*)g_zero16;
       __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)src,
                                        (__attribute__((address_space(3))) void*)(Bs + pl * PLANE_B + rg * 32 * BK * 2),
@@ -1686,14 +1678,15 @@ int fm_conv1d_valid(const float* x, int batch, int length, int in_channels,
   return run_gemm(p, workspace, workspace_bytes, stream);
 }
 
-// Appends the bf16x6 planes of a packed weight: planes [3][count] bf16
-// (count = N * K, a multiple of 4).  Callers store them right after the
-// FP32 weight and pass FM_WEIGHTS_X6 in flags.
-int fm_split_weights(const float* weight_packed, long count, void* planes, hipStream_t stream) {
-  if (!weight_packed || !planes || count <= 0 || count % 4) return FM_BAD_ARGUMENT;
-  const long n4 = count / 4;
+// The bf16x6 planes of a packed weight W^T [rows][cols] (cols % 16 == 0):
+// [3][cols/16][rows][16] bf16.  Callers store them right after the FP32
+// weight and pass FM_WEIGHTS_X6 in flags.
+int fm_split_weights(const float* weight_packed, int rows, int cols, void* planes, hipStream_t stream) {
+  if (!weight_packed || !planes || rows <= 0 || cols <= 0) return FM_BAD_ARGUMENT;
+  if (cols % 16) return FM_UNSUPPORTED;
+  const long n4 = (long)rows * cols / 4;
   hipLaunchKernelGGL(split_weights_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream,
-                     weight_packed, n4, reinterpret_cast<bf16x4*>(planes));
+                     weight_packed, rows, cols, reinterpret_cast<bf16x4*>(planes));
   return (int)hipGetLastError();
 }
 

@@ -473,6 +473,228 @@ __global__ __launch_bounds__(NT, 3) void resblock_direct_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// The C = 128 / 256 residual block on the bf16 matrix cores (bf16x6: every
+// FP32 operand is three round-to-nearest bf16 pieces and each product is the
+// six cross terms of order <= 2, accumulated in FP32; the error stays at FP32
+// level).  The block layout is resblock_direct_kernel's: wave (wr, wc) owns
+// positions wr*32 .. +31, hidden channels wc*32 .. +31 and output channels
+// wc*64 .. +63; weights stream from L2 into a PD-deep register ring.
+// ELU(x) of rows t0-2 .. t0+BM-1 is split once as it is staged and kept as
+// three bf16 planes [BM+2][C] whose 16-byte chunks are XOR-swizzled by
+// (row & 7), so the row-shifted tap views read conflict-free.  The k3 conv is
+// computed transposed (hidden x positions: the weight planes are the A
+// operand) so each lane ends with four consecutive hidden channels of one
+// position, split and written as 8-byte pieces into hidden planes [BM][C/2]
+// laid over the consumed ELU(x) planes.  The 1x1 conv reads them as A
+// fragments.  Weights are the packed W^T followed by their planes in k16-tile
+// order [3][K/16][N][16] (fm_split_weights).  Both operands use the same k
+// order: in a 32-deep k unit, MFMA step s of lane half h covers k = 16s + 8h
+// .. +7, so a wave's weight fragment (32 rows x 16 k) is one contiguous 1 KB
+// run (a [3][N][K] row-major layout spreads it over 32 cache lines, which the
+// per-CU address path, not the MFMAs, then limits: 1.55x slower).
+template <int C, int BM, int WM, int PD>
+__global__ __launch_bounds__(NT, 3) void resblock_x6_kernel(
+    const float* __restrict__ x, int L, const __bf16* __restrict__ w1x, const float* __restrict__ b1,
+    const __bf16* __restrict__ w2x, const float* __restrict__ b2, int elu_out, float* __restrict__ y) {
+  constexpr int WN = 4 / WM, HC = C / 2, K1 = 3 * C;
+  constexpr int XR = BM + 2, XPLANE = XR * C * 2, HPLANE = BM * HC * 2;
+  constexpr int T1 = K1 / 32, T2 = HC / 32, FN2 = 2;
+  constexpr int T = T1 + T2 * FN2;
+  static_assert(BM == 32 * WM && HC / WN == 32 && C / WN == 32 * FN2, "wave tiling");
+  static_assert(3 * HPLANE <= 3 * XPLANE, "hidden planes fit over the ELU(x) planes");
+  __shared__ __attribute__((aligned(16))) char smem[3 * XPLANE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, lcol = lane & 31;
+  const int wr = wave / WN, wc = wave % WN;
+  const long b = blockIdx.y;
+  const int t0 = blockIdx.x * BM;
+  const float* xb = x + b * (long)L * C;
+  const bool fast = t0 >= 2 && t0 + BM <= L && (long)L * C * 4 <= 0x7fffffffL;
+  const __amdgpu_buffer_rsrc_t rx = fm_buffer(xb, L * C * 4);
+  const __amdgpu_buffer_rsrc_t ry = fm_buffer(y + b * (long)L * C, L * C * 4);
+  const int vrow = ((t0 + wr * 32 + 4 * h) * C + wc * 64 + lcol) * 4;
+  auto row_off = [&](int r, int j) { return ((8 * (r >> 2) + (r & 3)) * C + j * 32) * 4; };
+  // Byte offset of 16-byte chunk c of row r in a plane of `pitch`-byte rows.
+  auto chunk = [](int r, int c, int pitch) { return r * pitch + ((c ^ (r & 7)) << 4); };
+
+  constexpr int CH = XR * C / 4, U = (CH + NT - 1) / NT;
+  floatx4 xv[U];
+  if (fast) {
+    const int vo = ((t0 - 2) * C + 4 * tid) * 4;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      xv[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (u + 1 < U || tid + u * NT < CH) xv[u] = fm_buf_load4(rx, vo, u * NT * 16);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = tid + u * NT;
+      const int r = c / (C / 4), k = (c % (C / 4)) * 4;
+      const int t = t0 - 2 + r;
+      xv[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (c < CH && t >= 0 && t < L) xv[u] = *reinterpret_cast<const floatx4*>(xb + (long)t * C + k);
+    }
+  }
+  // Weight ring: unit u is 32 k of one 32-row weight slice, three planes,
+  // two MFMA steps each.
+  const __bf16* w1p = w1x + (wc * 32 + lcol) * 16 + 8 * h;
+  const __bf16* w2p = w2x + (wc * 64 + lcol) * 16 + 8 * h;
+  bf16x8 ring[PD][3][2];
+  auto load_unit = [&](int u, bf16x8 (&d)[3][2]) {
+    const __bf16* src;
+    long plane;
+    if (u < T1) {
+      src = w1p + u * 2 * HC * 16;
+      plane = (long)HC * K1;
+    } else {
+      const int v = u - T1, kt = v / FN2, j = v % FN2;
+      src = w2p + (long)(j * 32 + kt * 2 * C) * 16;
+      plane = (long)C * HC;
+    }
+    const int tile = u < T1 ? HC * 16 : C * 16;  // elements per k16 tile of a plane
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) d[pl][s] = *reinterpret_cast<const bf16x8*>(src + pl * plane + s * tile);
+  };
+#pragma unroll
+  for (int d = 0; d < PD; ++d) load_unit(d, ring[d]);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = tid + u * NT;
+    if (c >= CH) continue;
+    const int r = c / (C / 4), k = (c % (C / 4)) * 4;
+    bf16x4 p0, p1, p2;
+    split3(floatx4{fm_elu(xv[u].x), fm_elu(xv[u].y), fm_elu(xv[u].z), fm_elu(xv[u].w)}, p0, p1, p2);
+    char* dst = smem + chunk(r, k >> 3, C * 2) + (k & 4) * 2;
+    *reinterpret_cast<bf16x4*>(dst) = p0;
+    *reinterpret_cast<bf16x4*>(dst + XPLANE) = p1;
+    *reinterpret_cast<bf16x4*>(dst + 2 * XPLANE) = p2;
+  }
+  __syncthreads();
+
+  // k3 conv, transposed: acc[hidden][position].  The B fragments (ELU(x)
+  // planes) of the next unit are read while the current unit's MFMAs run.
+  const int prow = wr * 32 + lcol;
+  auto load_x = [&](int u, bf16x8 (&a)[3][2]) {
+    const int kk0 = u * 32, tap = kk0 / C, c0 = (kk0 % C) / 8 + h;
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        a[pl][s] = *reinterpret_cast<const bf16x8*>(smem + pl * XPLANE + chunk(prow + tap, c0 + 2 * s, C * 2));
+  };
+  floatx16 acc1[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc1[i][r] = 0.0f;
+  bf16x8 xf[2][3][2];
+  load_x(0, xf[0]);
+#pragma unroll
+  for (int u = 0; u < T1; ++u) {
+    if (u + 1 < T1) load_x(u + 1, xf[(u + 1) & 1]);
+    const bf16x8(&w)[3][2] = ring[u % PD];
+    const bf16x8(&a)[3][2] = xf[u & 1];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      acc1[0] = fm_mfma32_bf16(w[1][s], a[1][s], acc1[0]);
+      acc1[1] = fm_mfma32_bf16(w[2][s], a[0][s], acc1[1]);
+      acc1[0] = fm_mfma32_bf16(w[1][s], a[0][s], acc1[0]);
+      acc1[1] = fm_mfma32_bf16(w[0][s], a[2][s], acc1[1]);
+      acc1[0] = fm_mfma32_bf16(w[0][s], a[1][s], acc1[0]);
+      acc1[1] = fm_mfma32_bf16(w[0][s], a[0][s], acc1[1]);
+    }
+    if (u + PD < T) load_unit(u + PD, ring[u % PD]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __syncthreads();  // every wave is done with the ELU(x) planes
+  {
+    // Lane: position prow, hidden channels wc*32 + 8g + 4h .. +3 (g = 0..3).
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const floatx4 bb = *reinterpret_cast<const floatx4*>(b1 + wc * 32 + 8 * g + 4 * h);
+      floatx4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = fm_elu(__fadd_rn(__fadd_rn(acc1[0][4 * g + e], acc1[1][4 * g + e]), bb[e]));
+      bf16x4 p0, p1, p2;
+      split3(v, p0, p1, p2);
+      char* dst = smem + chunk(prow, wc * 4 + g, HC * 2) + 8 * h;
+      *reinterpret_cast<bf16x4*>(dst) = p0;
+      *reinterpret_cast<bf16x4*>(dst + HPLANE) = p1;
+      *reinterpret_cast<bf16x4*>(dst + 2 * HPLANE) = p2;
+    }
+  }
+  __syncthreads();
+
+  float* yb = y + b * (long)L * C;
+  float rv[FN2][16];
+  if (fast) {
+#pragma unroll
+    for (int j = 0; j < FN2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) rv[j][r] = fm_buf_load1(rx, vrow, row_off(r, j));
+  } else {
+#pragma unroll
+    for (int j = 0; j < FN2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = min(t0 + wr * 32 + fm_mfma32_row(r, lane), L - 1);
+        rv[j][r] = xb[(long)t * C + wc * 64 + j * 32 + lcol];
+      }
+  }
+  // 1x1 conv: acc[position][output channel], two 32-wide column tiles.
+  floatx16 acc2[FN2];
+#pragma unroll
+  for (int j = 0; j < FN2; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc2[j][r] = 0.0f;
+#pragma unroll
+  for (int kt = 0; kt < T2; ++kt) {
+    bf16x8 a[3][2];
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        a[pl][s] = *reinterpret_cast<const bf16x8*>(smem + pl * HPLANE + chunk(prow, kt * 4 + 2 * s + h, HC * 2));
+#pragma unroll
+    for (int j = 0; j < FN2; ++j) {
+      const int u = T1 + kt * FN2 + j;
+      const bf16x8(&w)[3][2] = ring[u % PD];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        acc2[j] = fm_mfma32_bf16(a[1][s], w[1][s], acc2[j]);
+        acc2[j] = fm_mfma32_bf16(a[2][s], w[0][s], acc2[j]);
+        acc2[j] = fm_mfma32_bf16(a[1][s], w[0][s], acc2[j]);
+        acc2[j] = fm_mfma32_bf16(a[0][s], w[2][s], acc2[j]);
+        acc2[j] = fm_mfma32_bf16(a[0][s], w[1][s], acc2[j]);
+        acc2[j] = fm_mfma32_bf16(a[0][s], w[0][s], acc2[j]);
+      }
+      if (u + PD < T) load_unit(u + PD, ring[u % PD]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < FN2; ++j) {
+    const int n = wc * 64 + j * 32 + lcol;
+    const float bias = b2[n];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = t0 + wr * 32 + fm_mfma32_row(r, lane);
+      float v = __fadd_rn(rv[j][r], __fadd_rn(acc2[j][r], bias));
+      if (elu_out) v = fm_elu(v);
+      if (fast) {
+        fm_buf_store1(v, ry, vrow, row_off(r, j));
+      } else if (t < L) {
+        yb[(long)t * C + n] = v;
+      }
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -490,18 +712,31 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
   if (!fm_resblock_supported(channels)) return FM_UNSUPPORTED;
   if (x == y) return FM_BAD_ARGUMENT;  // the halo rows of other blocks must stay intact
   if (batch == 0 || length == 0) return FM_OK;
+  const int elu = (elu_out & ~FM_WEIGHTS_X6) != 0;
+  const bool x6 = elu_out & FM_WEIGHTS_X6;
   if (channels == 64) {
     // Persistent: one 12-wave block per CU (LDS-bound), waves stride over 32-row tiles.
     const long tiles = (long)batch * ((length + 31) / 32);
     const int blocks = (int)std::min<long>((tiles + R64_WAVES - 1) / R64_WAVES, 256);
     hipLaunchKernelGGL((resblock64_kernel<false, false>), dim3(blocks), dim3(64 * R64_WAVES), 0, stream, x,
-                       batch, length, w1_packed, b1, w2_packed, b2, elu_out, y, nullptr, nullptr);
+                       batch, length, w1_packed, b1, w2_packed, b2, elu, y, nullptr, nullptr);
+  } else if (x6) {
+    // Split planes follow each packed weight: [3][N][K] bf16 after N*K floats.
+    const int hc = channels / 2;
+    const __bf16* w1x = reinterpret_cast<const __bf16*>(w1_packed + (long)hc * 3 * channels);
+    const __bf16* w2x = reinterpret_cast<const __bf16*>(w2_packed + (long)channels * hc);
+    if (channels == 128)
+      hipLaunchKernelGGL((resblock_x6_kernel<128, 64, 2, 2>), dim3((length + 63) / 64, batch), dim3(NT), 0,
+                         stream, x, length, w1x, b1, w2x, b2, elu, y);
+    else
+      hipLaunchKernelGGL((resblock_x6_kernel<256, 32, 1, 2>), dim3((length + 31) / 32, batch), dim3(NT), 0,
+                         stream, x, length, w1x, b1, w2x, b2, elu, y);
   } else if (channels == 128) {
     hipLaunchKernelGGL((resblock_direct_kernel<128, 64, 2, 3>), dim3((length + 63) / 64, batch), dim3(NT),
-                       0, stream, x, length, w1_packed, b1, w2_packed, b2, elu_out, y);
+                       0, stream, x, length, w1_packed, b1, w2_packed, b2, elu, y);
   } else {
     hipLaunchKernelGGL((resblock_direct_kernel<256, 32, 1, 3>), dim3((length + 31) / 32, batch), dim3(NT),
-                       0, stream, x, length, w1_packed, b1, w2_packed, b2, elu_out, y);
+                       0, stream, x, length, w1_packed, b1, w2_packed, b2, elu, y);
   }
   return (int)hipGetLastError();
 }

@@ -22,7 +22,7 @@ from . import _native as nat
 # Argument kinds and names per entry point, in C order, stream excluded
 # (in: const pointer, out: mutable pointer, i: integer / size, f: float).
 SPECS = {
-    "fm_split_weights": "in:weight_packed i:count out:planes",
+    "fm_split_weights": "in:weight_packed i:rows i:cols out:planes",
     "fm_conv1d": "in:x i:batch i:length i:in_channels in:weight_packed in:bias i:out_channels i:kernel i:stride i:pad_mode i:flags in:residual out:y i:y_length out:workspace i:workspace_bytes",
     "fm_conv1d_valid": "in:x i:batch i:length i:in_channels in:weight_packed in:bias i:out_channels i:kernel i:stride i:flags in:residual out:y out:workspace i:workspace_bytes",
     "fm_conv_transpose1d": "in:x i:batch i:length i:in_channels in:weight_packed in:bias i:out_channels i:kernel i:stride i:flags in:residual out:y out:workspace i:workspace_bytes",

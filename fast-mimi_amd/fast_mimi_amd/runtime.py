@@ -184,8 +184,9 @@ class MimiRuntime:
         # planes: W^T followed by [3][N][K] bf16 in one buffer.
         self._x6: dict[int, torch.Tensor] = {}
         for layer in self._conv_layers():
-            layer.w = self._with_planes(layer.w)
-            layer.flags = nat.WEIGHTS_X6
+            w = self._with_planes(layer.w)
+            if w is not layer.w:
+                layer.w, layer.flags = w, nat.WEIGHTS_X6
         for w in [m for lay in self.enc_tf + self.dec_tf for m in (lay.wqkv, lay.wo, lay.w1, lay.w2)]:
             self._x6[w.data_ptr()] = self._with_planes(w)
         self.workspace = torch.empty(_WORKSPACE_BYTES // 4, device=device)
@@ -207,13 +208,15 @@ class MimiRuntime:
 
     def _with_planes(self, w: torch.Tensor) -> torch.Tensor:
         """``w`` [N, K] (FP32 W^T) as the first N*K floats of a buffer that
-        continues with its three bf16 planes (``fm_split_weights``)."""
-        n = w.numel()
-        if n % 4:
+        continues with its three bf16 planes (``fm_split_weights``); ``w``
+        itself when K is not a multiple of 16."""
+        rows, cols = w.shape
+        if cols % 16:
             return w
-        buf = torch.empty(n + (3 * n * 2 + 3) // 4, device=self.device)
+        n = w.numel()
+        buf = torch.empty(n + 3 * n // 2, device=self.device)
         buf[:n].copy_(w.reshape(-1))
-        nat.call("fm_split_weights", buf.data_ptr(), n, buf.data_ptr() + 4 * n,
+        nat.call("fm_split_weights", buf.data_ptr(), rows, cols, buf.data_ptr() + 4 * n,
                  torch.cuda.current_stream(self.device).cuda_stream)
         return buf[:n].view(w.shape)
 
@@ -301,8 +304,8 @@ class MimiRuntime:
         if fused:
             self._tag = tag
             y = torch.empty_like(x)
-            self._call("fm_resblock", x, B, L, c2.c_out, c1.w, c1.b,
-                       c2.w, c2.b, 1 if elu_after else 0, y)
+            flags = (1 if elu_after else 0) | (c1.flags & c2.flags & nat.WEIGHTS_X6)
+            self._call("fm_resblock", x, B, L, c2.c_out, c1.w, c1.b, c2.w, c2.b, flags, y)
             return y
         self._tag = f"{tag}.c1"
         h, _ = self._conv(x, B, L, c1, nat.ELU_IN | nat.EPI_ELU)

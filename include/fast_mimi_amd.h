@@ -52,18 +52,20 @@ enum {
 int fm_abi_version(void);
 
 /*
- * bf16x6 weights: writes the three round-to-nearest bf16 pieces of each of
- * the `count` floats of a packed weight (count = N * K, a multiple of 4) as
- * planes [3][count] into `planes`.  A caller that stores the planes directly
- * after the FP32 weight (one buffer of count * 4 + count * 6 bytes) and adds
- * FM_WEIGHTS_X6 (64) to `flags` of fm_conv1d / fm_conv1d_valid /
- * fm_conv_transpose1d / fm_linear lets the large direct-load tiles run the
- * FP32 contraction as six bf16 MFMA products per operand pair (FP32-accurate,
- * see csrc/fm_gemm.hip); every other kernel reads the FP32 part only.
+ * bf16x6 weights: writes the three round-to-nearest bf16 pieces of each
+ * float of a packed weight W^T [rows][cols] (cols a multiple of 16, else
+ * FM_UNSUPPORTED) into `planes` in k16-tile order [3][cols/16][rows][16].
+ * A caller that stores the planes directly after the FP32 weight (one buffer
+ * of rows * cols * 10 bytes) and adds FM_WEIGHTS_X6 (64) to `flags` of
+ * fm_conv1d / fm_conv1d_valid / fm_conv_transpose1d / fm_linear (or to
+ * `elu_out` of fm_resblock, both weights split) lets the large tiles and the
+ * C = 128 / 256 residual blocks run the FP32 contraction as six bf16 MFMA
+ * products per operand pair (FP32-accurate, see csrc/fm_gemm.hip); every
+ * other kernel reads the FP32 part only.
  * No reference counterpart: it prepares the operands of the convolutions the
  * entry points below replace.
  */
-int fm_split_weights(const float* weight_packed, long count, void* planes, hipStream_t stream);
+int fm_split_weights(const float* weight_packed, int rows, int cols, void* planes, hipStream_t stream);
 
 /*
  * Causal Conv1d, dilation 1: left zero (pad_mode 0) or edge (pad_mode 1)
@@ -126,6 +128,9 @@ int fm_resblock_supported(int channels);
 int fm_resblock(const float* x, int batch, int length, int channels, const float* w1_packed,
                 const float* b1, const float* w2_packed, const float* b2, int elu_out, float* y,
                 hipStream_t stream);
+/* elu_out: nonzero (other than the FM_WEIGHTS_X6 bit) applies the trailing
+ * ELU; FM_WEIGHTS_X6 says both packed weights carry their fm_split_weights
+ * planes (channels 128 and 256 then run on the bf16 matrix cores). */
 
 /*
  * The SEANet encoder's first conv (1 -> 64 channels, kernel 7, causal, no

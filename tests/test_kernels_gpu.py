@@ -45,31 +45,46 @@ def close(got, want, rel=2e-5):
 
 
 def with_planes(w):
-    """A packed weight followed by its bf16x6 planes (fm_split_weights), as
-    the runtime stores it; returns the FP32 view at the buffer's start."""
+    """A packed weight W^T [N, K] followed by its bf16x6 planes
+    (fm_split_weights, k16-tile order [3][K/16][N][16]), as the runtime
+    stores it; returns the FP32 view at the buffer's start."""
+    rows, cols = w.shape
+    if cols % 16:
+        pytest.skip("bf16x6 planes need K to be a multiple of 16")
     n = w.numel()
-    buf = torch.empty(n + (6 * n + 3) // 4, device=DEV)
+    buf = torch.empty(n + 3 * n // 2, device=DEV)
     buf[:n].copy_(w.reshape(-1))
-    nat.call("fm_split_weights", buf.data_ptr(), n, buf.data_ptr() + 4 * n, stream())
+    nat.call("fm_split_weights", buf.data_ptr(), rows, cols, buf.data_ptr() + 4 * n, stream())
     torch.cuda.synchronize()
     return buf[:n].view(w.shape)
 
 
+def planes_of(buf):
+    """The three planes after a with_planes weight, back in [3][N][K] order."""
+    rows, cols = buf.shape
+    n = buf.numel()
+    raw = torch.empty(0, dtype=torch.bfloat16, device=DEV).set_(
+        buf.reshape(-1).untyped_storage(), n * 2, (3, cols // 16, rows, 16))
+    return raw.permute(0, 2, 1, 3).reshape(3, rows, cols)
+
+
 def test_split_weights_pieces_sum_to_the_weight():
     """Each float is three round-to-nearest bf16 pieces whose sum is within
-    2^-24 of it, each piece at most half an ulp of the previous remainder."""
+    2^-24 of it, each piece at most half an ulp of the previous remainder;
+    the planes are in k16-tile order."""
     g = torch.Generator().manual_seed(3)
-    w = (torch.randn(4096, generator=g) * torch.logspace(-6, 3, 4096)).to(DEV)
-    buf = with_planes(w.view(64, 64))
-    planes = buf.reshape(-1).untyped_storage()
-    n = w.numel()
-    raw = torch.empty(0, dtype=torch.bfloat16, device=DEV).set_(planes, n * 2, (3, n))
+    w = (torch.randn(48 * 80, generator=g) * torch.logspace(-6, 3, 48 * 80)).view(48, 80).to(DEV)
+    buf = with_planes(w)
+    raw = planes_of(buf)
     h = raw.float().cpu().double()
     wd = w.cpu().double()
     assert torch.equal(raw[0].cpu(), w.cpu().to(torch.bfloat16))
+    assert torch.equal(raw[1].cpu(), (wd - h[0]).float().to(torch.bfloat16))
     assert torch.all((wd - h.sum(0)).abs() <= wd.abs() * 2.0 ** -24)
     with pytest.raises(nat.NativeError, match="bad argument"):
-        nat.call("fm_split_weights", buf.data_ptr(), 6, buf.data_ptr(), stream())
+        nat.call("fm_split_weights", buf.data_ptr(), 0, 16, buf.data_ptr(), stream())
+    with pytest.raises(nat.NativeError, match="unsupported"):
+        nat.call("fm_split_weights", buf.data_ptr(), 4, 24, buf.data_ptr(), stream())
 
 
 def run_conv(x_ncl, w, b, stride, pad_mode, flags, ws, residual_ncl=None, y_len=None, x6=False):
@@ -251,8 +266,10 @@ def test_long_k_epilogues(B, C, L, ws):
                                    (1, 256, 300), (2, 256, 33), (1, 64, 240000), (2, 128, 6001),
                                    (2, 256, 12001)])
 @pytest.mark.parametrize("elu_out", [1, 0])
-def test_fused_resblock(B, C, L, elu_out):
-    """fm_resblock equals the reference block x + conv1x1(ELU(conv_k3(ELU(x))))."""
+@pytest.mark.parametrize("x6", [False, True])
+def test_fused_resblock(B, C, L, elu_out, x6):
+    """fm_resblock equals the reference block x + conv1x1(ELU(conv_k3(ELU(x)))),
+    on FP32 weights and on weights followed by their bf16x6 planes."""
     g = torch.Generator().manual_seed(C + L)
     x = torch.randn(B, C, L, generator=g)
     w1 = torch.randn(C // 2, C, 3, generator=g) / math.sqrt(3 * C)
@@ -260,10 +277,14 @@ def test_fused_resblock(B, C, L, elu_out):
     w2 = torch.randn(C, C // 2, 1, generator=g) / math.sqrt(C // 2)
     b2 = torch.randn(C, generator=g) * 0.1
     c1, c2 = _Conv(w1.to(DEV), b1.to(DEV)), _Conv(w2.to(DEV), b2.to(DEV))
+    flags = elu_out
+    if x6:
+        c1.w, c2.w = with_planes(c1.w), with_planes(c2.w)
+        flags |= nat.WEIGHTS_X6
     xd = x.transpose(1, 2).contiguous().to(DEV)
     y = torch.empty_like(xd)
     nat.call("fm_resblock", xd.data_ptr(), B, L, C, c1.w.data_ptr(), c1.b.data_ptr(), c2.w.data_ptr(),
-             c2.b.data_ptr(), elu_out, y.data_ptr(), stream())
+             c2.b.data_ptr(), flags, y.data_ptr(), stream())
     torch.cuda.synchronize()
     xd64 = x.double()
     h = F.elu(causal_conv1d(F.elu(xd64), w1.double(), b1.double()))
@@ -409,8 +430,6 @@ def test_linear_epilogues(rows, k, n, x6, ws):
     xd, wd = x.to(DEV), w.to(DEV)
     f = 0
     if x6:
-        if (n * k) % 4:
-            pytest.skip("bf16x6 planes need N * K to be a multiple of 4")
         wd, f = with_planes(wd), nat.WEIGHTS_X6
     close(run_linear(xd, wd, f, ws=ws).cpu(), x.double() @ w.double().t())
     close(run_linear(xd, wd, nat.EPI_GELU | f, ws=ws).cpu(), F.gelu(x.double() @ w.double().t()))
