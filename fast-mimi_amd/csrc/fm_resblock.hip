@@ -493,35 +493,85 @@ __global__ __launch_bounds__(NT, 3) void resblock_direct_kernel(
 // .. +7, so a wave's weight fragment (32 rows x 16 k) is one contiguous 1 KB
 // run (a [3][N][K] row-major layout spreads it over 32 cache lines, which the
 // per-CU address path, not the MFMAs, then limits: 1.55x slower).
-template <int C, int BM, int WM, int PD>
+template <int C, int BM, int WM, int PD, bool WAVE_IN, bool WAVE_OUT>
 __global__ __launch_bounds__(NT, 3) void resblock_x6_kernel(
     const float* __restrict__ x, int L, const __bf16* __restrict__ w1x, const float* __restrict__ b1,
-    const __bf16* __restrict__ w2x, const float* __restrict__ b2, int elu_out, float* __restrict__ y) {
+    const __bf16* __restrict__ w2x, const float* __restrict__ b2, int elu_out, float* __restrict__ y,
+    const float* __restrict__ w0, const float* __restrict__ b0) {
   constexpr int WN = 4 / WM, HC = C / 2, K1 = 3 * C;
   constexpr int XR = BM + 2, XPLANE = XR * C * 2, HPLANE = BM * HC * 2;
   constexpr int T1 = K1 / 32, T2 = HC / 32, FN2 = 2;
   constexpr int T = T1 + T2 * FN2;
   static_assert(BM == 32 * WM && HC / WN == 32 && C / WN == 32 * FN2, "wave tiling");
   static_assert(3 * HPLANE <= 3 * XPLANE, "hidden planes fit over the ELU(x) planes");
+  static_assert(!(WAVE_IN || WAVE_OUT) || (C == 64 && WM == 4), "waveform ends: one wave per 32 rows x 64 channels");
+  static_assert(!WAVE_OUT || 4 * 32 * 68 * 4 <= 3 * XPLANE, "output tiles fit");
   __shared__ __attribute__((aligned(16))) char smem[3 * XPLANE];
+  __shared__ float wins[WAVE_IN ? BM + 8 : 1];  // WAVE_IN: waveform samples t0-8 .. t0+BM-1
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = lane >> 5, lcol = lane & 31;
   const int wr = wave / WN, wc = wave % WN;
   const long b = blockIdx.y;
   const int t0 = blockIdx.x * BM;
-  const float* xb = x + b * (long)L * C;
+  // WAVE_IN: x is the waveform [batch][L] and the block input is the first
+  // conv of the encoder, x64[t][c] = b0[c] + sum_j w0[c][j] wav[t-6+j]
+  // (w0 [64][7], zero outside the waveform; the FMA order of
+  // conv_cin1_kernel), formed for the staged rows and again for the
+  // residual.  WAVE_OUT: y receives per row the three tap products of the
+  // decoder's last conv (w0 = w3 [3][64]) instead of the block output.
+  const float* xb = x + b * (long)L * (WAVE_IN ? 1 : C);
   const bool fast = t0 >= 2 && t0 + BM <= L && (long)L * C * 4 <= 0x7fffffffL;
-  const __amdgpu_buffer_rsrc_t rx = fm_buffer(xb, L * C * 4);
+  const __amdgpu_buffer_rsrc_t rx = fm_buffer(xb, L * (WAVE_IN ? 1 : C) * 4);
   const __amdgpu_buffer_rsrc_t ry = fm_buffer(y + b * (long)L * C, L * C * 4);
   const int vrow = ((t0 + wr * 32 + 4 * h) * C + wc * 64 + lcol) * 4;
   auto row_off = [&](int r, int j) { return ((8 * (r >> 2) + (r & 3)) * C + j * 32) * 4; };
-  // Byte offset of 16-byte chunk c of row r in a plane of `pitch`-byte rows.
-  auto chunk = [](int r, int c, int pitch) { return r * pitch + ((c ^ (r & 7)) << 4); };
+  // Byte offset of 16-byte chunk c of row r in a plane of `pitch`-byte rows
+  // (chunks XOR-swizzled by the row within groups of up to 8 chunks).
+  auto chunk = [](int r, int c, int pitch) {
+    const int m = (pitch >> 4) < 8 ? (pitch >> 4) - 1 : 7;
+    return r * pitch + ((c ^ (r & m)) << 4);
+  };
 
   constexpr int CH = XR * C / 4, U = (CH + NT - 1) / NT;
   floatx4 xv[U];
-  if (fast) {
+  auto conv0 = [&](int c, int i0) {  // x64 at channel c from window samples i0 .. i0+6
+    float acc = b0[c];
+#pragma unroll
+    for (int j = 0; j < 7; ++j) acc = fmaf(w0[c * 7 + j], wins[i0 + j], acc);
+    return acc;
+  };
+  if constexpr (WAVE_IN) {
+    for (int i = tid; i < BM + 8; i += NT) {
+      const int t = t0 - 8 + i;
+      wins[i] = (t >= 0 && t < L) ? xb[t] : 0.0f;
+    }
+    __syncthreads();
+    // Staged row r (t = t0-2+r) reads samples t-6 .. t: window r .. r+6.
+    const int k = (tid % (C / 4)) * 4;
+    float w0r[4][7], b0r[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      b0r[e] = b0[k + e];
+#pragma unroll
+      for (int j = 0; j < 7; ++j) w0r[e][j] = w0[(k + e) * 7 + j];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = tid + u * NT;
+      const int r = c / (C / 4), t = t0 - 2 + r;
+      xv[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (c < CH && t >= 0 && t < L) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float acc = b0r[e];
+#pragma unroll
+          for (int j = 0; j < 7; ++j) acc = fmaf(w0r[e][j], wins[r + j], acc);
+          xv[u][e] = acc;
+        }
+      }
+    }
+  } else if (fast) {
     const int vo = ((t0 - 2) * C + 4 * tid) * 4;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -632,7 +682,13 @@ __global__ __launch_bounds__(NT, 3) void resblock_x6_kernel(
 
   float* yb = y + b * (long)L * C;
   float rv[FN2][16];
-  if (fast) {
+  if constexpr (WAVE_IN) {
+    // Row rr = wr*32 + fm_mfma32_row(r, lane) (t = t0 + rr) reads window rr+2 .. rr+8.
+#pragma unroll
+    for (int j = 0; j < FN2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) rv[j][r] = conv0(wc * 64 + j * 32 + lcol, wr * 32 + fm_mfma32_row(r, lane) + 2);
+  } else if (fast) {
 #pragma unroll
     for (int j = 0; j < FN2; ++j)
 #pragma unroll
@@ -677,6 +733,45 @@ __global__ __launch_bounds__(NT, 3) void resblock_x6_kernel(
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+  if constexpr (WAVE_OUT) {
+    // Output rows into this wave's [32][68] tile (over the consumed planes),
+    // then lane (r, half hh) forms w3[j] . y[r] over 32 channels and the
+    // halves are summed: D[b][t] = {d0, d1, d2, 0}.
+    __syncthreads();
+    float* E = reinterpret_cast<float*>(smem) + wave * 32 * 68;
+#pragma unroll
+    for (int j = 0; j < FN2; ++j) {
+      const float bias = b2[j * 32 + lcol];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float v = __fadd_rn(rv[j][r], __fadd_rn(acc2[j][r], bias));
+        if (elu_out) v = fm_elu(v);
+        E[fm_mfma32_row(r, lane) * 68 + j * 32 + lcol] = v;
+      }
+    }
+    wave_lds_fence();
+    const int r = lane & 31, hh = lane >> 5;
+    float d[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < 32; c += 4) {
+      const floatx4 v = *reinterpret_cast<const floatx4*>(E + r * 68 + 32 * hh + c);
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const floatx4 wj = *reinterpret_cast<const floatx4*>(w0 + j * 64 + 32 * hh + c);
+        d[j] = fmaf(wj[0], v[0], d[j]);
+        d[j] = fmaf(wj[1], v[1], d[j]);
+        d[j] = fmaf(wj[2], v[2], d[j]);
+        d[j] = fmaf(wj[3], v[3], d[j]);
+      }
+    }
+    floatx4 o;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) o[j] = __fadd_rn(d[j], __shfl_xor(d[j], 32, 64));
+    o[3] = 0.0f;
+    const int t = t0 + wr * 32 + r;
+    if (hh == 0 && t < L) *reinterpret_cast<floatx4*>(y + (b * L + t) * 4) = o;
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < FN2; ++j) {
     const int n = wc * 64 + j * 32 + lcol;
@@ -697,6 +792,11 @@ __global__ __launch_bounds__(NT, 3) void resblock_x6_kernel(
 
 }  // namespace
 
+// The bf16x6 planes stored after a packed weight W^T [rows][cols].
+static const __bf16* planes_after(const float* w, int rows, int cols) {
+  return reinterpret_cast<const __bf16*>(w + (long)rows * cols);
+}
+
 extern "C" {
 
 // Channel widths with a fused kernel; others run as two fm_conv1d calls.
@@ -714,23 +814,25 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
   if (batch == 0 || length == 0) return FM_OK;
   const int elu = (elu_out & ~FM_WEIGHTS_X6) != 0;
   const bool x6 = elu_out & FM_WEIGHTS_X6;
-  if (channels == 64) {
+  if (x6) {
+    // Split planes follow each packed weight (fm_split_weights).
+    const __bf16* w1x = planes_after(w1_packed, channels / 2, 3 * channels);
+    const __bf16* w2x = planes_after(w2_packed, channels, channels / 2);
+    if (channels == 64)
+      hipLaunchKernelGGL((resblock_x6_kernel<64, 128, 4, 2, false, false>), dim3((length + 127) / 128, batch),
+                         dim3(NT), 0, stream, x, length, w1x, b1, w2x, b2, elu, y, nullptr, nullptr);
+    else if (channels == 128)
+      hipLaunchKernelGGL((resblock_x6_kernel<128, 64, 2, 2, false, false>), dim3((length + 63) / 64, batch),
+                         dim3(NT), 0, stream, x, length, w1x, b1, w2x, b2, elu, y, nullptr, nullptr);
+    else
+      hipLaunchKernelGGL((resblock_x6_kernel<256, 32, 1, 2, false, false>), dim3((length + 31) / 32, batch),
+                         dim3(NT), 0, stream, x, length, w1x, b1, w2x, b2, elu, y, nullptr, nullptr);
+  } else if (channels == 64) {
     // Persistent: one 12-wave block per CU (LDS-bound), waves stride over 32-row tiles.
     const long tiles = (long)batch * ((length + 31) / 32);
     const int blocks = (int)std::min<long>((tiles + R64_WAVES - 1) / R64_WAVES, 256);
     hipLaunchKernelGGL((resblock64_kernel<false, false>), dim3(blocks), dim3(64 * R64_WAVES), 0, stream, x,
                        batch, length, w1_packed, b1, w2_packed, b2, elu, y, nullptr, nullptr);
-  } else if (x6) {
-    // Split planes follow each packed weight: [3][N][K] bf16 after N*K floats.
-    const int hc = channels / 2;
-    const __bf16* w1x = reinterpret_cast<const __bf16*>(w1_packed + (long)hc * 3 * channels);
-    const __bf16* w2x = reinterpret_cast<const __bf16*>(w2_packed + (long)channels * hc);
-    if (channels == 128)
-      hipLaunchKernelGGL((resblock_x6_kernel<128, 64, 2, 2>), dim3((length + 63) / 64, batch), dim3(NT), 0,
-                         stream, x, length, w1x, b1, w2x, b2, elu, y);
-    else
-      hipLaunchKernelGGL((resblock_x6_kernel<256, 32, 1, 2>), dim3((length + 31) / 32, batch), dim3(NT), 0,
-                         stream, x, length, w1x, b1, w2x, b2, elu, y);
   } else if (channels == 128) {
     hipLaunchKernelGGL((resblock_direct_kernel<128, 64, 2, 3>), dim3((length + 63) / 64, batch), dim3(NT),
                        0, stream, x, length, w1_packed, b1, w2_packed, b2, elu, y);
@@ -751,10 +853,17 @@ int fm_conv_resblock64(const float* wav, int batch, int length, const float* w0_
       length < 0)
     return FM_BAD_ARGUMENT;
   if (batch == 0 || length == 0) return FM_OK;
+  const int elu = (elu_out & ~FM_WEIGHTS_X6) != 0;
+  if (elu_out & FM_WEIGHTS_X6) {
+    hipLaunchKernelGGL((resblock_x6_kernel<64, 128, 4, 2, true, false>), dim3((length + 127) / 128, batch),
+                       dim3(NT), 0, stream, wav, length, planes_after(w1_packed, 32, 192), b1,
+                       planes_after(w2_packed, 64, 32), b2, elu, y, w0_packed, b0);
+    return (int)hipGetLastError();
+  }
   const long tiles = (long)batch * ((length + 31) / 32);
   const int blocks = (int)std::min<long>((tiles + R64_WAVES - 1) / R64_WAVES, 256);
   hipLaunchKernelGGL((resblock64_kernel<true, false>), dim3(blocks), dim3(64 * R64_WAVES), 0, stream, wav,
-                     batch, length, w1_packed, b1, w2_packed, b2, elu_out, y, w0_packed, b0);
+                     batch, length, w1_packed, b1, w2_packed, b2, elu, y, w0_packed, b0);
   return (int)hipGetLastError();
 }
 
@@ -775,11 +884,18 @@ int fm_resblock64_conv(const float* x, int batch, int length, const float* w1_pa
   if (batch == 0 || y_len == 0) return FM_OK;
   if (!workspace || workspace_bytes < fm_resblock64_conv_workspace_bytes(batch, length))
     return FM_WORKSPACE_TOO_SMALL;
-  const long tiles = (long)batch * ((length + 31) / 32);
-  const int blocks = (int)std::min<long>((tiles + R64_WAVES - 1) / R64_WAVES, 256);
-  hipLaunchKernelGGL((resblock64_kernel<false, true>), dim3(blocks), dim3(64 * R64_WAVES), 0, stream,
-                     x, batch, length, w1_packed, b1, w2_packed, b2, elu_mid, workspace, w3_packed,
-                     nullptr);
+  const int elu = (elu_mid & ~FM_WEIGHTS_X6) != 0;
+  if (elu_mid & FM_WEIGHTS_X6) {
+    hipLaunchKernelGGL((resblock_x6_kernel<64, 128, 4, 2, false, true>), dim3((length + 127) / 128, batch),
+                       dim3(NT), 0, stream, x, length, planes_after(w1_packed, 32, 192), b1,
+                       planes_after(w2_packed, 64, 32), b2, elu, workspace, w3_packed, nullptr);
+  } else {
+    const long tiles = (long)batch * ((length + 31) / 32);
+    const int blocks = (int)std::min<long>((tiles + R64_WAVES - 1) / R64_WAVES, 256);
+    hipLaunchKernelGGL((resblock64_kernel<false, true>), dim3(blocks), dim3(64 * R64_WAVES), 0, stream,
+                       x, batch, length, w1_packed, b1, w2_packed, b2, elu, workspace, w3_packed,
+                       nullptr);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   hipLaunchKernelGGL(conv3_finish_kernel, dim3((y_len + 255) / 256, batch), dim3(256), 0, stream,

@@ -420,7 +420,7 @@ class MimiRuntime:
             h = torch.empty((B, S, 64), device=self.device)
             self._call("fm_conv_resblock64", x, B, S, first.w,
                        first.b, c1.w, c1.b, c2.w,
-                       c2.b, 1, h)
+                       c2.b, 1 | (c1.flags & c2.flags & nat.WEIGHTS_X6), h)
             L, start = S, 1
         else:
             self._tag = "enc.first"
@@ -590,7 +590,7 @@ class MimiRuntime:
                 y = torch.empty((B, out_length), device=self.device)
                 last = self.dec_last
                 self._call("fm_resblock64_conv", h, B, L, c1.w, c1.b,
-                           c2.w, c2.b, 1, last.w, last.b,
+                           c2.w, c2.b, 1 | (c1.flags & c2.flags & nat.WEIGHTS_X6), last.w, last.b,
                            out_length, y, d, d.numel() * 4)
                 return y.view(B, 1, out_length)
             h = self._resblock(h, B, L, block, elu_after=True, tag=f"dec.res{convt.c_out}")

@@ -296,8 +296,10 @@ def test_fused_resblock(B, C, L, elu_out, x6):
 
 @pytest.mark.parametrize("B,L", [(1, 240000), (2, 1001), (1, 1), (3, 33), (1, 31), (2, 32), (1, 70000)])
 @pytest.mark.parametrize("elu_out", [1, 0])
-def test_conv_resblock64_equals_conv_then_block(B, L, elu_out, ws):
-    """fm_conv_resblock64 == fm_conv1d (1 -> 64, k 7) then fm_resblock, bit for bit."""
+@pytest.mark.parametrize("x6", [False, True], ids=["fp32", "bf16x6"])
+def test_conv_resblock64_equals_conv_then_block(B, L, elu_out, x6, ws):
+    """fm_conv_resblock64 == fm_conv1d (1 -> 64, k 7) then fm_resblock, bit for
+    bit, on FP32 weights and on weights with their bf16x6 planes."""
     g = torch.Generator().manual_seed(B * 31 + L)
     wav = torch.randn(B, 1, L, generator=g) * 0.5
     w0 = torch.randn(64, 1, 7, generator=g) / 3
@@ -308,16 +310,20 @@ def test_conv_resblock64_equals_conv_then_block(B, L, elu_out, ws):
     b2 = torch.randn(64, generator=g) * 0.1
     c0 = _Conv(w0.to(DEV), b0.to(DEV))
     c1, c2 = _Conv(w1.to(DEV), b1.to(DEV)), _Conv(w2.to(DEV), b2.to(DEV))
+    flags = elu_out
+    if x6:
+        c1.w, c2.w = with_planes(c1.w), with_planes(c2.w)
+        flags |= nat.WEIGHTS_X6
     wd = wav.reshape(B, L).contiguous().to(DEV)
     h = torch.empty(B, L, 64, device=DEV)
     nat.call("fm_conv1d", wd.data_ptr(), B, L, 1, c0.w.data_ptr(), c0.b.data_ptr(), 64, 7, 1, 0, 0,
              None, h.data_ptr(), L, ws.data_ptr(), WS_BYTES, stream())
     want = torch.empty_like(h)
     nat.call("fm_resblock", h.data_ptr(), B, L, 64, c1.w.data_ptr(), c1.b.data_ptr(), c2.w.data_ptr(),
-             c2.b.data_ptr(), elu_out, want.data_ptr(), stream())
+             c2.b.data_ptr(), flags, want.data_ptr(), stream())
     got = torch.full_like(h, float("nan"))
     nat.call("fm_conv_resblock64", wd.data_ptr(), B, L, c0.w.data_ptr(), c0.b.data_ptr(),
-             c1.w.data_ptr(), c1.b.data_ptr(), c2.w.data_ptr(), c2.b.data_ptr(), elu_out,
+             c1.w.data_ptr(), c1.b.data_ptr(), c2.w.data_ptr(), c2.b.data_ptr(), flags,
              got.data_ptr(), stream())
     torch.cuda.synchronize()
     assert torch.equal(got, want)
@@ -332,8 +338,10 @@ def test_conv_resblock64_equals_conv_then_block(B, L, elu_out, ws):
 
 @pytest.mark.parametrize("B,L,y_len", [(1, 240000, 240000), (2, 1001, 990), (1, 1, 1), (3, 33, 33),
                                        (1, 31, 2), (2, 32, 32), (1, 70000, 69999)])
-def test_resblock64_conv_matches_reference(B, L, y_len):
-    """fm_resblock64_conv == block (ELU after) then the 64 -> 1, k = 3 conv, cropped."""
+@pytest.mark.parametrize("x6", [False, True], ids=["fp32", "bf16x6"])
+def test_resblock64_conv_matches_reference(B, L, y_len, x6):
+    """fm_resblock64_conv == block (ELU after) then the 64 -> 1, k = 3 conv,
+    cropped; the bf16x6 form also against the FP32 form at every size."""
     g = torch.Generator().manual_seed(B * 17 + L + y_len)
     x = torch.randn(B, 64, L, generator=g)
     w1 = torch.randn(32, 64, 3, generator=g) / math.sqrt(192)
@@ -351,6 +359,16 @@ def test_resblock64_conv_matches_reference(B, L, y_len):
     nat.call("fm_resblock64_conv", xd.data_ptr(), B, L, c1.w.data_ptr(), c1.b.data_ptr(), c2.w.data_ptr(),
              c2.b.data_ptr(), 1, c3.w.data_ptr(), c3.b.data_ptr(), y_len, out.data_ptr(), d.data_ptr(),
              wsb, stream())
+    if x6:
+        fp32 = out.clone()
+        c1.w, c2.w = with_planes(c1.w), with_planes(c2.w)
+        out.fill_(float("nan"))
+        nat.call("fm_resblock64_conv", xd.data_ptr(), B, L, c1.w.data_ptr(), c1.b.data_ptr(), c2.w.data_ptr(),
+                 c2.b.data_ptr(), 1 | nat.WEIGHTS_X6, c3.w.data_ptr(), c3.b.data_ptr(), y_len, out.data_ptr(),
+                 d.data_ptr(), wsb, stream())
+        torch.cuda.synchronize()
+        assert not torch.isnan(out).any()
+        close(out, fp32, rel=5e-5)
     torch.cuda.synchronize()
     if L <= 2000:
         x64 = x.double()
