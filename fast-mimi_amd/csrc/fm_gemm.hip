@@ -1418,6 +1418,7 @@ constexpr TileCfg kBig64 = {64, 128, 1, 32, 11, 0};    // double-buffered, 32x32
 constexpr TileCfg kDl128 = {128, 128, 1, 32, 13, 0};
 constexpr TileCfg kX6 = {128, 128, 1, 32, 16, 0};     // bf16x6 tiles (k-tile 16; splits stay 32-aligned)
 constexpr TileCfg kX6Big = {256, 128, 1, 32, 17, 0};
+constexpr TileCfg kX6Small = {64, 128, 1, 32, 18, 0};  // four waves of 64x32
 constexpr TileCfg kDl192 = {192, 128, 1, 32, 14, 0};
 // 64x128 runs one block per CU: 64-deep k-tiles (96 KB ring) halve its barriers.
 constexpr TileCfg kDl64 = {64, 128, 1, 64, 15, 0};
@@ -1563,9 +1564,25 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
   // 64x128 FP32 tiles on all CUs against 80-128 bf16x6 tiles).
   const bool x6_ok = (p.flags & FM_WEIGHTS_X6) && big_ok && !(p.flags & FM_REPLICATE) &&
                      p.C_in % 16 == 0 && p.K % 16 == 0;
-  if (x6_ok && cfg.id >= 9 && cfg.id <= 15 && cfg.id != 12 && tile_count(M, p.N, kX6) * splits >= 192) {
-    cfg = tile_count(M, p.N, kX6Big) >= 384 ? kX6Big : kX6;
-    tiles = tile_count(M, p.N, cfg);
+  if (x6_ok && cfg.id >= 9 && cfg.id <= 15 && cfg.id != 12) {
+    const long t128 = tile_count(M, p.N, kX6);
+    if (p.K >= 1024 && M >= 1024 && t128 >= 80 && t128 * splits < 480 && workspace) {
+      // Long K over a few hundred tiles (the 2048-deep fc2 projection at
+      // 2500-8000 rows, the 12-25 Hz convs): the bf16x6 tile split along K
+      // to >= 480 blocks (at most 4 splits of >= 256 k), 64x128 tiles when
+      // four splits of 128x128 stay below that.  Measured against the FP32
+      // pick: fc2 at 4000 rows 65 vs 77 us, at 2500 rows 50 vs 59 us.
+      cfg = t128 * 4 >= 480 ? kX6 : kX6Small;
+      tiles = tile_count(M, p.N, cfg);
+      splits = 1;
+      while (splits < 4 && tiles * splits < 480 && p.K / (2 * splits) >= 256) splits *= 2;
+    } else if (t128 * splits >= 192) {
+      // 256x128 where it gives >= 384 tiles; unsplit grids of 192-383
+      // 128x128 tiles take 64x128 (the 2500-row qkv / fc1 and 8000-row
+      // output projections: 38 vs 42, 46 vs 51, 36 vs 39 us).
+      cfg = tile_count(M, p.N, kX6Big) >= 384 ? kX6Big : (t128 < 384 && splits == 1 ? kX6Small : kX6);
+      tiles = tile_count(M, p.N, cfg);
+    }
   }
   if (splits > 1) {
     const size_t per = (size_t)M * p.N * sizeof(float);
@@ -1604,6 +1621,10 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
       break;
     case 17:
       hipLaunchKernelGGL((gemm_x6_kernel<256, 128, 2, 4, 2>), grid, dim3(512), 0, s, p,
+                         reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
+      break;
+    case 18:
+      hipLaunchKernelGGL((gemm_x6_kernel<64, 128, 1, 4, 2>), grid, dim3(256), 0, s, p,
                          reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
       break;
     case 7: hipLaunchKernelGGL((gemm_mid_kernel<64, 64, 1>), grid, dim3(NTHREADS), 0, s, p); break;

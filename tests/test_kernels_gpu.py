@@ -159,6 +159,8 @@ DL_CASES = [
     (1, 2048, 512, 1, 1, 4000, None),   # long K, one 64x128 tile per CU, unsplit
     (1, 480, 512, 1, 1, 4000, None),    # 64x128 pick with C_in % 64 == 32 (32-deep tile)
     (1, 128, 256, 8, 4, 240001, 59990),  # >= 384 256x128 bf16x6 tiles, partial last row tile, crop
+    (1, 512, 1536, 1, 1, 2500, None),   # 240 128x128 tiles: 64x128 bf16x6 tiles
+    (1, 2048, 512, 1, 1, 2500, 2499),   # long K, 80 tiles: 64x128 bf16x6 tiles split along K
 ]
 
 
