@@ -93,6 +93,12 @@ FM_DEVICE floatx4 fm_mfma16(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// One v_mfma_f32_16x16x32_bf16: lane l supplies row / column l % 16 at
+// k = 8 (l / 16) .. +7; results as fm_mfma16.
+FM_DEVICE floatx4 fm_mfma16_bf16(bf16x8 a, bf16x8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
 constexpr int QB = 32;  // queries per block (one MFMA column tile)
 constexpr int KB = 32;  // keys per MFMA row tile
 
@@ -1230,7 +1236,14 @@ __global__ __launch_bounds__(512) void row_stream_linear_kernel(
 // are summed through LDS in wave order; epilogue as in row_linear_kernel.
 
 
-template <int K, int BN>
+// X6: the weight is W^T's bf16x6 planes ([3][K/16][N][16], fm_split_weights)
+// and the contraction runs on v_mfma_f32_16x16x32_bf16 as the six cross
+// terms of three-piece splits (FP32-accurate, see fm_gemm.hip): in a 32-deep
+// k step, lane group g covers k = 8g .. 8g + 7 of A and B, the A fragment is
+// split as it is read, and each B fragment of a plane is a 512-byte run.
+// 1.85x the FP32 16x16x4 MFMA rate per contraction (measured 13.4 vs 18.5 ns
+// per instruction, six against eight per 16 x 16 x 32).
+template <int K, int BN, bool X6 = false>
 __global__ __launch_bounds__(512) void row16_linear_kernel(
     const float* __restrict__ x, int rows, const float* __restrict__ gamma,
     const float* __restrict__ beta, float eps, const float* __restrict__ wp, int N, int flags,
@@ -1251,32 +1264,10 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
   const long m0 = (long)blockIdx.y * BM;
   const int n0 = blockIdx.x * BN;
   const int kw0 = wave * KW;
-  const long tstride = (long)(K / 64) * 4 * 64 * 4;  // floats between 16-column tiles
-  const float* wb = wp + ((((long)(n0 / 16) * (K / 64) + kw0 / 64) * 4) * 64 + lane) * 4;
-  const float* xs = x + min(m0 + li, (long)rows - 1) * K + kw0 + 16 * g;
 
-  floatx4 a[2][4], b[2][NT][4];
-  auto load_b = [&](int buf, int piece) {
-#pragma unroll
-    for (int j = 0; j < NT; ++j)
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        b[buf][j][t] = *reinterpret_cast<const floatx4*>(wb + j * tstride + piece * 1024 + t * 256);
-  };
-  auto load_a = [&](int buf, int piece) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-      a[buf][t] = STAGE ? *reinterpret_cast<const floatx4*>(As + li * PA + kw0 + 64 * piece + 16 * g + 4 * t)
-                        : *reinterpret_cast<const floatx4*>(xs + 64 * piece + 4 * t);
-  };
-
-  // The input rows are the critical path (LayerNorm, then the A operand).
-  // With staging, the weight fragments are issued once the rows are in LDS:
-  // issued earlier they queue ahead of the LayerNorm parameters and the
-  // other waves' rows (measured 0.2-0.6 us faster per launch at 250 rows).
-  if (!STAGE) load_b(0, 0);
-  if (STAGE) {
-    // 32 lanes per row, float4 chunks p, p + 32, ...
+  // The 16 input rows into LDS, layer-normalised when gamma is given (32
+  // lanes per row, float4 chunks p, p + 32, ..., shuffle-reduced).
+  auto stage_rows = [&]() {
     constexpr int TPR = 32, CH = K / 4 / TPR;
     const int r = tid / TPR, p = tid % TPR;
     const bool valid = m0 + r < rows;
@@ -1318,12 +1309,11 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
     for (int u = 0; u < CH; ++u)
       *reinterpret_cast<floatx4*>(As + r * PA + 4 * (p + TPR * u)) =
           valid ? v[u] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    load_b(0, 0);
-    __syncthreads();
-  }
-  load_a(0, 0);
-  // Epilogue operands (residual, LayerScale, RoPE tables) are fetched now so
-  // their latency hides under the MFMAs instead of trailing the reduction.
+  };
+
+  // Epilogue operands (residual, LayerScale, RoPE tables), fetched before
+  // the MFMAs so their latency hides under them instead of trailing the
+  // reduction.
   const int er = tid / (BN / OPT), ec = (tid % (BN / OPT)) * OPT;
   const long m = m0 + er;
   const long mc = min(m, (long)rows - 1);
@@ -1331,19 +1321,170 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
   const bool rope = BN == 64 && cos_t && n0 < rope_cols;
   const bool res_scale = flags & FM_EPI_RES_SCALE;
   float e_res[OPT], e_scale[OPT], e_cos[OPT], e_sin[OPT];
+  auto fetch_epilogue = [&]() {
 #pragma unroll
-  for (int c = 0; c < OPT; ++c) {
-    const int n = n0 + ec + c;
-    e_res[c] = res_scale ? res[mc * N + n] : 0.0f;
-    e_scale[c] = res_scale ? scale[n] : 0.0f;
-    e_cos[c] = rope ? cos_t[(long)tpos * 64 + ec + c] : 0.0f;
-    e_sin[c] = rope ? sin_t[(long)tpos * 64 + ec + c] : 0.0f;
-  }
-  __builtin_amdgcn_sched_barrier(0);
+    for (int c = 0; c < OPT; ++c) {
+      const int n = n0 + ec + c;
+      e_res[c] = res_scale ? res[mc * N + n] : 0.0f;
+      e_scale[c] = res_scale ? scale[n] : 0.0f;
+      e_cos[c] = rope ? cos_t[(long)tpos * 64 + ec + c] : 0.0f;
+      e_sin[c] = rope ? sin_t[(long)tpos * 64 + ec + c] : 0.0f;
+    }
+  };
+
+  // The 8 waves' partial tiles summed through LDS in wave order, then the
+  // epilogue (RoPE, GELU, LayerScale residual).
+  auto reduce_and_store = [&](floatx4 (&acc)[NT]) {
+    if (STAGE) __syncthreads();  // all waves are done with As before it becomes `red`
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[(wave * BM + 4 * g + r) * PR + 16 * j + li] = acc[j][r];
+    __syncthreads();
+    // OPT consecutive outputs per thread, BN / OPT threads per row.
+    float out[OPT];
+#pragma unroll
+    for (int c = 0; c < OPT; ++c) {
+      float v = red[er * PR + ec + c];
+#pragma unroll
+      for (int q = 1; q < NWV; ++q) v = __fadd_rn(v, red[(q * BM + er) * PR + ec + c]);
+      out[c] = v;
+    }
+    if (rope) {
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < OPT; ++c) red[er * PR + ec + c] = out[c];
+      __syncthreads();
+    }
+    if (m >= rows) return;
+#pragma unroll
+    for (int c = 0; c < OPT; ++c) {
+      float v = out[c];
+      if (rope) {
+        const int d = ec + c;
+        const float partner = red[er * PR + (d < 32 ? d + 32 : d - 32)];
+        const float rot = d < 32 ? -partner : partner;
+        v = __fadd_rn(__fmul_rn(v, e_cos[c]), __fmul_rn(rot, e_sin[c]));
+      }
+      if (flags & FM_EPI_GELU) v = fm_gelu(v);
+      if (res_scale) v = __fadd_rn(e_res[c], __fmul_rn(e_scale[c], v));
+      out[c] = v;
+    }
+    float* dst = y + m * N + n0 + ec;
+    if constexpr (OPT == 2) {
+      *reinterpret_cast<float2*>(dst) = float2{out[0], out[1]};
+    } else {
+#pragma unroll
+      for (int c = 0; c < OPT; ++c) dst[c] = out[c];
+    }
+  };
 
   floatx4 acc[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j) acc[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  if constexpr (X6) {
+    constexpr int KS = KW / 32, NU = 3 * KS;  // units: (k step, weight plane)
+    // Weight units in flight: a ring of R (all of K = 512 at 32-column tiles,
+    // four units of the 64-column tiles, six of the streamed K = 2048).
+    constexpr int R0 = NT == 4 ? 4 : 6, R = R0 < NU ? R0 : NU;
+    const __bf16* w3 = reinterpret_cast<const __bf16*>(wp);
+    const long PL = (long)N * K;  // elements per plane
+    // B fragment of k step st, tile j, plane pl: W rows n0 + 16 j + li, k = kw0 + 32 st + 8 g .. + 7,
+    // i.e. k16-tile kw0 / 16 + 2 st + g / 2 at offset 8 (g & 1).
+    const __bf16* wb3 = w3 + ((long)((kw0 >> 4) + (g >> 1)) * N + n0 + li) * 16 + 8 * (g & 1);
+    const float* xs3 = x + min(m0 + li, (long)rows - 1) * K + kw0 + 8 * g;
+    bf16x8 bu[R][NT];
+    floatx4 a3[2][2];
+    auto load_unit = [&](int buf, int u) {
+      const int st = u / 3, pl = u % 3;
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        bu[buf][j] = *reinterpret_cast<const bf16x8*>(wb3 + pl * PL + (long)st * 2 * N * 16 + j * 256);
+    };
+    auto load_a3 = [&](int buf, int st) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        a3[buf][h] = STAGE ? *reinterpret_cast<const floatx4*>(As + li * PA + kw0 + 32 * st + 8 * g + 4 * h)
+                           : *reinterpret_cast<const floatx4*>(xs3 + 32 * st + 4 * h);
+    };
+    auto load_ring = [&]() {
+#pragma unroll
+      for (int u = 0; u + 1 < R; ++u) load_unit(u, u);
+    };
+    if (!STAGE) load_ring();
+    if (STAGE) {
+      stage_rows();
+      load_ring();
+      __syncthreads();
+    }
+    load_a3(0, 0);
+    fetch_epilogue();
+    __builtin_amdgcn_sched_barrier(0);
+    bf16x8 p0, p1, p2;
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int st = u / 3, pl = u % 3, c = u % R;
+      if (u + R - 1 < NU) load_unit((u + R - 1) % R, u + R - 1);
+      if (pl == 0) {
+        if (st + 1 < KS) load_a3((st + 1) & 1, st + 1);
+        bf16x4 l0, l1, l2, h0, h1, h2;
+        split3(a3[st & 1][0], l0, l1, l2);
+        split3(a3[st & 1][1], h0, h1, h2);
+        p0 = __builtin_shufflevector(l0, h0, 0, 1, 2, 3, 4, 5, 6, 7);
+        p1 = __builtin_shufflevector(l1, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+        p2 = __builtin_shufflevector(l2, h2, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // Plane 0 of W meets all three A pieces, plane 1 the first two, plane 2
+      // the first (the six terms of order <= 2); tiles interleaved.
+      if (pl == 0) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[j] = fm_mfma16_bf16(p2, bu[c][j], acc[j]);
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[j] = fm_mfma16_bf16(p1, bu[c][j], acc[j]);
+      } else if (pl == 1) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[j] = fm_mfma16_bf16(p1, bu[c][j], acc[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < NT; ++j) acc[j] = fm_mfma16_bf16(p0, bu[c][j], acc[j]);
+    }
+    reduce_and_store(acc);
+    return;
+  }
+
+  const long tstride = (long)(K / 64) * 4 * 64 * 4;  // floats between 16-column tiles
+  const float* wb = wp + ((((long)(n0 / 16) * (K / 64) + kw0 / 64) * 4) * 64 + lane) * 4;
+  const float* xs = x + min(m0 + li, (long)rows - 1) * K + kw0 + 16 * g;
+  floatx4 a[2][4], b[2][NT][4];
+  auto load_b = [&](int buf, int piece) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        b[buf][j][t] = *reinterpret_cast<const floatx4*>(wb + j * tstride + piece * 1024 + t * 256);
+  };
+  auto load_a = [&](int buf, int piece) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      a[buf][t] = STAGE ? *reinterpret_cast<const floatx4*>(As + li * PA + kw0 + 64 * piece + 16 * g + 4 * t)
+                        : *reinterpret_cast<const floatx4*>(xs + 64 * piece + 4 * t);
+  };
+
+  // The input rows are the critical path (LayerNorm, then the A operand).
+  // With staging, the weight fragments are issued once the rows are in LDS:
+  // issued earlier they queue ahead of the LayerNorm parameters and the
+  // other waves' rows (measured 0.2-0.6 us faster per launch at 250 rows).
+  if (!STAGE) load_b(0, 0);
+  if (STAGE) {
+    stage_rows();
+    load_b(0, 0);
+    __syncthreads();
+  }
+  load_a(0, 0);
+  fetch_epilogue();
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int pc = 0; pc < NP; ++pc) {
     const int c = pc & 1;
@@ -1359,48 +1500,7 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
 #pragma unroll
         for (int j = 0; j < NT; ++j) acc[j] = fm_mfma16(a[c][t][e], b[c][j][t][e], acc[j]);
   }
-  if (STAGE) __syncthreads();  // all waves are done with As before it becomes `red`
-#pragma unroll
-  for (int j = 0; j < NT; ++j)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) red[(wave * BM + 4 * g + r) * PR + 16 * j + li] = acc[j][r];
-  __syncthreads();
-  // OPT consecutive outputs per thread, BN / OPT threads per row.
-  float out[OPT];
-#pragma unroll
-  for (int c = 0; c < OPT; ++c) {
-    float v = red[er * PR + ec + c];
-#pragma unroll
-    for (int q = 1; q < NWV; ++q) v = __fadd_rn(v, red[(q * BM + er) * PR + ec + c]);
-    out[c] = v;
-  }
-  if (rope) {
-    __syncthreads();
-#pragma unroll
-    for (int c = 0; c < OPT; ++c) red[er * PR + ec + c] = out[c];
-    __syncthreads();
-  }
-  if (m >= rows) return;
-#pragma unroll
-  for (int c = 0; c < OPT; ++c) {
-    float v = out[c];
-    if (rope) {
-      const int d = ec + c;
-      const float partner = red[er * PR + (d < 32 ? d + 32 : d - 32)];
-      const float rot = d < 32 ? -partner : partner;
-      v = __fadd_rn(__fmul_rn(v, e_cos[c]), __fmul_rn(rot, e_sin[c]));
-    }
-    if (flags & FM_EPI_GELU) v = fm_gelu(v);
-    if (res_scale) v = __fadd_rn(e_res[c], __fmul_rn(e_scale[c], v));
-    out[c] = v;
-  }
-  float* dst = y + m * N + n0 + ec;
-  if constexpr (OPT == 2) {
-    *reinterpret_cast<float2*>(dst) = float2{out[0], out[1]};
-  } else {
-#pragma unroll
-    for (int c = 0; c < OPT; ++c) dst[c] = out[c];
-  }
+  reduce_and_store(acc);
 }
 
 // Packs W^T [N][K] (row-major) into the fragment order of row16_linear_kernel.
@@ -1464,6 +1564,23 @@ int fm_row_linear(const float* x, int rows, int in_features, const float* ln_gam
   if ((flags & FM_EPI_RES_SCALE) && (!residual || !scale)) return FM_BAD_ARGUMENT;
   if (rope_cos && (!rope_sin || rope_cols % 64)) return FM_BAD_ARGUMENT;
   if (rows == 0) return FM_OK;
+  if (flags & FM_WEIGHTS_X6) {
+    // bf16x6 planes after W^T: 16-row blocks on the bf16 matrix cores.
+    if ((rows + 15) / 16 > 65535) return FM_UNSUPPORTED;
+    if (in_features == 2048 && (ln_gamma || rope_cos)) return FM_UNSUPPORTED;
+    const float* planes = weight + (long)out_features * in_features;
+    const dim3 g64(out_features / 64, (rows + 15) / 16), g32(out_features / 32, (rows + 15) / 16);
+    const bool wide = rope_cos || (long)(out_features / 32) * ((rows + 15) / 16) > 512;
+#define FM_R16X6(KK, BN, G)                                                                           \
+  hipLaunchKernelGGL((row16_linear_kernel<KK, BN, true>), G, dim3(512), 0, stream, x, rows, ln_gamma, \
+                     ln_beta, ln_eps, planes, out_features, flags, residual, scale, rope_cos,        \
+                     rope_sin, rope_cols, rows_per_seq, y)
+    if (in_features == 2048) FM_R16X6(2048, 32, g32);
+    else if (wide) FM_R16X6(512, 64, g64);
+    else FM_R16X6(512, 32, g32);
+#undef FM_R16X6
+    return (int)hipGetLastError();
+  }
   if ((rows + 31) / 32 > 65535) return FM_UNSUPPORTED;  // row blocks ride in grid y
   if (in_features == 2048) {  // streamed A operand: no LayerNorm / RoPE on this path
     if (ln_gamma || rope_cos) return FM_UNSUPPORTED;

@@ -281,8 +281,17 @@ class MimiRuntime:
         y = torch.empty((rows, n), device=self.device) if out is None else out
         g, b = (ln[0], ln[1]) if ln is not None else (None, None)
         cos, sin, rope_cols, per_seq = rope if rope is not None else (None, None, 0, 1)
-        packed = self._packed.get(w.data_ptr()) if rows <= _ROW16_MAX_ROWS else None
-        name, wp = ("fm_row_linear_packed", packed) if packed is not None else ("fm_row_linear", w)
+        few = rows <= _ROW16_MAX_ROWS
+        # bf16x6 where it measured faster: the 512-deep projections (qkv, o,
+        # fc1; the streamed 2048-deep fc2 stays on the FP32 tile).
+        wx = self._x6.get(w.data_ptr()) if few and k == 512 else None
+        packed = self._packed.get(w.data_ptr()) if few else None
+        if wx is not None:  # 16-row blocks on the bf16 matrix cores (bf16x6)
+            name, wp, flags = "fm_row_linear", wx, flags | nat.WEIGHTS_X6
+        elif packed is not None:
+            name, wp = "fm_row_linear_packed", packed
+        else:
+            name, wp = "fm_row_linear", w
         self._call(name, x, rows, k, g, b, self.config.norm_eps,
                    wp, n, flags, residual, scale, cos, sin,
                    rope_cols, per_seq, y)

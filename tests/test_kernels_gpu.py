@@ -556,7 +556,7 @@ def test_window_attention_prerotated(B, T):
     close(out.cpu(), attention_reference(qkv, B, T, H, D, window, cos, sin), rel=5e-5)
 
 
-PACKED = {"packed": True}
+PACKED = {"packed": True, "x6": False}
 
 
 def run_row_linear(x, w, flags=0, ln=None, rope=None, res=None, scale=None, out=None):
@@ -567,7 +567,9 @@ def run_row_linear(x, w, flags=0, ln=None, rope=None, res=None, scale=None, out=
     cos, sin, rope_cols, per_seq = rope if rope is not None else (None, None, 0, 1)
     p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     name, wp = "fm_row_linear", w
-    if PACKED["packed"]:
+    if PACKED["x6"]:
+        wp, flags = with_planes(w), flags | nat.WEIGHTS_X6
+    elif PACKED["packed"]:
         wp = torch.empty_like(w)
         nat.call("fm_pack_row_weights", w.data_ptr(), n, k, wp.data_ptr(), stream())
         name = "fm_row_linear_packed"
@@ -577,11 +579,13 @@ def run_row_linear(x, w, flags=0, ln=None, rope=None, res=None, scale=None, out=
     return y
 
 
-@pytest.fixture(params=["rowmajor", "packed"])
+@pytest.fixture(params=["rowmajor", "packed", "bf16x6"])
 def weight_layout(request):
     PACKED["packed"] = request.param == "packed"
+    PACKED["x6"] = request.param == "bf16x6"
     yield request.param
     PACKED["packed"] = False
+    PACKED["x6"] = False
 
 
 def test_pack_row_weights_layout():
