@@ -1566,16 +1566,28 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
                      p.C_in % 16 == 0 && p.K % 16 == 0;
   if (x6_ok && cfg.id >= 9 && cfg.id <= 15 && cfg.id != 12) {
     const long t128 = tile_count(M, p.N, kX6);
-    if (p.K >= 1024 && M >= 1024 && t128 >= 80 && t128 * splits < 480 && workspace) {
+    if (p.K >= 1024 && M >= 1024 && t128 < 360 && workspace) {
       // Long K over a few hundred tiles (the 2048-deep fc2 projection at
       // 2500-8000 rows, the 12-25 Hz convs): the bf16x6 tile split along K
-      // to >= 480 blocks (at most 4 splits of >= 256 k), 64x128 tiles when
-      // four splits of 128x128 stay below that.  Measured against the FP32
-      // pick: fc2 at 4000 rows 65 vs 77 us, at 2500 rows 50 vs 59 us.
-      cfg = t128 * 4 >= 480 ? kX6 : kX6Small;
+      // to >= 360 blocks, 128x128 with at most 4 splits, else 64x128 with
+      // at most 8 (>= 128 k per split).  Measured against the FP32 pick:
+      // fc2 at 4000 rows 65 vs 77 us, at 2500 rows 50 vs 59 us; dec.up6 at
+      // C2 61 vs 65 us.
+      auto fewest = [&](const TileCfg& t, int most) {
+        const long tc = tile_count(M, p.N, t);
+        int sp = 1;
+        while (sp < most && tc * sp < 360 && p.K / (2 * sp) >= 128) sp *= 2;
+        return sp;
+      };
+      const int s128 = fewest(kX6, 4);
+      if (t128 * s128 >= 360) {
+        cfg = kX6;
+        splits = s128;
+      } else {
+        cfg = kX6Small;
+        splits = fewest(kX6Small, 8);
+      }
       tiles = tile_count(M, p.N, cfg);
-      splits = 1;
-      while (splits < 4 && tiles * splits < 480 && p.K / (2 * splits) >= 256) splits *= 2;
     } else if (t128 * splits >= 192) {
       // 256x128 where it gives >= 384 tiles; unsplit grids of 192-383
       // 128x128 tiles take 64x128 (the 2500-row qkv / fc1 and 8000-row
