@@ -1395,7 +1395,9 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
     const __bf16* wb3 = w3 + ((long)((kw0 >> 4) + (g >> 1)) * N + n0 + li) * 16 + 8 * (g & 1);
     const float* xs3 = x + min(m0 + li, (long)rows - 1) * K + kw0 + 8 * g;
     bf16x8 bu[R][NT];
-    floatx4 a3[2][2];
+    // A steps in flight: one ahead from LDS, three ahead when streamed from global memory.
+    constexpr int RA0 = STAGE ? 2 : 4, RA = RA0 < KS ? RA0 : KS;
+    floatx4 a3[RA][2];
     auto load_unit = [&](int buf, int u) {
       const int st = u / 3, pl = u % 3;
 #pragma unroll
@@ -1418,7 +1420,9 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
       load_ring();
       __syncthreads();
     }
-    load_a3(0, 0);
+#pragma unroll
+    for (int st = 0; st + 1 < RA; ++st) load_a3(st, st);
+    if (RA == 1) load_a3(0, 0);
     fetch_epilogue();
     __builtin_amdgcn_sched_barrier(0);
     bf16x8 p0, p1, p2;
@@ -1427,10 +1431,10 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
       const int st = u / 3, pl = u % 3, c = u % R;
       if (u + R - 1 < NU) load_unit((u + R - 1) % R, u + R - 1);
       if (pl == 0) {
-        if (st + 1 < KS) load_a3((st + 1) & 1, st + 1);
+        if (RA > 1 && st + RA - 1 < KS) load_a3((st + RA - 1) % RA, st + RA - 1);
         bf16x4 l0, l1, l2, h0, h1, h2;
-        split3(a3[st & 1][0], l0, l1, l2);
-        split3(a3[st & 1][1], h0, h1, h2);
+        split3(a3[st % RA][0], l0, l1, l2);
+        split3(a3[st % RA][1], h0, h1, h2);
         p0 = __builtin_shufflevector(l0, h0, 0, 1, 2, 3, 4, 5, 6, 7);
         p1 = __builtin_shufflevector(l1, h1, 0, 1, 2, 3, 4, 5, 6, 7);
         p2 = __builtin_shufflevector(l2, h2, 0, 1, 2, 3, 4, 5, 6, 7);

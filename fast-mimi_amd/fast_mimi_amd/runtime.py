@@ -282,9 +282,11 @@ class MimiRuntime:
         g, b = (ln[0], ln[1]) if ln is not None else (None, None)
         cos, sin, rope_cols, per_seq = rope if rope is not None else (None, None, 0, 1)
         few = rows <= _ROW16_MAX_ROWS
-        # bf16x6 where it measured faster: the 512-deep projections (qkv, o,
-        # fc1; the streamed 2048-deep fc2 stays on the FP32 tile).
-        wx = self._x6.get(w.data_ptr()) if few and k == 512 else None
+        # bf16x6 where it measured faster at 250 rows: the wide 512-deep
+        # projections (qkv 7.5 vs 9.4 us, fc1 7.7 vs 9.6 us); the output
+        # projection (3.5 vs 3.4 us) and the streamed fc2 (8.1 vs 8.1 us)
+        # keep the FP32 fragment-packed kernel.
+        wx = self._x6.get(w.data_ptr()) if few and k == 512 and n >= 1024 else None
         packed = self._packed.get(w.data_ptr()) if few else None
         if wx is not None:  # 16-row blocks on the bf16 matrix cores (bf16x6)
             name, wp, flags = "fm_row_linear", wx, flags | nat.WEIGHTS_X6
