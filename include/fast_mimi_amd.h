@@ -139,6 +139,7 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
  * w0_packed is the conv's packed [64][7] weight.  The 64-channel conv output
  * is formed on chip and never stored.
  * Replaces MimiEncoder layers.0 + layers.1 (model.py:1013-1031).
+ * elu_out may carry FM_WEIGHTS_X6 as in fm_resblock (w1/w2 with planes).
  */
 int fm_conv_resblock64(const float* wav, int batch, int length, const float* w0_packed,
                        const float* b0, const float* w1_packed, const float* b1,
@@ -156,6 +157,7 @@ int fm_conv_resblock64(const float* wav, int batch, int length, const float* w0_
  * Replaces MimiDecoder's last MimiResnetBlock + ELU + MimiConv1d
  * (model.py:1269-1285).
  */
+/* elu_mid may carry FM_WEIGHTS_X6 as in fm_resblock (w1/w2 with planes). */
 size_t fm_resblock64_conv_workspace_bytes(int batch, int length);
 int fm_resblock64_conv(const float* x, int batch, int length, const float* w1_packed,
                        const float* b1, const float* w2_packed, const float* b2, int elu_mid,
@@ -170,7 +172,9 @@ int fm_resblock64_conv(const float* x, int batch, int length, const float* w1_pa
  *     rope_cols (a multiple of 64) get RoPE per 64-wide head, position
  *     row % rows_per_seq;
  *   - flags: FM_EPI_GELU, or FM_EPI_RES_SCALE (y = residual + scale[n] * acc,
- *     y may alias residual).
+ *     y may alias residual); with FM_WEIGHTS_X6 the weight is followed by its
+ *     fm_split_weights planes and 16-row blocks run the contraction on the
+ *     bf16 matrix cores (bf16x6, FP32-accurate).
  * Supported shapes: fm_row_linear_supported(in, out) != 0 (in 512 or 2048,
  * out a multiple of 64; LayerNorm and RoPE only with in == 512).  Replaces the LayerNorm + q/k/v projection + _apply_rope
  * and LayerNorm + fc1 + GELU sequences of MimiTransformerLayer
