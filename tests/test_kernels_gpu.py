@@ -44,6 +44,19 @@ def close(got, want, rel=2e-5):
     assert err <= rel * scale, f"max err {err:.3e} vs scale {scale:.3e}"
 
 
+def close_dot(got, want, absref, rel=1e-5):
+    """Per-element FP32 accumulation bound: |got - want| <= rel * sum_k |a_k b_k|
+    (absref, the same contraction on absolute values in float64), so
+    small-magnitude outputs are held as tightly as large ones."""
+    got = got.double().cpu()
+    want = want.double().cpu()
+    absref = absref.double().cpu()
+    err = (got - want).abs()
+    bound = rel * absref + 1e-30
+    worst = (err / bound).max().item()
+    assert worst <= 1.0, f"error {worst:.2f}x the per-element bound (rel {rel:.0e} of sum |a b|)"
+
+
 def with_planes(w):
     """A packed weight W^T [N, K] followed by its bf16x6 planes
     (fm_split_weights, k16-tile order [3][K/16][N][16]), as the runtime
@@ -143,6 +156,7 @@ def test_conv1d(B, cin, cout, k, stride, L, ws):
     want = causal_conv1d(x.double(), w.double(), b.double(), stride)
     assert got.shape == want.shape
     close(got, want)
+    close_dot(got, want, causal_conv1d(x.double().abs(), w.double().abs(), b.double().abs(), stride))
 
 
 # Direct-load tiles (C_in a multiple of 16, zero padding, no ELU on load):
@@ -176,6 +190,9 @@ def test_conv1d_direct_load_tiles(B, cin, cout, k, stride, L, y_len, epi, x6, ws
     want = causal_conv1d(x.double(), w.double(), b.double(), stride)
     if epi == "plain":
         got = run_conv(x, w, b, stride, "constant", 0, ws, y_len=y_len, x6=x6)
+        absref = causal_conv1d(x.double().abs(), w.double().abs(), b.double().abs(), stride)
+        absref = absref[..., :y_len] if y_len is not None else absref
+        close_dot(got, want[..., :y_len] if y_len is not None else want, absref)
     else:
         res = torch.randn(B, cout, rows, generator=g)
         got = run_conv(x, w, b, stride, "constant", nat.EPI_RES_ADD | nat.EPI_ELU, ws,
@@ -422,6 +439,8 @@ def test_conv_transpose1d(B, cin, cout, stride, L, x6, ws):
     torch.cuda.synchronize()
     want = causal_conv_transpose1d(x.double(), w.double(), b.double(), stride)
     close(y.cpu().transpose(1, 2), want)
+    close_dot(y.cpu().transpose(1, 2), want,
+              causal_conv_transpose1d(x.double().abs(), w.double().abs(), b.double().abs(), stride))
 
 
 def run_linear(x, w, flags=0, res=None, scale=None, ws=None, out=None):
@@ -452,6 +471,8 @@ def test_linear_epilogues(rows, k, n, x6, ws):
     if x6:
         wd, f = with_planes(wd), nat.WEIGHTS_X6
     close(run_linear(xd, wd, f, ws=ws).cpu(), x.double() @ w.double().t())
+    close_dot(run_linear(xd, wd, f, ws=ws).cpu(), x.double() @ w.double().t(),
+              x.double().abs() @ w.double().abs().t())
     close(run_linear(xd, wd, nat.EPI_GELU | f, ws=ws).cpu(), F.gelu(x.double() @ w.double().t()))
     res = torch.randn(rows, n, generator=g)
     scale = torch.rand(n, generator=g) * 0.1
@@ -621,6 +642,8 @@ def test_row_linear(rows, weight_layout):
     xn = F.layer_norm(x.double(), (k,), gamma.double(), beta.double(), 1e-5)
     # Plain product and LN + product.
     close(run_row_linear(d["x"], d["wo"]).cpu(), x.double() @ wo.double().t())
+    close_dot(run_row_linear(d["x"], d["wo"]).cpu(), x.double() @ wo.double().t(),
+              x.double().abs() @ wo.double().abs().t())
     # LN + qkv + RoPE on q and k (positions row % T).
     got = run_row_linear(d["x"], d["wqkv"], ln=(d["gamma"], d["beta"]),
                          rope=(d["cos"], d["sin"], 2 * k, T)).cpu()
@@ -650,6 +673,7 @@ def test_row_linear_long_k(rows, weight_layout):
     xd, wd = x.to(DEV), w.to(DEV)
     want = x.double() @ w.double().t()
     close(run_row_linear(xd, wd).cpu(), want)
+    close_dot(run_row_linear(xd, wd).cpu(), want, x.double().abs() @ w.double().abs().t())
     close(run_row_linear(xd, wd, nat.EPI_GELU).cpu(), F.gelu(want))
     res = torch.randn(rows, 512, generator=g)
     scale = torch.rand(512, generator=g) * 0.1
