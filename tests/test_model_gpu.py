@@ -165,6 +165,18 @@ def test_full_batch_padded_32_codebooks(full, golden):
     assert_audio(out.audio_values.cpu()[..., ::10], torch.from_numpy(golden["full_b2_values_dec10"]))
 
 
+@pytest.mark.parametrize("B,S,nq", [(3, 32_881, 5), (1, 1_921, 8), (2, 80_003, 12)])
+def test_full_config_odd_lengths_and_batches(full, B, S, nq):
+    """Lengths that are not multiples of the 1920-sample frame, odd batches and
+    codebook counts, against the oracle (bit-exact codes expected; certified
+    near-ties allowed and recorded)."""
+    model, oracle = full
+    audio, mask = synthetic.batch(B, S)
+    check_against_oracle(model, oracle, torch.from_numpy(audio), torch.from_numpy(mask), nq,
+                         f"odd_b{B}_s{S}_nq{nq}", allow=(2, 1e-6))
+    model.release_graphs()
+
+
 @pytest.mark.parametrize("name", ["c1", "c2"])
 def test_benchmark_configs_match_reference(full, golden, name):
     model, oracle = full
