@@ -988,3 +988,44 @@ def test_split_k_is_deterministic(ws):
     second = run_linear(x, w, ws=ws)
     assert torch.equal(first, second)
     close(first.cpu(), x.double().cpu() @ w.double().cpu().t())
+
+
+@pytest.mark.parametrize("rows,k,n,x6", [
+    (250, 8192, 512, False),    # 64x64 16x16-MFMA tiles split along K
+    (125, 4096, 512, False),    # 32x32 tiles, K split inside the block and across blocks
+    (12000, 1280, 256, True),   # 128x128 bf16x6 tiles split along K
+    (2500, 2048, 512, True),    # 64x128 bf16x6 tiles split along K
+])
+def test_split_k_repeats_and_graph_replays(rows, k, n, x6, ws):
+    """K-split GEMMs (partials in the shared workspace, summed in split order):
+    back-to-back calls, calls of another split shape in between and hipGraph
+    replays all give the same bits, and the LayerScale residual epilogue is
+    applied once to the ordered sum."""
+    g = torch.Generator().manual_seed(rows + k + n)
+    x = torch.randn(rows, k, generator=g)
+    w = torch.randn(n, k, generator=g) / math.sqrt(k)
+    res = torch.randn(rows, n, generator=g)
+    scale = torch.rand(n, generator=g) + 0.5
+    xd, wd, rd, sd = x.to(DEV), w.to(DEV), res.to(DEV), scale.to(DEV)
+    f = nat.EPI_RES_SCALE
+    if x6:
+        wd, f = with_planes(wd), f | nat.WEIGHTS_X6
+    first = run_linear(xd, wd, f, res=rd, scale=sd, ws=ws).clone()
+    prod = x.double() @ w.double().t()
+    close(first.cpu(), res.double() + scale.double() * prod)
+    other_x = torch.randn(250, 8192, generator=g).to(DEV)
+    other_w = (torch.randn(512, 8192, generator=g) * 0.01).to(DEV)
+    for _ in range(3):
+        assert torch.equal(run_linear(xd, wd, f, res=rd, scale=sd, ws=ws), first)
+        run_linear(other_x, other_w, ws=ws)
+    out = torch.empty_like(first)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        nat.call("fm_linear", xd.data_ptr(), rows, k, wd.data_ptr(), n, f, rd.data_ptr(),
+                 sd.data_ptr(), out.data_ptr(), ws.data_ptr(), WS_BYTES, stream())
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, first)
+        run_linear(other_x, other_w, ws=ws)
