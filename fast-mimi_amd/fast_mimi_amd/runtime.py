@@ -41,6 +41,9 @@ _WORKSPACE_BYTES = 64 << 20
 _ROW_LINEAR_MAX_ROWS = 1024
 # Up to this many rows the 16-row kernels on fragment-packed weights are used.
 _ROW16_MAX_ROWS = 512
+# Few-row long-K convolutions (fm_conv1d_rows) up to this many output rows;
+# beyond it the tiled GEMM engine has enough tiles.
+_ROWCONV_MAX_ROWS = 512
 
 
 class _Conv:
@@ -54,6 +57,7 @@ class _Conv:
         self.w = weight.permute(0, 2, 1).reshape(c_out, k * c_in).contiguous()
         self.b = None if bias is None else bias.contiguous()
         self.flags = 0  # nat.WEIGHTS_X6 once the runtime appends the bf16 planes
+        self.wr = None  # fragment-packed W^T for fm_conv1d_rows, where that kernel applies
 
 
 class _ConvT:
@@ -189,6 +193,10 @@ class MimiRuntime:
                 layer.w, layer.flags = w, nat.WEIGHTS_X6
         for w in [m for lay in self.enc_tf + self.dec_tf for m in (lay.wqkv, lay.wo, lay.w1, lay.w2)]:
             self._x6[w.data_ptr()] = self._with_planes(w)
+        for layer in [self.enc_last, self.dec_first] + ([self.down] if self.bottleneck else []):
+            if lib.fm_conv1d_rows_supported(layer.c_in, layer.c_out, layer.k):
+                layer.wr = torch.empty_like(layer.w)
+                ops.call("fm_pack_row_weights", layer.w, layer.c_out, layer.k * layer.c_in, layer.wr)
         self.workspace = torch.empty(_WORKSPACE_BYTES // 4, device=device)
         self._rope: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
         # Optional per-op timing: a list of (tag, start_event, end_event).
@@ -245,6 +253,11 @@ class MimiRuntime:
         rows = -(-L // layer.stride)
         y_len = rows if y_len is None else y_len
         y = torch.empty((B, y_len, layer.c_out), device=self.device)
+        if (layer.wr is not None and residual is None and y_len == rows and B * rows <= _ROWCONV_MAX_ROWS
+                and not flags & ~(nat.ELU_IN | nat.EPI_ELU)):
+            self._call("fm_conv1d_rows", x, B, L, layer.c_in, layer.wr, layer.b, layer.c_out,
+                       layer.k, layer.stride, layer.replicate, flags, y)
+            return y, rows
         self._call("fm_conv1d", x, B, L, layer.c_in, layer.w, layer.b,
                  layer.c_out, layer.k, layer.stride, layer.replicate, flags | layer.flags, residual,
                  y, y_len, self.workspace, _WORKSPACE_BYTES)

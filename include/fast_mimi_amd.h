@@ -82,6 +82,25 @@ int fm_conv1d(const float* x, int batch, int length, int in_channels, const floa
               size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * fm_conv1d for few output rows and long K (the 12.5-25 Hz end of the SEANet
+ * stacks at batch x rows <= a few hundred): same padding, output length and
+ * arithmetic contract, but every 16 output rows x 32 columns is one block
+ * whose 8 waves split K, so there is no K-split partial buffer and no second
+ * launch.  weight_rowpacked is the conv's W^T [out_channels][kernel *
+ * in_channels] in fm_pack_row_weights order.  flags: FM_ELU_IN and/or
+ * FM_EPI_ELU; y is [batch][ceil(length / stride)][out_channels].
+ * Shapes: fm_conv1d_rows_supported(in, out, kernel) != 0 (in_channels a
+ * multiple of 64, out_channels of 32, in_channels * kernel 2048, 3072 or
+ * 3584), else FM_UNSUPPORTED.  Replaces MimiConv1d.forward (model.py:697-797)
+ * for the encoder's last conv, the replicate-padded downsample
+ * (model.py:2730-2741) and the decoder's first conv.
+ */
+int fm_conv1d_rows_supported(int in_channels, int out_channels, int kernel);
+int fm_conv1d_rows(const float* x, int batch, int length, int in_channels,
+                   const float* weight_rowpacked, const float* bias, int out_channels, int kernel,
+                   int stride, int pad_mode, int flags, float* y, hipStream_t stream);
+
+/*
  * Conv1d over exactly the given rows, no padding: output row t reads input
  * rows t*stride .. t*stride + kernel - 1; y is [batch][(length - kernel) /
  * stride + 1][out_channels].  Streaming convolution: the caller prepends the

@@ -242,6 +242,65 @@ def test_conv1d_replicate(B, L, ws):
     close(got, want)
 
 
+# Few-row long-K convolutions (fm_conv1d_rows): the encoder's last conv
+# (1024 -> 512 k3), the replicate-padded downsample (512 -> 512 k4 s2, odd
+# and even lengths) and the decoder's first conv (512 -> 1024 k7), with batch
+# seams and partial 16-row blocks; same float64 bars as fm_conv1d, and the
+# same result as fm_conv1d to FP32 accumulation error.
+ROWCONV_CASES = [
+    # B, Cin, Cout, k, stride, L, pad_mode, flags
+    (1, 1024, 512, 3, 1, 250, "constant", 0),
+    (1, 1024, 512, 3, 1, 250, "constant", nat.ELU_IN | nat.EPI_ELU),
+    (1, 512, 512, 4, 2, 250, "replicate", 0),
+    (2, 512, 512, 4, 2, 63, "replicate", 0),
+    (3, 512, 512, 4, 2, 1, "replicate", 0),
+    (1, 512, 1024, 7, 1, 250, "constant", nat.EPI_ELU),
+    (2, 512, 1024, 7, 1, 37, "constant", 0),
+]
+
+
+@pytest.mark.parametrize("B,cin,cout,k,stride,L,pad_mode,flags", ROWCONV_CASES)
+def test_conv1d_rows(B, cin, cout, k, stride, L, pad_mode, flags, ws):
+    lib = nat.library()
+    assert lib.fm_conv1d_rows_supported(cin, cout, k)
+    g = torch.Generator().manual_seed(B * 7 + cin + cout + k + L)
+    x = torch.randn(B, cin, L, generator=g)
+    w = torch.randn(cout, cin, k, generator=g) / math.sqrt(cin * k)
+    b = torch.randn(cout, generator=g) * 0.1 if pad_mode == "constant" else None
+    layer = _Conv(w.to(DEV), None if b is None else b.to(DEV), stride, pad_mode)
+    wr = torch.empty_like(layer.w)
+    nat.call("fm_pack_row_weights", layer.w.data_ptr(), cout, k * cin, wr.data_ptr(), stream())
+    xd = x.transpose(1, 2).contiguous().to(DEV)
+    rows = -(-L // stride)
+    y = torch.full((B, rows, cout), float("nan"), device=DEV)
+    nat.call("fm_conv1d_rows", xd.data_ptr(), B, L, cin, wr.data_ptr(),
+             None if layer.b is None else layer.b.data_ptr(), cout, k, stride, layer.replicate, flags,
+             y.data_ptr(), stream())
+    torch.cuda.synchronize()
+    got = y.cpu().transpose(1, 2)
+    xi = F.elu(x.double()) if flags & nat.ELU_IN else x.double()
+    bd = None if b is None else b.double()
+    want = causal_conv1d(xi, w.double(), bd, stride, pad_mode=pad_mode)
+    absref = causal_conv1d(xi.abs(), w.double().abs(), None if bd is None else bd.abs(), stride,
+                           pad_mode=pad_mode)
+    if flags & nat.EPI_ELU:
+        want = F.elu(want)
+    else:
+        close_dot(got, want, absref)
+    close(got, want)
+    same = run_conv(x, w, b, stride, pad_mode, flags, ws)
+    close(got, same.double())
+
+
+def test_conv1d_rows_rejects():
+    with pytest.raises(nat.NativeError, match="unsupported"):
+        nat.call("fm_conv1d_rows", 1, 1, 4, 64, 1, None, 32, 3, 1, 0, 0, 1, stream())  # K = 192
+    with pytest.raises(nat.NativeError, match="unsupported"):
+        nat.call("fm_conv1d_rows", 1, 1, 4, 512, 1, None, 512, 4, 2, 0, nat.EPI_GELU, 1, stream())
+    with pytest.raises(nat.NativeError, match="bad argument"):
+        nat.call("fm_conv1d_rows", 1, 1, 4, 512, 1, None, 512, 4, 2, 2, 0, 1, stream())
+
+
 def test_conv1d_fused_resblock_epilogues(ws):
     """ELU-on-load + k3 conv + ELU, then 1x1 conv + residual add + ELU."""
     g = torch.Generator().manual_seed(3)
