@@ -29,10 +29,10 @@ struct RowConvArgs {
   const float* w;    // fragment-packed W^T [N][K]
   const float* bias; // [N] or null
   float* y;          // [batch][rows_per_batch][N]
-  int L, c_in, stride, pad_l, replicate, rows_per_batch, rows, N, flags;
+  int L, c_in, stride, pad_l, replicate, rows_per_batch, rows, N, bias_len, flags;
 };
 
-template <int K, int BN>
+template <int K, int BN, bool X6>
 __global__ __launch_bounds__(512) void row16_conv_kernel(RowConvArgs p) {
   constexpr int NWV = 8, BM = 16, KW = K / NWV, NP = KW / 64, NT = BN / 16;
   constexpr int PR = BN + 4, OPT = BM * BN / 512;
@@ -51,18 +51,93 @@ __global__ __launch_bounds__(512) void row16_conv_kernel(RowConvArgs p) {
   const int b = (int)(mr / p.rows_per_batch);
   const int t = (int)(mr - (long)b * p.rows_per_batch);
   const int p0 = t * p.stride - p.pad_l;
-  const float* xb = p.x + (long)b * p.L * p.c_in + 16 * g;
-  auto a_src = [&](int piece) -> const float* {
-    const int k = kw0 + 64 * piece;  // wave-uniform
+  const float* xb = p.x + (long)b * p.L * p.c_in;
+  // Input run of this lane for the k-range starting at k (wave-uniform; the
+  // range lies inside one tap).
+  auto a_src = [&](int k, int lane_off) -> const float* {
     const int tap = k / p.c_in;
     int pos = p0 + tap;
     if (p.replicate) pos = min(max(pos, 0), p.L - 1);
     else if ((unsigned)pos >= (unsigned)p.L) return g_zero_row;
-    return xb + (long)pos * p.c_in + (k - tap * p.c_in);
+    return xb + (long)pos * p.c_in + (k - tap * p.c_in) + lane_off;
   };
+  const bool elu_in = p.flags & FM_ELU_IN;
+  floatx4 acc[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) acc[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  if constexpr (X6) {
+    // bf16x6: W^T's planes [3][K/16][N][16] after the FP32 weight; 32-deep k
+    // steps on v_mfma_f32_16x16x32_bf16, lane group g covering k = 8g .. 8g+7
+    // of A and B.  Units (step, plane) stream through a ring of R weight
+    // fragments; A runs RA - 1 steps ahead and is split as it is used.  The
+    // unit loop is unrolled by CHU units so every ring index is static.
+    constexpr int KS = KW / 32, NU = 3 * KS, R = 6, RA = KS % 4 == 0 ? 4 : 2, CHU = 3 * RA;
+    static_assert(KW % 32 == 0 && KS % RA == 0 && CHU % R == 0, "whole 32-deep steps per wave");
+    const __bf16* w3 = reinterpret_cast<const __bf16*>(p.w + (long)p.N * K);
+    const long PL = (long)p.N * K;
+    const __bf16* wb3 = w3 + ((long)((kw0 >> 4) + (g >> 1)) * p.N + n0 + li) * 16 + 8 * (g & 1);
+    bf16x8 bu[R][NT];
+    floatx4 a3[RA][2];
+    auto load_unit = [&](int buf, int u) {
+      if (u >= NU) return;
+      const int st = u / 3, pl = u - 3 * st;
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        bu[buf][j] = *reinterpret_cast<const bf16x8*>(wb3 + pl * PL + (long)st * 2 * p.N * 16 + j * 256);
+    };
+    auto load_a3 = [&](int buf, int st) {
+      if (st >= KS) return;
+      const float* src = a_src(kw0 + 32 * st, 8 * g);
+      a3[buf][0] = *reinterpret_cast<const floatx4*>(src);
+      a3[buf][1] = *reinterpret_cast<const floatx4*>(src + 4);
+    };
+#pragma unroll
+    for (int u = 0; u + 1 < R; ++u) load_unit(u, u);
+#pragma unroll
+    for (int st = 0; st + 1 < RA; ++st) load_a3(st, st);
+    __builtin_amdgcn_sched_barrier(0);
+    bf16x8 p0v, p1v, p2v;
+    for (int u0 = 0; u0 < NU; u0 += CHU) {
+#pragma unroll
+      for (int i = 0; i < CHU; ++i) {
+        const int u = u0 + i;
+        const int pl = i % 3, c = i % R;
+        load_unit((i + R - 1) % R, u + R - 1);
+        if (pl == 0) {
+          const int sa = i / 3;  // u0 / 3 is a multiple of RA
+          load_a3((sa + RA - 1) % RA, u / 3 + RA - 1);
+          floatx4 v0 = a3[sa % RA][0], v1 = a3[sa % RA][1];
+          if (elu_in) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v0[e] = fm_elu(v0[e]), v1[e] = fm_elu(v1[e]);
+          }
+          bf16x4 l0, l1, l2, h0, h1, h2;
+          split3(v0, l0, l1, l2);
+          split3(v1, h0, h1, h2);
+          p0v = __builtin_shufflevector(l0, h0, 0, 1, 2, 3, 4, 5, 6, 7);
+          p1v = __builtin_shufflevector(l1, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+          p2v = __builtin_shufflevector(l2, h2, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // Plane 0 of W meets all three A pieces, plane 1 the first two,
+        // plane 2 the first: the six terms of order <= 2.
+        if (pl == 0) {
+#pragma unroll
+          for (int j = 0; j < NT; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(p2v, bu[c][j], acc[j], 0, 0, 0);
+#pragma unroll
+          for (int j = 0; j < NT; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(p1v, bu[c][j], acc[j], 0, 0, 0);
+        } else if (pl == 1) {
+#pragma unroll
+          for (int j = 0; j < NT; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(p1v, bu[c][j], acc[j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(p0v, bu[c][j], acc[j], 0, 0, 0);
+      }
+    }
+  } else {
   const long tstride = (long)(K / 64) * 4 * 64 * 4;  // floats between 16-column tiles
   const float* wb = p.w + ((((long)(n0 / 16) * (K / 64) + kw0 / 64) * 4) * 64 + lane) * 4;
-  const bool elu_in = p.flags & FM_ELU_IN;
   floatx4 a[2][4], bw[2][NT][4];
   auto load = [&](int buf, int piece) {
 #pragma unroll
@@ -70,14 +145,10 @@ __global__ __launch_bounds__(512) void row16_conv_kernel(RowConvArgs p) {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         bw[buf][j][q] = *reinterpret_cast<const floatx4*>(wb + j * tstride + piece * 1024 + q * 256);
-    const float* src = a_src(piece);
+    const float* src = a_src(kw0 + 64 * piece, 16 * g);
 #pragma unroll
     for (int q = 0; q < 4; ++q) a[buf][q] = *reinterpret_cast<const floatx4*>(src + 4 * q);
   };
-
-  floatx4 acc[NT];
-#pragma unroll
-  for (int j = 0; j < NT; ++j) acc[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   load(0, 0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -99,6 +170,7 @@ __global__ __launch_bounds__(512) void row16_conv_kernel(RowConvArgs p) {
         for (int j = 0; j < NT; ++j)
           acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c][q][e], bw[c][j][q][e], acc[j], 0, 0, 0);
   }
+  }
 
   // The 8 partial tiles summed in wave order, then bias and the output ELU.
 #pragma unroll
@@ -115,7 +187,7 @@ __global__ __launch_bounds__(512) void row16_conv_kernel(RowConvArgs p) {
     float v = red[er * PR + ec + c];
 #pragma unroll
     for (int q = 1; q < NWV; ++q) v = __fadd_rn(v, red[(q * BM + er) * PR + ec + c]);
-    if (p.bias) v = __fadd_rn(v, p.bias[n0 + ec + c]);
+    if (p.bias) v = __fadd_rn(v, p.bias[(n0 + ec + c) % p.bias_len]);
     if (p.flags & FM_EPI_ELU) v = fm_elu(v);
     out[c] = v;
   }
@@ -128,31 +200,40 @@ __global__ __launch_bounds__(512) void row16_conv_kernel(RowConvArgs p) {
 
 extern "C" {
 
-int fm_conv1d_rows_supported(int in_channels, int out_channels, int kernel) {
+int fm_conv1d_rows_supported(int in_channels, int out_channels, int kernel, int flags) {
   const int K = in_channels * kernel;
-  return in_channels % 64 == 0 && out_channels % 32 == 0 && (K == 2048 || K == 3072 || K == 3584);
+  if (out_channels % 32) return 0;
+  return in_channels % (flags & FM_WEIGHTS_X6 ? 32 : 64) == 0 && (K == 2048 || K == 3072 || K == 3584);
 }
 
-int fm_conv1d_rows(const float* x, int batch, int length, int in_channels,
-                   const float* weight_rowpacked, const float* bias, int out_channels, int kernel,
-                   int stride, int pad_mode, int flags, float* y, hipStream_t stream) {
-  if (!x || !weight_rowpacked || !y || batch < 0 || length < 0 || kernel <= 0 || stride <= 0 ||
-      kernel < stride || (pad_mode != 0 && pad_mode != 1))
+int fm_conv1d_rows(const float* x, int batch, int length, int in_channels, const float* weight,
+                   const float* bias, int bias_len, int out_channels, int kernel, int stride,
+                   int pad_mode, int flags, float* y, hipStream_t stream) {
+  if (!x || !weight || !y || batch < 0 || length < 0 || kernel <= 0 || stride <= 0 ||
+      kernel < stride || (pad_mode != 0 && pad_mode != 1) || (bias && bias_len <= 0))
     return FM_BAD_ARGUMENT;
-  if (flags & ~(FM_ELU_IN | FM_EPI_ELU)) return FM_UNSUPPORTED;
-  if (!fm_conv1d_rows_supported(in_channels, out_channels, kernel)) return FM_UNSUPPORTED;
+  if (flags & ~(FM_ELU_IN | FM_EPI_ELU | FM_WEIGHTS_X6)) return FM_UNSUPPORTED;
+  if (!fm_conv1d_rows_supported(in_channels, out_channels, kernel, flags)) return FM_UNSUPPORTED;
   const int rows_per_batch = (length + stride - 1) / stride;
   const long rows = (long)batch * rows_per_batch;
   if (rows == 0) return FM_OK;
   if (length == 0) return FM_BAD_ARGUMENT;
   if ((rows + 15) / 16 > 65535) return FM_UNSUPPORTED;
-  RowConvArgs p{x, weight_rowpacked, bias, y, length, in_channels, stride, kernel - stride, pad_mode,
-                rows_per_batch, (int)rows, out_channels, flags};
+  RowConvArgs p{x, weight, bias, y, length, in_channels, stride, kernel - stride, pad_mode,
+                rows_per_batch, (int)rows, out_channels, bias ? bias_len : 1, flags};
   const dim3 grid(out_channels / 32, (unsigned)((rows + 15) / 16));
   const int K = in_channels * kernel;
-  if (K == 2048) hipLaunchKernelGGL((row16_conv_kernel<2048, 32>), grid, dim3(512), 0, stream, p);
-  else if (K == 3072) hipLaunchKernelGGL((row16_conv_kernel<3072, 32>), grid, dim3(512), 0, stream, p);
-  else hipLaunchKernelGGL((row16_conv_kernel<3584, 32>), grid, dim3(512), 0, stream, p);
+#define FM_ROWCONV(KK, X6) hipLaunchKernelGGL((row16_conv_kernel<KK, 32, X6>), grid, dim3(512), 0, stream, p)
+  if (flags & FM_WEIGHTS_X6) {
+    if (K == 2048) FM_ROWCONV(2048, true);
+    else if (K == 3072) FM_ROWCONV(3072, true);
+    else FM_ROWCONV(3584, true);
+  } else {
+    if (K == 2048) FM_ROWCONV(2048, false);
+    else if (K == 3072) FM_ROWCONV(3072, false);
+    else FM_ROWCONV(3584, false);
+  }
+#undef FM_ROWCONV
   return (int)hipGetLastError();
 }
 

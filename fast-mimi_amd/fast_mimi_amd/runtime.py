@@ -193,8 +193,16 @@ class MimiRuntime:
                 layer.w, layer.flags = w, nat.WEIGHTS_X6
         for w in [m for lay in self.enc_tf + self.dec_tf for m in (lay.wqkv, lay.wo, lay.w1, lay.w2)]:
             self._x6[w.data_ptr()] = self._with_planes(w)
-        for layer in [self.enc_last, self.dec_first] + ([self.down] if self.bottleneck else []):
-            if lib.fm_conv1d_rows_supported(layer.c_in, layer.c_out, layer.k):
+        # Few-row long-K convolutions (fm_conv1d_rows; the encoder's last conv,
+        # the downsample and the decoder's first conv at a few hundred rows:
+        # 12.6 / 8.4 / 25.1 us against 21.1 / 12.2 / 27.9 us for the split
+        # GEMM at C2, warm): on the bf16x6 planes where the layer has them,
+        # else on fragment-packed FP32 weights.
+        for layer in self._conv_layers():
+            if layer.flags & nat.WEIGHTS_X6 and lib.fm_conv1d_rows_supported(
+                    layer.c_in, layer.c_out, layer.k, nat.WEIGHTS_X6):
+                layer.wr = layer.w
+            elif lib.fm_conv1d_rows_supported(layer.c_in, layer.c_out, layer.k, 0):
                 layer.wr = torch.empty_like(layer.w)
                 ops.call("fm_pack_row_weights", layer.w, layer.c_out, layer.k * layer.c_in, layer.wr)
         self.workspace = torch.empty(_WORKSPACE_BYTES // 4, device=device)
@@ -256,7 +264,8 @@ class MimiRuntime:
         if (layer.wr is not None and residual is None and y_len == rows and B * rows <= _ROWCONV_MAX_ROWS
                 and not flags & ~(nat.ELU_IN | nat.EPI_ELU)):
             self._call("fm_conv1d_rows", x, B, L, layer.c_in, layer.wr, layer.b, layer.c_out,
-                       layer.k, layer.stride, layer.replicate, flags, y)
+                       layer.c_out, layer.k, layer.stride, layer.replicate,
+                       flags | (layer.flags if layer.wr is layer.w else 0), y)
             return y, rows
         self._call("fm_conv1d", x, B, L, layer.c_in, layer.w, layer.b,
                  layer.c_out, layer.k, layer.stride, layer.replicate, flags | layer.flags, residual,

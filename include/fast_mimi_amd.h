@@ -86,19 +86,25 @@ int fm_conv1d(const float* x, int batch, int length, int in_channels, const floa
  * stacks at batch x rows <= a few hundred): same padding, output length and
  * arithmetic contract, but every 16 output rows x 32 columns is one block
  * whose 8 waves split K, so there is no K-split partial buffer and no second
- * launch.  weight_rowpacked is the conv's W^T [out_channels][kernel *
- * in_channels] in fm_pack_row_weights order.  flags: FM_ELU_IN and/or
- * FM_EPI_ELU; y is [batch][ceil(length / stride)][out_channels].
- * Shapes: fm_conv1d_rows_supported(in, out, kernel) != 0 (in_channels a
- * multiple of 64, out_channels of 32, in_channels * kernel 2048, 3072 or
- * 3584), else FM_UNSUPPORTED.  Replaces MimiConv1d.forward (model.py:697-797)
- * for the encoder's last conv, the replicate-padded downsample
- * (model.py:2730-2741) and the decoder's first conv.
+ * launch.  weight is the conv's W^T [out_channels][kernel * in_channels],
+ * either in fm_pack_row_weights order (FP32 MFMA) or, with FM_WEIGHTS_X6 in
+ * flags, the plain W^T followed by its fm_split_weights planes (bf16x6).
+ * bias[n % bias_len] is added to output column n.  flags: FM_ELU_IN,
+ * FM_EPI_ELU, FM_WEIGHTS_X6; y is [batch][ceil(length / stride)][out_channels].
+ * A causal ConvTranspose1d of stride s and kernel taps * s is this call with
+ * kernel taps, stride 1, out_channels s * c_out (its phase-major W^T) and
+ * bias_len c_out: y is then [batch][length * s][c_out].
+ * Shapes: fm_conv1d_rows_supported(in, out, kernel, flags) != 0 (out_channels
+ * a multiple of 32, in_channels * kernel 2048, 3072 or 3584, in_channels a
+ * multiple of 64, or of 32 with FM_WEIGHTS_X6), else FM_UNSUPPORTED.
+ * Replaces MimiConv1d.forward (model.py:697-797) at those shapes: the
+ * encoder's last conv, the replicate-padded downsample (model.py:2730-2741)
+ * and the decoder's first conv.
  */
-int fm_conv1d_rows_supported(int in_channels, int out_channels, int kernel);
-int fm_conv1d_rows(const float* x, int batch, int length, int in_channels,
-                   const float* weight_rowpacked, const float* bias, int out_channels, int kernel,
-                   int stride, int pad_mode, int flags, float* y, hipStream_t stream);
+int fm_conv1d_rows_supported(int in_channels, int out_channels, int kernel, int flags);
+int fm_conv1d_rows(const float* x, int batch, int length, int in_channels, const float* weight,
+                   const float* bias, int bias_len, int out_channels, int kernel, int stride,
+                   int pad_mode, int flags, float* y, hipStream_t stream);
 
 /*
  * Conv1d over exactly the given rows, no padding: output row t reads input

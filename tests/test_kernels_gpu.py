@@ -256,25 +256,30 @@ ROWCONV_CASES = [
     (3, 512, 512, 4, 2, 1, "replicate", 0),
     (1, 512, 1024, 7, 1, 250, "constant", nat.EPI_ELU),
     (2, 512, 1024, 7, 1, 37, "constant", 0),
+    (2, 256, 512, 12, 1, 70, "constant", nat.ELU_IN),  # 3072-deep with k = 12 taps of 256
 ]
 
 
+@pytest.mark.parametrize("x6", [False, True], ids=["fp32", "bf16x6"])
 @pytest.mark.parametrize("B,cin,cout,k,stride,L,pad_mode,flags", ROWCONV_CASES)
-def test_conv1d_rows(B, cin, cout, k, stride, L, pad_mode, flags, ws):
+def test_conv1d_rows(B, cin, cout, k, stride, L, pad_mode, flags, x6, ws):
     lib = nat.library()
-    assert lib.fm_conv1d_rows_supported(cin, cout, k)
+    assert lib.fm_conv1d_rows_supported(cin, cout, k, nat.WEIGHTS_X6 if x6 else 0)
     g = torch.Generator().manual_seed(B * 7 + cin + cout + k + L)
     x = torch.randn(B, cin, L, generator=g)
     w = torch.randn(cout, cin, k, generator=g) / math.sqrt(cin * k)
     b = torch.randn(cout, generator=g) * 0.1 if pad_mode == "constant" else None
     layer = _Conv(w.to(DEV), None if b is None else b.to(DEV), stride, pad_mode)
-    wr = torch.empty_like(layer.w)
-    nat.call("fm_pack_row_weights", layer.w.data_ptr(), cout, k * cin, wr.data_ptr(), stream())
+    if x6:
+        wr, f = with_planes(layer.w), flags | nat.WEIGHTS_X6
+    else:
+        wr, f = torch.empty_like(layer.w), flags
+        nat.call("fm_pack_row_weights", layer.w.data_ptr(), cout, k * cin, wr.data_ptr(), stream())
     xd = x.transpose(1, 2).contiguous().to(DEV)
     rows = -(-L // stride)
     y = torch.full((B, rows, cout), float("nan"), device=DEV)
     nat.call("fm_conv1d_rows", xd.data_ptr(), B, L, cin, wr.data_ptr(),
-             None if layer.b is None else layer.b.data_ptr(), cout, k, stride, layer.replicate, flags,
+             None if layer.b is None else layer.b.data_ptr(), cout, cout, k, stride, layer.replicate, f,
              y.data_ptr(), stream())
     torch.cuda.synchronize()
     got = y.cpu().transpose(1, 2)
@@ -292,13 +297,39 @@ def test_conv1d_rows(B, cin, cout, k, stride, L, pad_mode, flags, ws):
     close(got, same.double())
 
 
+@pytest.mark.parametrize("B,L", [(1, 250), (2, 37)])
+def test_conv_transpose1d_rows(B, L):
+    """The decoder's first transposed conv (1024 -> 512, k16 s8) as the few-row
+    conv over its two taps with the phase-major weight and bias period c_out."""
+    g = torch.Generator().manual_seed(B + L)
+    cin, cout, k, s = 1024, 512, 16, 8
+    x = torch.randn(B, cin, L, generator=g)
+    w = torch.randn(cin, cout, k, generator=g) / math.sqrt(cin * k / s)
+    b = torch.randn(cout, generator=g) * 0.1
+    layer = _ConvT(w.to(DEV), b.to(DEV), s)
+    wx = with_planes(layer.w)
+    xd = x.transpose(1, 2).contiguous().to(DEV)
+    y = torch.full((B, L * s, cout), float("nan"), device=DEV)
+    nat.call("fm_conv1d_rows", xd.data_ptr(), B, L, cin, wx.data_ptr(), layer.b.data_ptr(), cout,
+             s * cout, k // s, 1, 0, nat.WEIGHTS_X6, y.data_ptr(), stream())
+    torch.cuda.synchronize()
+    got = y.cpu().transpose(1, 2)
+    want = causal_conv_transpose1d(x.double(), w.double(), b.double(), s)
+    close(got, want)
+    close_dot(got, want, causal_conv_transpose1d(x.double().abs(), w.double().abs(), b.double().abs(), s))
+
+
 def test_conv1d_rows_rejects():
     with pytest.raises(nat.NativeError, match="unsupported"):
-        nat.call("fm_conv1d_rows", 1, 1, 4, 64, 1, None, 32, 3, 1, 0, 0, 1, stream())  # K = 192
+        nat.call("fm_conv1d_rows", 1, 1, 4, 64, 1, None, 32, 32, 3, 1, 0, 0, 1, stream())  # K = 192
     with pytest.raises(nat.NativeError, match="unsupported"):
-        nat.call("fm_conv1d_rows", 1, 1, 4, 512, 1, None, 512, 4, 2, 0, nat.EPI_GELU, 1, stream())
+        nat.call("fm_conv1d_rows", 1, 1, 4, 512, 1, None, 512, 512, 4, 2, 0, nat.EPI_GELU, 1, stream())
+    with pytest.raises(nat.NativeError, match="unsupported"):  # K = 8192
+        nat.call("fm_conv1d_rows", 1, 1, 4, 512, 1, None, 1024, 1024, 16, 8, 0, nat.WEIGHTS_X6, 1, stream())
+    with pytest.raises(nat.NativeError, match="unsupported"):  # C_in = 96: 64-deep pieces would cross taps
+        nat.call("fm_conv1d_rows", 1, 1, 4, 96, 1, None, 512, 512, 32, 1, 0, 0, 1, stream())
     with pytest.raises(nat.NativeError, match="bad argument"):
-        nat.call("fm_conv1d_rows", 1, 1, 4, 512, 1, None, 512, 4, 2, 2, 0, 1, stream())
+        nat.call("fm_conv1d_rows", 1, 1, 4, 512, 1, None, 512, 512, 4, 2, 2, 0, 1, stream())
 
 
 def test_conv1d_fused_resblock_epilogues(ws):
