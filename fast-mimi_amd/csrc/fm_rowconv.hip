@@ -203,7 +203,7 @@ extern "C" {
 int fm_conv1d_rows_supported(int in_channels, int out_channels, int kernel, int flags) {
   const int K = in_channels * kernel;
   if (out_channels % 32) return 0;
-  return in_channels % (flags & FM_WEIGHTS_X6 ? 32 : 64) == 0 && (K == 2048 || K == 3072 || K == 3584);
+  return in_channels % (flags & FM_WEIGHTS_X6 ? 32 : 64) == 0 && (K == 1536 || K == 2048 || K == 3072 || K == 3584);
 }
 
 int fm_conv1d_rows(const float* x, int batch, int length, int in_channels, const float* weight,
@@ -225,11 +225,13 @@ int fm_conv1d_rows(const float* x, int batch, int length, int in_channels, const
   const int K = in_channels * kernel;
 #define FM_ROWCONV(KK, X6) hipLaunchKernelGGL((row16_conv_kernel<KK, 32, X6>), grid, dim3(512), 0, stream, p)
   if (flags & FM_WEIGHTS_X6) {
-    if (K == 2048) FM_ROWCONV(2048, true);
+    if (K == 1536) FM_ROWCONV(1536, true);
+    else if (K == 2048) FM_ROWCONV(2048, true);
     else if (K == 3072) FM_ROWCONV(3072, true);
     else FM_ROWCONV(3584, true);
   } else {
-    if (K == 2048) FM_ROWCONV(2048, false);
+    if (K == 1536) FM_ROWCONV(1536, false);
+    else if (K == 2048) FM_ROWCONV(2048, false);
     else if (K == 3072) FM_ROWCONV(3072, false);
     else FM_ROWCONV(3584, false);
   }

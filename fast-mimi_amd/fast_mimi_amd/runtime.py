@@ -41,9 +41,13 @@ _WORKSPACE_BYTES = 64 << 20
 _ROW_LINEAR_MAX_ROWS = 1024
 # Up to this many rows the 16-row kernels on fragment-packed weights are used.
 _ROW16_MAX_ROWS = 512
-# Few-row long-K convolutions (fm_conv1d_rows) up to this many output rows;
-# beyond it the tiled GEMM engine has enough tiles.
-_ROWCONV_MAX_ROWS = 512
+# Few-row long-K convolutions (fm_conv1d_rows) up to this many multiply-adds
+# (rows x out x K); beyond it the tiled GEMM engine has enough tiles.  Measured
+# at C2 shapes (warm, us, split GEMM -> row blocks): encoder last conv 21.1 ->
+# 12.6, downsample 12.2 -> 8.4, decoder first conv 27.9 -> 25.1, 512-channel
+# residual block's k3 conv at 2000 rows 27.2 -> 21.8; at 1.6e9 MACs and above
+# the row blocks lose (the 512-channel k3 conv at 4000 rows 34.2 -> 40.9).
+_ROWCONV_MAX_MACS = 1_000_000_000
 
 
 class _Conv:
@@ -193,11 +197,9 @@ class MimiRuntime:
                 layer.w, layer.flags = w, nat.WEIGHTS_X6
         for w in [m for lay in self.enc_tf + self.dec_tf for m in (lay.wqkv, lay.wo, lay.w1, lay.w2)]:
             self._x6[w.data_ptr()] = self._with_planes(w)
-        # Few-row long-K convolutions (fm_conv1d_rows; the encoder's last conv,
-        # the downsample and the decoder's first conv at a few hundred rows:
-        # 12.6 / 8.4 / 25.1 us against 21.1 / 12.2 / 27.9 us for the split
-        # GEMM at C2, warm): on the bf16x6 planes where the layer has them,
-        # else on fragment-packed FP32 weights.
+        # Few-row long-K convolutions (fm_conv1d_rows, see _ROWCONV_MAX_MACS):
+        # on the bf16x6 planes where the layer has them, else on
+        # fragment-packed FP32 weights.
         for layer in self._conv_layers():
             if layer.flags & nat.WEIGHTS_X6 and lib.fm_conv1d_rows_supported(
                     layer.c_in, layer.c_out, layer.k, nat.WEIGHTS_X6):
@@ -261,7 +263,8 @@ class MimiRuntime:
         rows = -(-L // layer.stride)
         y_len = rows if y_len is None else y_len
         y = torch.empty((B, y_len, layer.c_out), device=self.device)
-        if (layer.wr is not None and residual is None and y_len == rows and B * rows <= _ROWCONV_MAX_ROWS
+        if (layer.wr is not None and residual is None and y_len == rows
+                and B * rows * layer.c_out * layer.k * layer.c_in <= _ROWCONV_MAX_MACS
                 and not flags & ~(nat.ELU_IN | nat.EPI_ELU)):
             self._call("fm_conv1d_rows", x, B, L, layer.c_in, layer.wr, layer.b, layer.c_out,
                        layer.c_out, layer.k, layer.stride, layer.replicate,

@@ -95,11 +95,12 @@ int fm_conv1d(const float* x, int batch, int length, int in_channels, const floa
  * kernel taps, stride 1, out_channels s * c_out (its phase-major W^T) and
  * bias_len c_out: y is then [batch][length * s][c_out].
  * Shapes: fm_conv1d_rows_supported(in, out, kernel, flags) != 0 (out_channels
- * a multiple of 32, in_channels * kernel 2048, 3072 or 3584, in_channels a
- * multiple of 64, or of 32 with FM_WEIGHTS_X6), else FM_UNSUPPORTED.
- * Replaces MimiConv1d.forward (model.py:697-797) at those shapes: the
- * encoder's last conv, the replicate-padded downsample (model.py:2730-2741)
- * and the decoder's first conv.
+ * a multiple of 32, in_channels * kernel 1536, 2048, 3072 or 3584,
+ * in_channels a multiple of 64, or of 32 with FM_WEIGHTS_X6), else
+ * FM_UNSUPPORTED.  Replaces MimiConv1d.forward (model.py:697-797) at those
+ * shapes: the encoder's last conv, the replicate-padded downsample
+ * (model.py:2730-2741), the decoder's first conv and the 512-channel
+ * residual blocks' k3 convs.
  */
 int fm_conv1d_rows_supported(int in_channels, int out_channels, int kernel, int flags);
 int fm_conv1d_rows(const float* x, int batch, int length, int in_channels, const float* weight,

@@ -257,6 +257,7 @@ ROWCONV_CASES = [
     (1, 512, 1024, 7, 1, 250, "constant", nat.EPI_ELU),
     (2, 512, 1024, 7, 1, 37, "constant", 0),
     (2, 256, 512, 12, 1, 70, "constant", nat.ELU_IN),  # 3072-deep with k = 12 taps of 256
+    (1, 512, 256, 3, 1, 2000, "constant", nat.ELU_IN | nat.EPI_ELU),  # residual block k3 conv, 2000 rows
 ]
 
 
