@@ -27,7 +27,8 @@ __device__ __attribute__((aligned(16))) float g_zero_row[16];
 struct RowConvArgs {
   const float* x;    // [batch][L][C_in]
   const float* w;    // fragment-packed W^T [N][K]
-  const float* bias; // [N] or null
+  const float* bias; // [bias_len], or null
+  const float* res;  // [batch][rows_per_batch][N] with FM_EPI_RES_ADD, else null
   float* y;          // [batch][rows_per_batch][N]
   int L, c_in, stride, pad_l, replicate, rows_per_batch, rows, N, bias_len, flags;
 };
@@ -36,7 +37,7 @@ template <int K, int BN, bool X6>
 __global__ __launch_bounds__(512) void row16_conv_kernel(RowConvArgs p) {
   constexpr int NWV = 8, BM = 16, KW = K / NWV, NP = KW / 64, NT = BN / 16;
   constexpr int PR = BN + 4, OPT = BM * BN / 512;
-  static_assert(KW % 64 == 0 && OPT >= 1, "tile shape");
+  static_assert((X6 ? KW % 32 : KW % 64) == 0 && OPT >= 1, "tile shape");
   __shared__ __attribute__((aligned(16))) float red[NWV * BM * PR];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -72,7 +73,8 @@ __global__ __launch_bounds__(512) void row16_conv_kernel(RowConvArgs p) {
     // of A and B.  Units (step, plane) stream through a ring of R weight
     // fragments; A runs RA - 1 steps ahead and is split as it is used.  The
     // unit loop is unrolled by CHU units so every ring index is static.
-    constexpr int KS = KW / 32, NU = 3 * KS, R = 6, RA = KS % 4 == 0 ? 4 : 2, CHU = 3 * RA;
+    constexpr int KS = KW / 32, NU = 3 * KS;
+    constexpr int RA = KS % 4 == 0 ? 4 : KS % 2 == 0 ? 2 : 1, CHU = 3 * RA, R = CHU >= 6 ? 6 : 3;
     static_assert(KW % 32 == 0 && KS % RA == 0 && CHU % R == 0, "whole 32-deep steps per wave");
     const __bf16* w3 = reinterpret_cast<const __bf16*>(p.w + (long)p.N * K);
     const long PL = (long)p.N * K;
@@ -188,6 +190,7 @@ __global__ __launch_bounds__(512) void row16_conv_kernel(RowConvArgs p) {
 #pragma unroll
     for (int q = 1; q < NWV; ++q) v = __fadd_rn(v, red[(q * BM + er) * PR + ec + c]);
     if (p.bias) v = __fadd_rn(v, p.bias[(n0 + ec + c) % p.bias_len]);
+    if (p.flags & FM_EPI_RES_ADD) v = __fadd_rn(p.res[m * p.N + n0 + ec + c], v);
     if (p.flags & FM_EPI_ELU) v = fm_elu(v);
     out[c] = v;
   }
@@ -203,29 +206,34 @@ extern "C" {
 int fm_conv1d_rows_supported(int in_channels, int out_channels, int kernel, int flags) {
   const int K = in_channels * kernel;
   if (out_channels % 32) return 0;
-  return in_channels % (flags & FM_WEIGHTS_X6 ? 32 : 64) == 0 && (K == 1536 || K == 2048 || K == 3072 || K == 3584);
+  if (flags & FM_WEIGHTS_X6)
+    return in_channels % 32 == 0 && (K == 256 || K == 1536 || K == 2048 || K == 3072 || K == 3584);
+  return in_channels % 64 == 0 && (K == 1536 || K == 2048 || K == 3072 || K == 3584);
 }
 
 int fm_conv1d_rows(const float* x, int batch, int length, int in_channels, const float* weight,
                    const float* bias, int bias_len, int out_channels, int kernel, int stride,
-                   int pad_mode, int flags, float* y, hipStream_t stream) {
+                   int pad_mode, int flags, const float* residual, float* y, hipStream_t stream) {
   if (!x || !weight || !y || batch < 0 || length < 0 || kernel <= 0 || stride <= 0 ||
-      kernel < stride || (pad_mode != 0 && pad_mode != 1) || (bias && bias_len <= 0))
+      kernel < stride || (pad_mode != 0 && pad_mode != 1) || (bias && bias_len <= 0) ||
+      (flags & FM_EPI_RES_ADD && !residual))
     return FM_BAD_ARGUMENT;
-  if (flags & ~(FM_ELU_IN | FM_EPI_ELU | FM_WEIGHTS_X6)) return FM_UNSUPPORTED;
+  if (flags & ~(FM_ELU_IN | FM_EPI_ELU | FM_EPI_RES_ADD | FM_WEIGHTS_X6)) return FM_UNSUPPORTED;
   if (!fm_conv1d_rows_supported(in_channels, out_channels, kernel, flags)) return FM_UNSUPPORTED;
   const int rows_per_batch = (length + stride - 1) / stride;
   const long rows = (long)batch * rows_per_batch;
   if (rows == 0) return FM_OK;
   if (length == 0) return FM_BAD_ARGUMENT;
   if ((rows + 15) / 16 > 65535) return FM_UNSUPPORTED;
-  RowConvArgs p{x, weight, bias, y, length, in_channels, stride, kernel - stride, pad_mode,
-                rows_per_batch, (int)rows, out_channels, bias ? bias_len : 1, flags};
+  RowConvArgs p{x, weight, bias, flags & FM_EPI_RES_ADD ? residual : nullptr, y, length, in_channels,
+                stride, kernel - stride, pad_mode, rows_per_batch, (int)rows, out_channels,
+                bias ? bias_len : 1, flags};
   const dim3 grid(out_channels / 32, (unsigned)((rows + 15) / 16));
   const int K = in_channels * kernel;
 #define FM_ROWCONV(KK, X6) hipLaunchKernelGGL((row16_conv_kernel<KK, 32, X6>), grid, dim3(512), 0, stream, p)
   if (flags & FM_WEIGHTS_X6) {
-    if (K == 1536) FM_ROWCONV(1536, true);
+    if (K == 256) FM_ROWCONV(256, true);
+    else if (K == 1536) FM_ROWCONV(1536, true);
     else if (K == 2048) FM_ROWCONV(2048, true);
     else if (K == 3072) FM_ROWCONV(3072, true);
     else FM_ROWCONV(3584, true);

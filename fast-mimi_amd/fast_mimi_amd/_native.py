@@ -50,7 +50,7 @@ _SIGNATURES = {
     "fm_split_weights": ([_P, _I, _I, _P, _P], _I),
     "fm_conv1d": ([_P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _S, _P], _I),
     "fm_conv1d_rows_supported": ([_I, _I, _I, _I], _I),
-    "fm_conv1d_rows": ([_P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P], _I),
+    "fm_conv1d_rows": ([_P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P], _I),
     "fm_conv1d_valid": ([_P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _S, _P], _I),
     "fm_conv_transpose1d": ([_P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _S, _P], _I),
     "fm_linear": ([_P, _I, _I, _P, _I, _I, _P, _P, _P, _P, _S, _P], _I),

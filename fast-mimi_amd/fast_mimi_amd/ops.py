@@ -24,7 +24,7 @@ from . import _native as nat
 SPECS = {
     "fm_split_weights": "in:weight_packed i:rows i:cols out:planes",
     "fm_conv1d": "in:x i:batch i:length i:in_channels in:weight_packed in:bias i:out_channels i:kernel i:stride i:pad_mode i:flags in:residual out:y i:y_length out:workspace i:workspace_bytes",
-    "fm_conv1d_rows": "in:x i:batch i:length i:in_channels in:weight in:bias i:bias_len i:out_channels i:kernel i:stride i:pad_mode i:flags out:y",
+    "fm_conv1d_rows": "in:x i:batch i:length i:in_channels in:weight in:bias i:bias_len i:out_channels i:kernel i:stride i:pad_mode i:flags in:residual out:y",
     "fm_conv1d_valid": "in:x i:batch i:length i:in_channels in:weight_packed in:bias i:out_channels i:kernel i:stride i:flags in:residual out:y out:workspace i:workspace_bytes",
     "fm_conv_transpose1d": "in:x i:batch i:length i:in_channels in:weight_packed in:bias i:out_channels i:kernel i:stride i:flags in:residual out:y out:workspace i:workspace_bytes",
     "fm_linear": "in:x i:rows i:in_features in:weight_packed i:out_features i:flags in:residual in:scale out:y out:workspace i:workspace_bytes",

@@ -263,12 +263,12 @@ class MimiRuntime:
         rows = -(-L // layer.stride)
         y_len = rows if y_len is None else y_len
         y = torch.empty((B, y_len, layer.c_out), device=self.device)
-        if (layer.wr is not None and residual is None and y_len == rows
+        if (layer.wr is not None and y_len == rows
                 and B * rows * layer.c_out * layer.k * layer.c_in <= _ROWCONV_MAX_MACS
-                and not flags & ~(nat.ELU_IN | nat.EPI_ELU)):
+                and not flags & ~(nat.ELU_IN | nat.EPI_ELU | nat.EPI_RES_ADD)):
             self._call("fm_conv1d_rows", x, B, L, layer.c_in, layer.wr, layer.b, layer.c_out,
                        layer.c_out, layer.k, layer.stride, layer.replicate,
-                       flags | (layer.flags if layer.wr is layer.w else 0), y)
+                       flags | (layer.flags if layer.wr is layer.w else 0), residual, y)
             return y, rows
         self._call("fm_conv1d", x, B, L, layer.c_in, layer.w, layer.b,
                  layer.c_out, layer.k, layer.stride, layer.replicate, flags | layer.flags, residual,

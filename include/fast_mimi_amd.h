@@ -90,22 +90,23 @@ int fm_conv1d(const float* x, int batch, int length, int in_channels, const floa
  * either in fm_pack_row_weights order (FP32 MFMA) or, with FM_WEIGHTS_X6 in
  * flags, the plain W^T followed by its fm_split_weights planes (bf16x6).
  * bias[n % bias_len] is added to output column n.  flags: FM_ELU_IN,
- * FM_EPI_ELU, FM_WEIGHTS_X6; y is [batch][ceil(length / stride)][out_channels].
+ * FM_EPI_ELU, FM_EPI_RES_ADD (residual shaped as y), FM_WEIGHTS_X6; y is
+ * [batch][ceil(length / stride)][out_channels].
  * A causal ConvTranspose1d of stride s and kernel taps * s is this call with
  * kernel taps, stride 1, out_channels s * c_out (its phase-major W^T) and
  * bias_len c_out: y is then [batch][length * s][c_out].
  * Shapes: fm_conv1d_rows_supported(in, out, kernel, flags) != 0 (out_channels
- * a multiple of 32, in_channels * kernel 1536, 2048, 3072 or 3584,
- * in_channels a multiple of 64, or of 32 with FM_WEIGHTS_X6), else
- * FM_UNSUPPORTED.  Replaces MimiConv1d.forward (model.py:697-797) at those
- * shapes: the encoder's last conv, the replicate-padded downsample
- * (model.py:2730-2741), the decoder's first conv and the 512-channel
- * residual blocks' k3 convs.
+ * a multiple of 32; in_channels * kernel 1536, 2048, 3072 or 3584 with
+ * in_channels a multiple of 64, or with FM_WEIGHTS_X6 also 256 and
+ * in_channels a multiple of 32), else FM_UNSUPPORTED.  Replaces
+ * MimiConv1d.forward (model.py:697-797) at those shapes: the encoder's last
+ * conv, the replicate-padded downsample (model.py:2730-2741), the decoder's
+ * first conv and the 512-channel residual blocks' two convs.
  */
 int fm_conv1d_rows_supported(int in_channels, int out_channels, int kernel, int flags);
 int fm_conv1d_rows(const float* x, int batch, int length, int in_channels, const float* weight,
                    const float* bias, int bias_len, int out_channels, int kernel, int stride,
-                   int pad_mode, int flags, float* y, hipStream_t stream);
+                   int pad_mode, int flags, const float* residual, float* y, hipStream_t stream);
 
 /*
  * Conv1d over exactly the given rows, no padding: output row t reads input

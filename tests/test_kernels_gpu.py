@@ -258,6 +258,8 @@ ROWCONV_CASES = [
     (2, 512, 1024, 7, 1, 37, "constant", 0),
     (2, 256, 512, 12, 1, 70, "constant", nat.ELU_IN),  # 3072-deep with k = 12 taps of 256
     (1, 512, 256, 3, 1, 2000, "constant", nat.ELU_IN | nat.EPI_ELU),  # residual block k3 conv, 2000 rows
+    (1, 256, 512, 1, 1, 2000, "constant", nat.EPI_RES_ADD | nat.EPI_ELU),  # its 1x1 conv (bf16x6 only)
+    (2, 256, 512, 1, 1, 77, "constant", nat.EPI_RES_ADD),
 ]
 
 
@@ -265,7 +267,9 @@ ROWCONV_CASES = [
 @pytest.mark.parametrize("B,cin,cout,k,stride,L,pad_mode,flags", ROWCONV_CASES)
 def test_conv1d_rows(B, cin, cout, k, stride, L, pad_mode, flags, x6, ws):
     lib = nat.library()
-    assert lib.fm_conv1d_rows_supported(cin, cout, k, nat.WEIGHTS_X6 if x6 else 0)
+    if not lib.fm_conv1d_rows_supported(cin, cout, k, nat.WEIGHTS_X6 if x6 else 0):
+        assert not x6 and cin * k == 256
+        pytest.skip("256-deep convs run only on the bf16x6 weights")
     g = torch.Generator().manual_seed(B * 7 + cin + cout + k + L)
     x = torch.randn(B, cin, L, generator=g)
     w = torch.randn(cout, cin, k, generator=g) / math.sqrt(cin * k)
@@ -279,9 +283,11 @@ def test_conv1d_rows(B, cin, cout, k, stride, L, pad_mode, flags, x6, ws):
     xd = x.transpose(1, 2).contiguous().to(DEV)
     rows = -(-L // stride)
     y = torch.full((B, rows, cout), float("nan"), device=DEV)
+    res = torch.randn(B, cout, rows, generator=g) if flags & nat.EPI_RES_ADD else None
+    resd = None if res is None else res.transpose(1, 2).contiguous().to(DEV)
     nat.call("fm_conv1d_rows", xd.data_ptr(), B, L, cin, wr.data_ptr(),
              None if layer.b is None else layer.b.data_ptr(), cout, cout, k, stride, layer.replicate, f,
-             y.data_ptr(), stream())
+             None if resd is None else resd.data_ptr(), y.data_ptr(), stream())
     torch.cuda.synchronize()
     got = y.cpu().transpose(1, 2)
     xi = F.elu(x.double()) if flags & nat.ELU_IN else x.double()
@@ -289,12 +295,14 @@ def test_conv1d_rows(B, cin, cout, k, stride, L, pad_mode, flags, x6, ws):
     want = causal_conv1d(xi, w.double(), bd, stride, pad_mode=pad_mode)
     absref = causal_conv1d(xi.abs(), w.double().abs(), None if bd is None else bd.abs(), stride,
                            pad_mode=pad_mode)
+    if res is not None:
+        want = want + res.double()
     if flags & nat.EPI_ELU:
         want = F.elu(want)
-    else:
+    elif res is None:
         close_dot(got, want, absref)
     close(got, want)
-    same = run_conv(x, w, b, stride, pad_mode, flags, ws)
+    same = run_conv(x, w, b, stride, pad_mode, flags, ws, residual_ncl=res)
     close(got, same.double())
 
 
@@ -312,7 +320,7 @@ def test_conv_transpose1d_rows(B, L):
     xd = x.transpose(1, 2).contiguous().to(DEV)
     y = torch.full((B, L * s, cout), float("nan"), device=DEV)
     nat.call("fm_conv1d_rows", xd.data_ptr(), B, L, cin, wx.data_ptr(), layer.b.data_ptr(), cout,
-             s * cout, k // s, 1, 0, nat.WEIGHTS_X6, y.data_ptr(), stream())
+             s * cout, k // s, 1, 0, nat.WEIGHTS_X6, None, y.data_ptr(), stream())
     torch.cuda.synchronize()
     got = y.cpu().transpose(1, 2)
     want = causal_conv_transpose1d(x.double(), w.double(), b.double(), s)
@@ -322,15 +330,17 @@ def test_conv_transpose1d_rows(B, L):
 
 def test_conv1d_rows_rejects():
     with pytest.raises(nat.NativeError, match="unsupported"):
-        nat.call("fm_conv1d_rows", 1, 1, 4, 64, 1, None, 32, 32, 3, 1, 0, 0, 1, stream())  # K = 192
+        nat.call("fm_conv1d_rows", 1, 1, 4, 64, 1, None, 32, 32, 3, 1, 0, 0, None, 1, stream())  # K = 192
     with pytest.raises(nat.NativeError, match="unsupported"):
-        nat.call("fm_conv1d_rows", 1, 1, 4, 512, 1, None, 512, 512, 4, 2, 0, nat.EPI_GELU, 1, stream())
+        nat.call("fm_conv1d_rows", 1, 1, 4, 512, 1, None, 512, 512, 4, 2, 0, nat.EPI_GELU, None, 1, stream())
     with pytest.raises(nat.NativeError, match="unsupported"):  # K = 8192
-        nat.call("fm_conv1d_rows", 1, 1, 4, 512, 1, None, 1024, 1024, 16, 8, 0, nat.WEIGHTS_X6, 1, stream())
+        nat.call("fm_conv1d_rows", 1, 1, 4, 512, 1, None, 1024, 1024, 16, 8, 0, nat.WEIGHTS_X6, None, 1, stream())
     with pytest.raises(nat.NativeError, match="unsupported"):  # C_in = 96: 64-deep pieces would cross taps
-        nat.call("fm_conv1d_rows", 1, 1, 4, 96, 1, None, 512, 512, 32, 1, 0, 0, 1, stream())
+        nat.call("fm_conv1d_rows", 1, 1, 4, 96, 1, None, 512, 512, 32, 1, 0, 0, None, 1, stream())
     with pytest.raises(nat.NativeError, match="bad argument"):
-        nat.call("fm_conv1d_rows", 1, 1, 4, 512, 1, None, 512, 512, 4, 2, 2, 0, 1, stream())
+        nat.call("fm_conv1d_rows", 1, 1, 4, 512, 1, None, 512, 512, 4, 2, 2, 0, None, 1, stream())
+    with pytest.raises(nat.NativeError, match="bad argument"):  # residual epilogue without residual
+        nat.call("fm_conv1d_rows", 1, 1, 4, 512, 1, None, 512, 512, 4, 2, 0, nat.EPI_RES_ADD, None, 1, stream())
 
 
 def test_conv1d_fused_resblock_epilogues(ws):
