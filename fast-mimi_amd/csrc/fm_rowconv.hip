@@ -3,9 +3,10 @@
 // bottleneck's replicate-padded downsample 512 -> 512 k4 s2, the decoder's
 // first conv 512 -> 1024 k7).  The tiled GEMM engine has a few dozen tiles
 // there and splits K across blocks with a second reduce launch; this kernel
-// instead gives every 16 output rows x BN columns one block of 8 waves that
-// split K, as the transformer's row-block projections do, and sums the 8
-// partial tiles through LDS in wave order.
+// instead gives every 16 output rows x BN columns (32, or 64 where 32-column
+// blocks would not all be resident at once) one block of 8 waves that split
+// K, as the transformer's row-block projections do, and sums the 8 partial
+// tiles through LDS in wave order.
 //
 // Weights are the conv's W^T [N][K] (k = tap * C_in + c) in the fragment
 // order of fm_pack_row_weights: the float4 at ((nt * (K/64) + kp) * 4 + t) *
@@ -74,7 +75,8 @@ __global__ __launch_bounds__(512) void row16_conv_kernel(RowConvArgs p) {
     // fragments; A runs RA - 1 steps ahead and is split as it is used.  The
     // unit loop is unrolled by CHU units so every ring index is static.
     constexpr int KS = KW / 32, NU = 3 * KS;
-    constexpr int RA = KS % 4 == 0 ? 4 : KS % 2 == 0 ? 2 : 1, CHU = 3 * RA, R = CHU >= 6 ? 6 : 3;
+    // Weight ring: six units of 32-column fragments, three of 64-column ones.
+    constexpr int RA = KS % 4 == 0 ? 4 : KS % 2 == 0 ? 2 : 1, CHU = 3 * RA, R = CHU >= 6 && NT == 2 ? 6 : 3;
     static_assert(KW % 32 == 0 && KS % RA == 0 && CHU % R == 0, "whole 32-deep steps per wave");
     const __bf16* w3 = reinterpret_cast<const __bf16*>(p.w + (long)p.N * K);
     const long PL = (long)p.N * K;
@@ -228,10 +230,22 @@ int fm_conv1d_rows(const float* x, int batch, int length, int in_channels, const
   RowConvArgs p{x, weight, bias, flags & FM_EPI_RES_ADD ? residual : nullptr, y, length, in_channels,
                 stride, kernel - stride, pad_mode, rows_per_batch, (int)rows, out_channels,
                 bias ? bias_len : 1, flags};
-  const dim3 grid(out_channels / 32, (unsigned)((rows + 15) / 16));
+  const unsigned row_blocks = (unsigned)((rows + 15) / 16);
+  const dim3 grid(out_channels / 32, row_blocks);
   const int K = in_channels * kernel;
 #define FM_ROWCONV(KK, X6) hipLaunchKernelGGL((row16_conv_kernel<KK, 32, X6>), grid, dim3(512), 0, stream, p)
-  if (flags & FM_WEIGHTS_X6) {
+  // bf16x6: 64-column blocks where 32-column ones would not all be resident
+  // at once (two 8-wave blocks per CU).
+  const bool wide = out_channels % 64 == 0 && (long)(out_channels / 32) * row_blocks > 512;
+  const dim3 grid64(out_channels / 64, row_blocks);
+#define FM_ROWCONV64(KK) hipLaunchKernelGGL((row16_conv_kernel<KK, 64, true>), grid64, dim3(512), 0, stream, p)
+  if ((flags & FM_WEIGHTS_X6) && wide) {
+    if (K == 256) FM_ROWCONV64(256);
+    else if (K == 1536) FM_ROWCONV64(1536);
+    else if (K == 2048) FM_ROWCONV64(2048);
+    else if (K == 3072) FM_ROWCONV64(3072);
+    else FM_ROWCONV64(3584);
+  } else if (flags & FM_WEIGHTS_X6) {
     if (K == 256) FM_ROWCONV(256, true);
     else if (K == 1536) FM_ROWCONV(1536, true);
     else if (K == 2048) FM_ROWCONV(2048, true);
@@ -244,6 +258,7 @@ int fm_conv1d_rows(const float* x, int batch, int length, int in_channels, const
     else FM_ROWCONV(3584, false);
   }
 #undef FM_ROWCONV
+#undef FM_ROWCONV64
   return (int)hipGetLastError();
 }
 
