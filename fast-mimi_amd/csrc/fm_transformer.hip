@@ -1243,13 +1243,21 @@ __global__ __launch_bounds__(512) void row_stream_linear_kernel(
 // split as it is read, and each B fragment of a plane is a 512-byte run.
 // 1.85x the FP32 16x16x4 MFMA rate per contraction (measured 13.4 vs 18.5 ns
 // per instruction, six against eight per 16 x 16 x 32).
-template <int K, int BN, bool X6 = false>
+//
+// UPS: the projection feeds the depthwise ConvTranspose1d (kernel 4, stride
+// 2, trim 2) of the decoder's upsample, y[2t + p] = h[t-1] w[p+2] + h[t] w[p]
+// per channel (h[t-1] = 0 at a sequence start), computed in the epilogue: a
+// block's 16 rows are t0 - 1 .. t0 + 14 (the first one only feeds row t0's
+// taps), and y is the upsampled [rows * 2][N]; up_w is [N][4].
+template <int K, int BN, bool X6 = false, bool UPS = false>
 __global__ __launch_bounds__(512) void row16_linear_kernel(
     const float* __restrict__ x, int rows, const float* __restrict__ gamma,
     const float* __restrict__ beta, float eps, const float* __restrict__ wp, int N, int flags,
     const float* res, const float* __restrict__ scale, const float* __restrict__ cos_t,
-    const float* __restrict__ sin_t, int rope_cols, int rows_per_seq, float* y) {
+    const float* __restrict__ sin_t, int rope_cols, int rows_per_seq, float* y,
+    const float* __restrict__ up_w = nullptr) {
   constexpr int NWV = 8, BM = 16, KW = K / NWV, NP = KW / 64, NT = BN / 16;
+  static_assert(!UPS || (!X6 && K == 512), "upsample epilogue on the staged FP32 path");
   constexpr bool STAGE = (K == 512);
   // PR = 4 mod 16: the four 16-lane groups of a partial-tile store hit disjoint banks.
   constexpr int PA = K + 4, PR = BN + 4, OPT = BM * BN / 512;
@@ -1261,7 +1269,7 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
-  const long m0 = (long)blockIdx.y * BM;
+  const long m0 = UPS ? (long)blockIdx.y * (BM - 1) - 1 : (long)blockIdx.y * BM;
   const int n0 = blockIdx.x * BN;
   const int kw0 = wave * KW;
 
@@ -1270,8 +1278,8 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
   auto stage_rows = [&]() {
     constexpr int TPR = 32, CH = K / 4 / TPR;
     const int r = tid / TPR, p = tid % TPR;
-    const bool valid = m0 + r < rows;
-    const float* xr = x + min(m0 + r, (long)rows - 1) * K;
+    const bool valid = m0 + r < rows && m0 + r >= 0;
+    const float* xr = x + max(min(m0 + r, (long)rows - 1), 0L) * K;
     floatx4 v[CH];
 #pragma unroll
     for (int u = 0; u < CH; ++u) v[u] = *reinterpret_cast<const floatx4*>(xr + 4 * (p + TPR * u));
@@ -1316,7 +1324,7 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
   // reduction.
   const int er = tid / (BN / OPT), ec = (tid % (BN / OPT)) * OPT;
   const long m = m0 + er;
-  const long mc = min(m, (long)rows - 1);
+  const long mc = max(min(m, (long)rows - 1), 0L);
   const int tpos = (int)(mc % rows_per_seq);
   const bool rope = BN == 64 && cos_t && n0 < rope_cols;
   const bool res_scale = flags & FM_EPI_RES_SCALE;
@@ -1350,11 +1358,27 @@ __global__ __launch_bounds__(512) void row16_linear_kernel(
       for (int q = 1; q < NWV; ++q) v = __fadd_rn(v, red[(q * BM + er) * PR + ec + c]);
       out[c] = v;
     }
-    if (rope) {
+    if (rope || UPS) {
       __syncthreads();
 #pragma unroll
       for (int c = 0; c < OPT; ++c) red[er * PR + ec + c] = out[c];
       __syncthreads();
+    }
+    if constexpr (UPS) {
+      // Row er >= 1 is frame t = m; its two output rows read frames t and t - 1.
+      if (er == 0 || m >= rows) return;
+      const bool first = m % rows_per_seq == 0;
+#pragma unroll
+      for (int c = 0; c < OPT; ++c) {
+        const int n = n0 + ec + c;
+        const float cur = out[c], prev = red[(er - 1) * PR + ec + c];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const float v = __fmul_rn(cur, up_w[n * 4 + q]);
+          y[(2 * m + q) * N + n] = first ? v : __fadd_rn(__fmul_rn(prev, up_w[n * 4 + q + 2]), v);
+        }
+      }
+      return;
     }
     if (m >= rows) return;
 #pragma unroll
@@ -1640,6 +1664,23 @@ int fm_row_linear_packed(const float* x, int rows, int in_features, const float*
   else if (wide) FM_R16(512, 64, g64);
   else FM_R16(512, 32, g32);
 #undef FM_R16
+  return (int)hipGetLastError();
+}
+
+// Projection of the RVQ decoder output followed by the bottleneck's
+// depthwise ConvTranspose1d upsample (kernel 4, stride 2), in one launch.
+int fm_row_linear_packed_upsample(const float* x, int rows, int in_features,
+                                  const float* weight_packed, int out_features, int rows_per_seq,
+                                  const float* up_weight, float* y, hipStream_t stream) {
+  if (!x || !weight_packed || !up_weight || !y || rows < 0 || rows_per_seq <= 0)
+    return FM_BAD_ARGUMENT;
+  if (in_features != 512 || out_features <= 0 || out_features % 32) return FM_UNSUPPORTED;
+  if (rows == 0) return FM_OK;
+  const long blocks = (rows + 14) / 15;  // 15 new frames per 16-row block
+  if (blocks > 65535) return FM_UNSUPPORTED;
+  hipLaunchKernelGGL((row16_linear_kernel<512, 32, false, true>), dim3(out_features / 32, (unsigned)blocks),
+                     dim3(512), 0, stream, x, rows, nullptr, nullptr, 0.0f, weight_packed, out_features, 0,
+                     nullptr, nullptr, nullptr, nullptr, 0, rows_per_seq, y, up_weight);
   return (int)hipGetLastError();
 }
 

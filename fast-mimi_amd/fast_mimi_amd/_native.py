@@ -58,6 +58,7 @@ _SIGNATURES = {
     "fm_row_linear": ([_P, _I, _I, _P, _P, _F, _P, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P], _I),
     "fm_row_linear_packed": ([_P, _I, _I, _P, _P, _F, _P, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P], _I),
     "fm_pack_row_weights": ([_P, _I, _I, _P, _P], _I),
+    "fm_row_linear_packed_upsample": ([_P, _I, _I, _P, _I, _I, _P, _P, _P], _I),
     "fm_apply_rope": ([_P, _L, _I, _I, _I, _P, _P, _I, _P], _I),
     "fm_layer_norm": ([_P, _P, _P, _L, _I, _F, _P, _P], _I),
     "fm_window_attention": ([_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _I, _P], _I),

@@ -34,6 +34,7 @@ SPECS = {
     "fm_row_linear": "in:x i:rows i:in_features in:ln_gamma in:ln_beta f:ln_eps in:weight i:out_features i:flags in:residual in:scale in:rope_cos in:rope_sin i:rope_cols i:rows_per_seq out:y",
     "fm_row_linear_packed": "in:x i:rows i:in_features in:ln_gamma in:ln_beta f:ln_eps in:weight_packed i:out_features i:flags in:residual in:scale in:rope_cos in:rope_sin i:rope_cols i:rows_per_seq out:y",
     "fm_pack_row_weights": "in:weight i:out_features i:in_features out:out",
+    "fm_row_linear_packed_upsample": "in:x i:rows i:in_features in:weight_packed i:out_features i:rows_per_seq in:up_weight out:y",
     "fm_apply_rope": "out:x i:rows i:ld i:rope_cols i:head_dim in:cos_table in:sin_table i:rows_per_seq",
     "fm_layer_norm": "in:x in:gamma in:beta i:rows i:channels f:eps out:y",
     "fm_window_attention": "in:qkv i:ld_qkv i:q_offset i:k_offset i:v_offset in:cos_table in:sin_table i:batch i:length i:heads i:kv_heads i:head_dim i:window f:scale out:out i:ld_out",

@@ -597,10 +597,20 @@ class MimiRuntime:
         self._call("fm_rvq_decode", codes, B, nq, T, cfg.num_semantic_quantizers,
                  self.embeds, cfg.codebook_size, vq, q)
         self._tag = "rvq.out"
-        h = self._proj(q, M, self.w_out).reshape(B, T, cfg.hidden_size)
-        self._tag = "up"
         L = T
-        if self.bottleneck:
+        packed = self._packed.get(self.w_out.data_ptr())
+        fused_up = (self.bottleneck and self.up_k == 4 and packed is not None and M <= _ROW16_MAX_ROWS
+                    and self.w_out.shape[1] == 512 and cfg.hidden_size % 32 == 0)
+        if fused_up:
+            # Output projection and the depthwise upsample in one launch.
+            h = torch.empty((B, 2 * T, cfg.hidden_size), device=self.device)
+            self._call("fm_row_linear_packed_upsample", q, M, 2 * vq, packed, cfg.hidden_size, T,
+                       self.up_w, h)
+            L = 2 * T
+        else:
+            h = self._proj(q, M, self.w_out).reshape(B, T, cfg.hidden_size)
+        self._tag = "up"
+        if self.bottleneck and not fused_up:
             up = torch.empty((B, L * 2, cfg.hidden_size), device=self.device)
             self._call("fm_upsample_depthwise", h, B, L, cfg.hidden_size,
                      self.up_w, self.up_k, 2, up)

@@ -231,6 +231,20 @@ int fm_row_linear_packed(const float* x, int rows, int in_features, const float*
                          int out_features, int flags, const float* residual, const float* scale,
                          const float* rope_cos, const float* rope_sin, int rope_cols,
                          int rows_per_seq, float* y, hipStream_t stream);
+/*
+ * fm_row_linear_packed (no LayerNorm, RoPE or epilogue; in_features 512,
+ * out_features a multiple of 32) followed by the depthwise causal
+ * ConvTranspose1d of kernel 4 and stride 2 (up_weight [out_features][4], the
+ * reference's [channels][1][4]), in one launch: y is [rows * 2][out_features],
+ * y[2t + p] = h[t-1] * w[p+2] + h[t] * w[p] with h[t-1] = 0 at the start of
+ * each sequence of rows_per_seq rows, rounded as fm_upsample_depthwise.
+ * Replaces the RVQ output projection and the bottleneck upsample of the
+ * decoder (model.py:2570-2627 output_proj, :2744-2752).
+ */
+int fm_row_linear_packed_upsample(const float* x, int rows, int in_features,
+                                  const float* weight_packed, int out_features, int rows_per_seq,
+                                  const float* up_weight, float* y, hipStream_t stream);
+
 /* Packs a [out_features][in_features] weight (out % 16 == 0, in % 64 == 0);
  * out must not alias weight.  One-time preparation, like the reference's
  * weight packing in _optimized_runtime.py / _packed_qkv.py. */

@@ -1058,6 +1058,36 @@ def test_rvq_decode_gather_sum_is_exact(B, nq, T, nsem):
     assert torch.equal(got[..., d:], ac.expand(B, T, d))
 
 
+@pytest.mark.parametrize("B,T", [(1, 125), (2, 63), (3, 1), (1, 31)])
+def test_row_linear_packed_upsample_matches_two_launches(B, T):
+    """Output projection + depthwise k4 s2 upsample in one launch gives the
+    bits of fm_row_linear_packed followed by fm_upsample_depthwise, sequence
+    starts included (frames whose 16-row block begins inside another sequence)."""
+    g = torch.Generator().manual_seed(B * 100 + T)
+    N, K = 512, 512
+    x = torch.randn(B * T, K, generator=g).to(DEV)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(DEV)
+    up = (torch.randn(N, 1, 4, generator=g) * 0.5).to(DEV)
+    wp = torch.empty_like(w)
+    nat.call("fm_pack_row_weights", w.data_ptr(), N, K, wp.data_ptr(), stream())
+    h = torch.empty(B * T, N, device=DEV)
+    nat.call("fm_row_linear_packed", x.data_ptr(), B * T, K, None, None, 1e-5, wp.data_ptr(), N, 0,
+             None, None, None, None, 0, T, h.data_ptr(), stream())
+    want = torch.empty(B, 2 * T, N, device=DEV)
+    nat.call("fm_upsample_depthwise", h.data_ptr(), B, T, N, up.data_ptr(), 4, 2, want.data_ptr(), stream())
+    got = torch.full((B, 2 * T, N), float("nan"), device=DEV)
+    nat.call("fm_row_linear_packed_upsample", x.data_ptr(), B * T, K, wp.data_ptr(), N, T, up.data_ptr(),
+             got.data_ptr(), stream())
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    ref = F.conv_transpose1d((x.double().cpu() @ w.double().cpu().t()).view(B, T, N).transpose(1, 2),
+                             up.double().cpu(), None, 2, 0, 0, N)[..., : 2 * T]
+    close(got.cpu().transpose(1, 2), ref)
+    with pytest.raises(nat.NativeError, match="unsupported"):
+        nat.call("fm_row_linear_packed_upsample", x.data_ptr(), B * T, 2048, wp.data_ptr(), N, T,
+                 up.data_ptr(), got.data_ptr(), stream())
+
+
 @pytest.mark.parametrize("B,L,C", [(1, 125, 512), (3, 7, 16), (2, 1, 512)])
 def test_upsample_depthwise(B, L, C):
     g = torch.Generator().manual_seed(L)
