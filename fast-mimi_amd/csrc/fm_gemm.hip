@@ -1288,6 +1288,211 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6_kernel(GemmArgs p, const
 }
 
 // ---------------------------------------------------------------------------
+// bf16x6 tile with the FP32 A operand loaded global -> LDS directly: each
+// lane's 16-byte chunk of the 16-deep A k-tile lands in an XOR-swizzled slot
+// (chunk c of row r at position c ^ ((r / 4) & 3), so the 16-lane groups of a
+// fragment read hit distinct banks) with the zero page for out-of-window and
+// past-M rows, next to the B planes as in gemm_x6_kernel; NST-stage ring, one
+// barrier per k-tile.  Each wave splits its own A fragments after the LDS
+// read (64 x 64 wave tiles, so an A fragment is split by two waves), which
+// takes the register staging and its wait out of the k-loop.  Same six
+// products in the same order as gemm_x6_kernel, so the same results.
+template <int BM, int BN, int WM, int WN, int NST>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, const __bf16* __restrict__ w3) {
+  constexpr int NW = WM * WN, NTH = 64 * NW, BK = 16;
+  static_assert(NW == 8 && NST == 2, "eight waves, two stages");
+  constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
+  constexpr int CPR = 4, RPI = 16, SWR = 4;  // A: chunks per row, rows per load instruction
+  constexpr int AI = BM / (NW * RPI);        // A load instructions per wave per stage
+  static_assert(AI >= 1 && AI * NW * RPI == BM && FM >= 1 && FN >= 1 && BN % 32 == 0, "tiling");
+  constexpr int PLANE_B = BN * BK * 2, STAGE_A = BM * BK * 4, STAGE = STAGE_A + 3 * PLANE_B;
+  constexpr int NBI = 3 * BN / 32;  // 1 KB B load instructions per stage
+  constexpr int HM = WTM, PC = BN + 4, TILE_B = HM * PC * 4;
+  __shared__ __attribute__((aligned(16))) char smem[NST * STAGE > TILE_B ? NST * STAGE : TILE_B];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave / WN;
+  const int wm0 = wr * WTM, wn0 = (wave % WN) * WTN;
+  const long M = (long)p.batch * p.rows;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int tile = tile_index();
+  const long m0 = (long)(tile / tiles_n) * BM;
+  const int n0 = (tile % tiles_n) * BN;
+  const int k_begin = blockIdx.y * p.k_split;
+  const int k_end = min(p.K, k_begin + p.k_split);
+
+  // This lane's chunk of each A load instruction: tile row r, chunk position
+  // cp (global chunk cp ^ swizzle).
+  const int lr = lane / CPR, cp = lane % CPR;
+  const float* a_row[AI];
+  int a_p0[AI];
+#pragma unroll
+  for (int i = 0; i < AI; ++i) {
+    const int r = (wave * AI + i) * RPI + lr;
+    const long mm = m0 + r;
+    const int m = (int)min(mm, M - 1);
+    const int b = (int)fm_div((unsigned)m, p.rows_div);
+    const int t = m - b * p.rows;
+    a_p0[i] = mm < M ? t * p.rs - p.padL : INT_MIN / 2;
+    a_row[i] = p.x + (long)b * p.L_in * p.C_in + (long)a_p0[i] * p.C_in + 4 * (cp ^ ((r / SWR) & (CPR - 1)));
+  }
+  const long KN = (long)p.K * p.N;
+  auto issue = [&](int stage, int k0) {
+    char* As = smem + stage * STAGE;
+    char* Bs = As + STAGE_A;
+    const int tap = k0 / p.C_in;  // uniform: a k-tile lies in one tap
+#pragma unroll
+    for (int i = 0; i < AI; ++i) {
+      const bool ok = (unsigned)(a_p0[i] + tap) < (unsigned)p.L_in;
+      const float* src = ok ? a_row[i] + k0 : g_zero16;
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(As + (wave * AI + i) * RPI * BK * 4),
+                                       16, 0, 0);
+    }
+#pragma unroll
+    for (int i = wave; i < NBI; i += NW) {
+      const int pl = i / (BN / 32), rg = i % (BN / 32);
+      const int row = rg * 32 + (lane >> 1);
+      const void* src = (n0 + row < p.N) ? (const void*)(w3 + pl * KN + ((long)(k0 >> 4) * p.N + n0 + row) * 16 + 8 * (lane & 1))
+                                         : (const void*)g_zero16;
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(Bs + pl * PLANE_B + rg * 32 * BK * 2),
+                                       16, 0, 0);
+    }
+  };
+
+  floatx16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int lrow = lane & 31, lk = lane >> 5;
+  const bool elu_in = p.flags & FM_ELU_IN;
+  const int nkt = (k_end - k_begin) / BK;
+  if (nkt > 0) issue(0, k_begin);
+  for (int kt = 0; kt < nkt; ++kt) {
+    // This wave's loads of stage kt are done; after the barrier every wave's
+    // are, and every wave has finished reading stage (kt + 1) % 2.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (kt + 1 < nkt) issue((kt + 1) % NST, k_begin + (kt + 1) * BK);
+    const char* As = smem + (kt % NST) * STAGE;
+    const char* Bs = As + STAGE_A;
+    bf16x8 a0[FM], a1[FM], a2[FM], b0[FN], b1[FN], b2[FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int row = wm0 + 32 * i + lrow;
+      const int sw = (row / SWR) & (CPR - 1);
+      floatx4 v0 = *reinterpret_cast<const floatx4*>(As + row * BK * 4 + 16 * ((2 * lk) ^ sw));
+      floatx4 v1 = *reinterpret_cast<const floatx4*>(As + row * BK * 4 + 16 * ((2 * lk + 1) ^ sw));
+      if (elu_in) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v0[e] = fm_elu(v0[e]), v1[e] = fm_elu(v1[e]);
+      }
+      bf16x4 l0, l1, l2, h0, h1, h2;
+      split3(v0, l0, l1, l2);
+      split3(v1, h0, h1, h2);
+      a0[i] = __builtin_shufflevector(l0, h0, 0, 1, 2, 3, 4, 5, 6, 7);
+      a1[i] = __builtin_shufflevector(l1, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+      a2[i] = __builtin_shufflevector(l2, h2, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const char* bb = Bs + (wn0 + 32 * j + lrow) * (BK * 2) + lk * 16;
+      b0[j] = *reinterpret_cast<const bf16x8*>(bb);
+      b1[j] = *reinterpret_cast<const bf16x8*>(bb + PLANE_B);
+      b2[j] = *reinterpret_cast<const bf16x8*>(bb + 2 * PLANE_B);
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        acc[i][j] = fm_mfma32_bf16(a1[i], b1[j], acc[i][j]);
+        acc[i][j] = fm_mfma32_bf16(a1[i], b0[j], acc[i][j]);
+        acc[i][j] = fm_mfma32_bf16(a0[i], b1[j], acc[i][j]);
+      }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        acc[i][j] = fm_mfma32_bf16(a2[i], b0[j], acc[i][j]);
+        acc[i][j] = fm_mfma32_bf16(a0[i], b2[j], acc[i][j]);
+        acc[i][j] = fm_mfma32_bf16(a0[i], b0[j], acc[i][j]);
+      }
+  }
+  lds_barrier();
+
+  // Epilogue: WM passes of one wave row (WTM rows) through LDS.
+  float* fsm = reinterpret_cast<float*>(smem);
+  const int lcol = lane & 31;
+  const bool crop = p.y_rows != p.rows;
+  const bool has_res = p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE);
+  float* part = p.partial ? p.partial + (long)blockIdx.y * M * p.N : nullptr;
+  constexpr int CG = BN / 4, RSTEP = NTH / CG, NRUN = HM / RSTEP, RB = NRUN < 2 ? NRUN : 2;
+  static_assert(NTH % CG == 0 && HM % RSTEP == 0 && NRUN % RB == 0, "epilogue runs");
+  const int c = (tid % CG) * 4, r0 = tid / CG;
+  const int n = n0 + c;
+  const bool n_ok = n < p.N;
+  const int ncl = n_ok ? n : 0;
+  const floatx4 bias = (p.bias && !part) ? *reinterpret_cast<const floatx4*>(p.bias + ncl % p.bias_len)
+                                         : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  const floatx4 scale = ((p.flags & FM_EPI_RES_SCALE) && !part)
+                            ? *reinterpret_cast<const floatx4*>(p.scale + ncl)
+                            : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int hf = 0; hf < WM; ++hf) {
+    if (wr == hf) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            fsm[(i * 32 + fm_mfma32_row(r, lane)) * PC + wn0 + j * 32 + lcol] = acc[i][j][r];
+    }
+    lds_barrier();
+    const long mh = m0 + hf * HM;
+#pragma unroll
+    for (int u0 = 0; u0 < NRUN; u0 += RB) {
+      floatx4 v[RB], res[RB];
+#pragma unroll
+      for (int u = 0; u < RB; ++u) {
+        const int r = r0 + (u0 + u) * RSTEP;
+        const long m = min(mh + r, M - 1);
+        v[u] = *reinterpret_cast<const floatx4*>(fsm + r * PC + c);
+        res[u] = (has_res && !part) ? *reinterpret_cast<const floatx4*>(p.res + m * p.N + ncl)
+                                    : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (int u = 0; u < RB; ++u) {
+        const long m = mh + r0 + (u0 + u) * RSTEP;
+        if (m >= M || !n_ok) continue;
+        if (part) {
+          *reinterpret_cast<floatx4*>(part + m * p.N + n) = v[u];
+          continue;
+        }
+        floatx4 o = v[u];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = epilogue_v(o[e], bias[e], res[u][e], scale[e], p.flags);
+        long dst = m * p.N + n;
+        if (crop) {
+          const int b = (int)(m / p.rows);
+          const int t = (int)(m - (long)b * p.rows);
+          if (t >= p.y_rows) continue;
+          dst = ((long)b * p.y_rows + t) * p.N + n;
+        }
+        *reinterpret_cast<floatx4*>(p.y + dst) = o;
+      }
+    }
+    if (hf + 1 < WM) lds_barrier();
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Single-input-channel causal conv (the waveform -> num_filters first layer):
 // y[b, t, c] = bias[c] + sum_j w[c, j] * x[b, t - pad + j].  HBM-bound on the
 // output; a block stages its 256 positions plus the causal halo in LDS and
@@ -1416,7 +1621,7 @@ constexpr TileCfg kBig64 = {64, 128, 1, 32, 11, 0};    // double-buffered, 32x32
 // Direct-load forms of the three double-buffered tiles (taken when the
 // operands allow, see gemm_dl_kernel).
 constexpr TileCfg kDl128 = {128, 128, 1, 32, 13, 0};
-constexpr TileCfg kX6 = {128, 128, 1, 32, 16, 0};     // bf16x6 tiles (k-tile 16; splits stay 32-aligned)
+constexpr TileCfg kX6 = {128, 128, 1, 32, 16, 0};     // bf16x6 tiles (k-tile 16; splits stay 32-aligned); direct-load A
 constexpr TileCfg kX6Big = {256, 128, 1, 32, 17, 0};
 constexpr TileCfg kX6Small = {64, 128, 1, 32, 18, 0};  // four waves of 64x32
 constexpr TileCfg kDl192 = {192, 128, 1, 32, 14, 0};
@@ -1579,8 +1784,11 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
         while (sp < most && tc * sp < 360 && p.K / (2 * sp) >= 128) sp *= 2;
         return sp;
       };
-      const int s128 = fewest(kX6, 4);
-      if (t128 * s128 >= 360) {
+      // From 160 tiles the direct-load 128x128 tile runs unsplit (no
+      // partials, no reduce launch): C2 enc.down5 64 us against 70 us split,
+      // C2 dec.up6 53 against 63 us, fc2 at 8000 rows 108 against 117 us.
+      const int s128 = t128 >= 160 ? 1 : fewest(kX6, 4);
+      if (t128 * s128 >= 360 || s128 == 1) {
         cfg = kX6;
         splits = s128;
       } else {
@@ -1589,10 +1797,10 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
       }
       tiles = tile_count(M, p.N, cfg);
     } else if (t128 * splits >= 192) {
-      // 256x128 where it gives >= 384 tiles; unsplit grids of 192-383
-      // 128x128 tiles take 64x128 (the 2500-row qkv / fc1 and 8000-row
-      // output projections: 38 vs 42, 46 vs 51, 36 vs 39 us).
-      cfg = tile_count(M, p.N, kX6Big) >= 384 ? kX6Big : (t128 < 384 && splits == 1 ? kX6Small : kX6);
+      // 256x128 where it gives >= 384 tiles, else the direct-load 128x128
+      // tile (the 2500-row qkv projection 34 us against 40 us for 64x128
+      // tiles, the 8000-row output projection 34 against 37 us).
+      cfg = tile_count(M, p.N, kX6Big) >= 384 ? kX6Big : kX6;
       tiles = tile_count(M, p.N, cfg);
     }
   }
@@ -1628,7 +1836,7 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     case 14: hipLaunchKernelGGL((gemm_dl_kernel<192, 128, 4, 32, 2, 4>), grid, dim3(512), 0, s, p); break;
     case 15: hipLaunchKernelGGL((gemm_dl_kernel<64, 128, 4, 64, 2, 4>), grid, dim3(512), 0, s, p); break;
     case 16:
-      hipLaunchKernelGGL((gemm_x6_kernel<128, 128, 2, 4, 2>), grid, dim3(512), 0, s, p,
+      hipLaunchKernelGGL((gemm_x6d_kernel<128, 128, 4, 2, 2>), grid, dim3(512), 0, s, p,
                          reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
       break;
     case 17:
