@@ -1294,13 +1294,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6_kernel(GemmArgs p, const
 // fragment read hit distinct banks) with the zero page for out-of-window and
 // past-M rows, next to the B planes as in gemm_x6_kernel; NST-stage ring, one
 // barrier per k-tile.  Each wave splits its own A fragments after the LDS
-// read (64 x 64 wave tiles, so an A fragment is split by two waves), which
-// takes the register staging and its wait out of the k-loop.  Same six
+// read (64 x 64 / 32 x 64 wave tiles, so an A fragment is split by two
+// waves), which takes the register staging and its wait out of the k-loop.  Same six
 // products in the same order as gemm_x6_kernel, so the same results.
 template <int BM, int BN, int WM, int WN, int NST>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, const __bf16* __restrict__ w3) {
   constexpr int NW = WM * WN, NTH = 64 * NW, BK = 16;
-  static_assert(NW == 8 && NST == 2, "eight waves, two stages");
+  static_assert((NW == 8 || NW == 4) && NST == 2, "eight or four waves, two stages");
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
   constexpr int CPR = 4, RPI = 16, SWR = 4;  // A: chunks per row, rows per load instruction
   constexpr int AI = BM / (NW * RPI);        // A load instructions per wave per stage
@@ -1623,7 +1623,7 @@ constexpr TileCfg kBig64 = {64, 128, 1, 32, 11, 0};    // double-buffered, 32x32
 constexpr TileCfg kDl128 = {128, 128, 1, 32, 13, 0};
 constexpr TileCfg kX6 = {128, 128, 1, 32, 16, 0};     // bf16x6 tiles (k-tile 16; splits stay 32-aligned); direct-load A
 constexpr TileCfg kX6Big = {256, 128, 1, 32, 17, 0};
-constexpr TileCfg kX6Small = {64, 128, 1, 32, 18, 0};  // four waves of 64x32
+constexpr TileCfg kX6Small = {64, 128, 1, 32, 18, 0};  // direct-load A, four waves of 32x64
 constexpr TileCfg kDl192 = {192, 128, 1, 32, 14, 0};
 // 64x128 runs one block per CU: 64-deep k-tiles (96 KB ring) halve its barriers.
 constexpr TileCfg kDl64 = {64, 128, 1, 64, 15, 0};
@@ -1844,7 +1844,7 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
                          reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
       break;
     case 18:
-      hipLaunchKernelGGL((gemm_x6_kernel<64, 128, 1, 4, 2>), grid, dim3(256), 0, s, p,
+      hipLaunchKernelGGL((gemm_x6d_kernel<64, 128, 2, 2, 2>), grid, dim3(256), 0, s, p,
                          reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
       break;
     case 7: hipLaunchKernelGGL((gemm_mid_kernel<64, 64, 1>), grid, dim3(NTHREADS), 0, s, p); break;
