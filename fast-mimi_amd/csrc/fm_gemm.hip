@@ -1294,20 +1294,25 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6_kernel(GemmArgs p, const
 // fragment read hit distinct banks) with the zero page for out-of-window and
 // past-M rows, next to the B planes as in gemm_x6_kernel; NST-stage ring, one
 // barrier per k-tile.  Each wave splits its own A fragments after the LDS
-// read (64 x 64 / 32 x 64 wave tiles, so an A fragment is split by two
-// waves), which takes the register staging and its wait out of the k-loop.  Same six
+// read (32 x 64 wave tiles in two columns, so an A fragment is split by two
+// waves; 4, 8 or 12 waves), which takes the register staging and its wait out of the k-loop.  Same six
 // products in the same order as gemm_x6_kernel, so the same results.
 template <int BM, int BN, int WM, int WN, int NST>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, const __bf16* __restrict__ w3) {
   constexpr int NW = WM * WN, NTH = 64 * NW, BK = 16;
-  static_assert((NW == 8 || NW == 4) && NST == 2, "eight or four waves, two stages");
+  static_assert((NW == 12 || NW == 8 || NW == 4) && NST == 2, "twelve, eight or four waves, two stages");
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
   constexpr int CPR = 4, RPI = 16, SWR = 4;  // A: chunks per row, rows per load instruction
   constexpr int AI = BM / (NW * RPI);        // A load instructions per wave per stage
   static_assert(AI >= 1 && AI * NW * RPI == BM && FM >= 1 && FN >= 1 && BN % 32 == 0, "tiling");
   constexpr int PLANE_B = BN * BK * 2, STAGE_A = BM * BK * 4, STAGE = STAGE_A + 3 * PLANE_B;
   constexpr int NBI = 3 * BN / 32;  // 1 KB B load instructions per stage
-  constexpr int HM = WTM, PC = BN + 4, TILE_B = HM * PC * 4;
+  // Epilogue passes of EG wave rows (EG the fewest that the block's rows
+  // per store step divide).
+  constexpr int CG = BN / 4, RSTEP = NTH / CG;
+  constexpr int EG = (WTM % RSTEP == 0) ? 1 : (2 * WTM % RSTEP == 0 && WM % 2 == 0) ? 2 : 3;
+  constexpr int HM = EG * WTM, PC = BN + 4, TILE_B = HM * PC * 4;
+  static_assert(WM % EG == 0 && HM % RSTEP == 0, "epilogue passes");
   __shared__ __attribute__((aligned(16))) char smem[NST * STAGE > TILE_B ? NST * STAGE : TILE_B];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1432,7 +1437,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
   const bool crop = p.y_rows != p.rows;
   const bool has_res = p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE);
   float* part = p.partial ? p.partial + (long)blockIdx.y * M * p.N : nullptr;
-  constexpr int CG = BN / 4, RSTEP = NTH / CG, NRUN = HM / RSTEP, RB = NRUN < 2 ? NRUN : 2;
+  constexpr int NRUN = HM / RSTEP, RB = NRUN < 2 ? NRUN : 2;
   static_assert(NTH % CG == 0 && HM % RSTEP == 0 && NRUN % RB == 0, "epilogue runs");
   const int c = (tid % CG) * 4, r0 = tid / CG;
   const int n = n0 + c;
@@ -1444,15 +1449,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
                             ? *reinterpret_cast<const floatx4*>(p.scale + ncl)
                             : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int hf = 0; hf < WM; ++hf) {
-    if (wr == hf) {
+  for (int hf = 0; hf < WM / EG; ++hf) {
+    if (wr / EG == hf) {
+      const int rb = (wr % EG) * WTM;
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            fsm[(i * 32 + fm_mfma32_row(r, lane)) * PC + wn0 + j * 32 + lcol] = acc[i][j][r];
+            fsm[(rb + i * 32 + fm_mfma32_row(r, lane)) * PC + wn0 + j * 32 + lcol] = acc[i][j][r];
     }
     lds_barrier();
     const long mh = m0 + hf * HM;
@@ -1488,7 +1494,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
         *reinterpret_cast<floatx4*>(p.y + dst) = o;
       }
     }
-    if (hf + 1 < WM) lds_barrier();
+    if (hf + 1 < WM / EG) lds_barrier();
   }
 }
 
@@ -1624,6 +1630,7 @@ constexpr TileCfg kDl128 = {128, 128, 1, 32, 13, 0};
 constexpr TileCfg kX6 = {128, 128, 1, 32, 16, 0};     // bf16x6 tiles (k-tile 16; splits stay 32-aligned); direct-load A
 constexpr TileCfg kX6Big = {256, 128, 1, 32, 17, 0};
 constexpr TileCfg kX6Small = {64, 128, 1, 32, 18, 0};  // direct-load A, four waves of 32x64
+constexpr TileCfg kX6Wide = {192, 128, 1, 32, 19, 0};  // direct-load A, twelve waves, one block per CU
 constexpr TileCfg kDl192 = {192, 128, 1, 32, 14, 0};
 // 64x128 runs one block per CU: 64-deep k-tiles (96 KB ring) halve its barriers.
 constexpr TileCfg kDl64 = {64, 128, 1, 64, 15, 0};
@@ -1801,6 +1808,7 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
       // tile (the 2500-row qkv projection 34 us against 40 us for 64x128
       // tiles, the 8000-row output projection 34 against 37 us).
       cfg = tile_count(M, p.N, kX6Big) >= 384 ? kX6Big : kX6;
+      if (cfg.id == kX6.id && t128 > 256 && tile_count(M, p.N, kX6Wide) <= 256) cfg = kX6Wide;
       tiles = tile_count(M, p.N, cfg);
     }
   }
@@ -1845,6 +1853,10 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
       break;
     case 18:
       hipLaunchKernelGGL((gemm_x6d_kernel<64, 128, 2, 2, 2>), grid, dim3(256), 0, s, p,
+                         reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
+      break;
+    case 19:
+      hipLaunchKernelGGL((gemm_x6d_kernel<192, 128, 6, 2, 2>), grid, dim3(768), 0, s, p,
                          reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
       break;
     case 7: hipLaunchKernelGGL((gemm_mid_kernel<64, 64, 1>), grid, dim3(NTHREADS), 0, s, p); break;

@@ -175,6 +175,7 @@ DL_CASES = [
     (1, 128, 256, 8, 4, 240001, 59990),  # >= 384 256x128 bf16x6 tiles, partial last row tile, crop
     (1, 512, 1536, 1, 1, 2500, None),   # 240 128x128 tiles: 64x128 bf16x6 tiles
     (1, 2048, 512, 1, 1, 2500, 2499),   # long K, 80 tiles: 64x128 bf16x6 tiles split along K
+    (1, 128, 1024, 3, 1, 5000, 4990),   # 320 128x128 tiles: 192x128 bf16x6 tiles, partial, crop
 ]
 
 
@@ -203,7 +204,8 @@ def test_conv1d_direct_load_tiles(B, cin, cout, k, stride, L, y_len, epi, x6, ws
     close(got, want)
 
 
-@pytest.mark.parametrize("B,cin,cout,L", [(1, 512, 256, 2000), (16, 512, 256, 2000), (2, 256, 128, 9001)])
+@pytest.mark.parametrize("B,cin,cout,L", [(1, 512, 256, 2000), (16, 512, 256, 2000), (2, 256, 128, 9001),
+                                          (1, 128, 1024, 5000)])
 def test_conv1d_bf16x6_elu_on_load(B, cin, cout, L, ws):
     """bf16x6 tiles with ELU applied to the A operand as it is loaded (the
     residual block's first conv, k = 3), ELU epilogue, vs float64."""
