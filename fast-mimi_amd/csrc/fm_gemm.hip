@@ -1794,7 +1794,10 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
       // From 160 tiles the direct-load 128x128 tile runs unsplit (no
       // partials, no reduce launch): C2 enc.down5 64 us against 70 us split,
       // C2 dec.up6 53 against 63 us, fc2 at 8000 rows 108 against 117 us.
-      const int s128 = t128 >= 160 ? 1 : fewest(kX6, 4);
+      // At most one tile per CU with K >= 2048 splits in two instead, so
+      // each CU holds two blocks (C3 enc.down8 495 -> 460 us, C4 dec.first
+      // 178 -> 150 us).
+      const int s128 = t128 < 160 ? fewest(kX6, 4) : (t128 <= 256 && p.K >= 2048) ? 2 : 1;
       if (t128 * s128 >= 360 || s128 == 1) {
         cfg = kX6;
         splits = s128;
