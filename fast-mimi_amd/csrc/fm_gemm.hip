@@ -1801,6 +1801,9 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
       if (t128 * s128 >= 360 || s128 == 1) {
         cfg = kX6;
         splits = s128;
+        // Unsplit with two tiles on some CUs: 192x128 tiles, one per CU,
+        // when they fit in one round (C4 res512.c1 at 20000 rows).
+        if (s128 == 1 && t128 > 256 && tile_count(M, p.N, kX6Wide) <= 256) cfg = kX6Wide;
       } else {
         cfg = kX6Small;
         splits = fewest(kX6Small, 8);

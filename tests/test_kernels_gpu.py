@@ -206,7 +206,7 @@ def test_conv1d_direct_load_tiles(B, cin, cout, k, stride, L, y_len, epi, x6, ws
 
 
 @pytest.mark.parametrize("B,cin,cout,L", [(1, 512, 256, 2000), (16, 512, 256, 2000), (2, 256, 128, 9001),
-                                          (1, 128, 1024, 5000)])
+                                          (1, 128, 1024, 5000), (1, 512, 256, 16500)])
 def test_conv1d_bf16x6_elu_on_load(B, cin, cout, L, ws):
     """bf16x6 tiles with ELU applied to the A operand as it is loaded (the
     residual block's first conv, k = 3), ELU epilogue, vs float64."""
