@@ -84,12 +84,30 @@ FM_DEVICE floatx16 fm_mfma32_bf16(bf16x8 a, bf16x8 b, floatx16 c) {
 }
 
 // v = h0 + h1 + h2 (+ a residual below 2^-24 |v|), each a round-to-nearest bf16.
+// Pairs are converted with one packed conversion whose two halves, widened
+// back by a shift and a mask, give the residuals: the same values as
+// converting each element and widening it, in fewer instructions.
 FM_DEVICE void split3(floatx4 v, bf16x4& h0, bf16x4& h1, bf16x4& h2) {
-  h0 = __builtin_convertvector(v, bf16x4);
-  const floatx4 r1 = v - __builtin_convertvector(h0, floatx4);
-  h1 = __builtin_convertvector(r1, bf16x4);
-  const floatx4 r2 = r1 - __builtin_convertvector(h1, floatx4);
-  h2 = __builtin_convertvector(r2, bf16x4);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float floatx2_t __attribute__((ext_vector_type(2)));
+  typedef unsigned uintx2_t __attribute__((ext_vector_type(2)));
+  auto pack = [](float a, float b) {
+    return __builtin_bit_cast(unsigned, __builtin_convertvector((floatx2_t{a, b}), bf16x2_t));
+  };
+  auto lo = [](unsigned u) { return __builtin_bit_cast(float, u << 16); };
+  auto hi = [](unsigned u) { return __builtin_bit_cast(float, u & 0xffff0000u); };
+  unsigned p0[2], p1[2], p2[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const float a = v[2 * q], b = v[2 * q + 1];
+    p0[q] = pack(a, b);
+    const float ra = a - lo(p0[q]), rb = b - hi(p0[q]);
+    p1[q] = pack(ra, rb);
+    p2[q] = pack(ra - lo(p1[q]), rb - hi(p1[q]));
+  }
+  h0 = __builtin_bit_cast(bf16x4, (uintx2_t{p0[0], p0[1]}));
+  h1 = __builtin_bit_cast(bf16x4, (uintx2_t{p1[0], p1[1]}));
+  h2 = __builtin_bit_cast(bf16x4, (uintx2_t{p2[0], p2[1]}));
 }
 
 static inline int fm_ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
