@@ -1076,7 +1076,7 @@ __global__ __launch_bounds__(256) void split_weights_kernel(const float* __restr
   out[2 * n4 + o] = h2;
 }
 
-template <int BM, int BN, int WM, int WN, int NST>
+template <int BM, int BN, int WM, int WN, int NST, bool ELU>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_x6_kernel(GemmArgs p, const __bf16* __restrict__ w3) {
   constexpr int NW = WM * WN, NTH = 64 * NW, BK = 16;
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
@@ -1136,7 +1136,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6_kernel(GemmArgs p, const
       areg[i] = *reinterpret_cast<const floatx4*>(ok ? a_row[i] + k0 : g_zero16);
     }
   };
-  const bool elu_in = p.flags & FM_ELU_IN;
+  constexpr bool elu_in = ELU;  // ELU on load (a separate instantiation)
   auto store_a = [&](int stage) {
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
@@ -1854,8 +1854,12 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
                          reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
       break;
     case 17:
-      hipLaunchKernelGGL((gemm_x6_kernel<256, 128, 2, 4, 2>), grid, dim3(512), 0, s, p,
-                         reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
+      if (p.flags & FM_ELU_IN)
+        hipLaunchKernelGGL((gemm_x6_kernel<256, 128, 2, 4, 2, true>), grid, dim3(512), 0, s, p,
+                           reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
+      else
+        hipLaunchKernelGGL((gemm_x6_kernel<256, 128, 2, 4, 2, false>), grid, dim3(512), 0, s, p,
+                           reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
       break;
     case 18:
       hipLaunchKernelGGL((gemm_x6d_kernel<64, 128, 2, 2, 2>), grid, dim3(256), 0, s, p,
