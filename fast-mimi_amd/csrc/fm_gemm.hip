@@ -1297,7 +1297,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6_kernel(GemmArgs p, const
 // read (32 x 64 wave tiles in two columns, so an A fragment is split by two
 // waves; 4, 8 or 12 waves), which takes the register staging and its wait out of the k-loop.  Same six
 // products in the same order as gemm_x6_kernel, so the same results.
-template <int BM, int BN, int WM, int WN, int NST>
+template <int BM, int BN, int WM, int WN, int NST, bool ELU>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, const __bf16* __restrict__ w3) {
   constexpr int NW = WM * WN, NTH = 64 * NW, BK = 16;
   static_assert((NW == 12 || NW == 8 || NW == 4) && NST == 2, "twelve, eight or four waves, two stages");
@@ -1375,7 +1375,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   const int lrow = lane & 31, lk = lane >> 5;
-  const bool elu_in = p.flags & FM_ELU_IN;
+  constexpr bool elu_in = ELU;  // ELU on load (a separate instantiation)
   const int nkt = (k_end - k_begin) / BK;
   if (nkt > 0) issue(0, k_begin);
   for (int kt = 0; kt < nkt; ++kt) {
@@ -1850,8 +1850,12 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     case 14: hipLaunchKernelGGL((gemm_dl_kernel<192, 128, 4, 32, 2, 4>), grid, dim3(512), 0, s, p); break;
     case 15: hipLaunchKernelGGL((gemm_dl_kernel<64, 128, 4, 64, 2, 4>), grid, dim3(512), 0, s, p); break;
     case 16:
-      hipLaunchKernelGGL((gemm_x6d_kernel<128, 128, 4, 2, 2>), grid, dim3(512), 0, s, p,
-                         reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
+      if (p.flags & FM_ELU_IN)
+        hipLaunchKernelGGL((gemm_x6d_kernel<128, 128, 4, 2, 2, true>), grid, dim3(512), 0, s, p,
+                           reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
+      else
+        hipLaunchKernelGGL((gemm_x6d_kernel<128, 128, 4, 2, 2, false>), grid, dim3(512), 0, s, p,
+                           reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
       break;
     case 17:
       if (p.flags & FM_ELU_IN)
@@ -1862,12 +1866,20 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
                            reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
       break;
     case 18:
-      hipLaunchKernelGGL((gemm_x6d_kernel<64, 128, 2, 2, 2>), grid, dim3(256), 0, s, p,
-                         reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
+      if (p.flags & FM_ELU_IN)
+        hipLaunchKernelGGL((gemm_x6d_kernel<64, 128, 2, 2, 2, true>), grid, dim3(256), 0, s, p,
+                           reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
+      else
+        hipLaunchKernelGGL((gemm_x6d_kernel<64, 128, 2, 2, 2, false>), grid, dim3(256), 0, s, p,
+                           reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
       break;
     case 19:
-      hipLaunchKernelGGL((gemm_x6d_kernel<192, 128, 6, 2, 2>), grid, dim3(768), 0, s, p,
-                         reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
+      if (p.flags & FM_ELU_IN)
+        hipLaunchKernelGGL((gemm_x6d_kernel<192, 128, 6, 2, 2, true>), grid, dim3(768), 0, s, p,
+                           reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
+      else
+        hipLaunchKernelGGL((gemm_x6d_kernel<192, 128, 6, 2, 2, false>), grid, dim3(768), 0, s, p,
+                           reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
       break;
     case 7: hipLaunchKernelGGL((gemm_mid_kernel<64, 64, 1>), grid, dim3(NTHREADS), 0, s, p); break;
     case 8: hipLaunchKernelGGL((gemm_mid_kernel<32, 32, 4>), grid, dim3(NTHREADS), 0, s, p); break;
