@@ -100,7 +100,7 @@ def dominant_kernel(model: MimiModel, name: str, batch: int, samples: int, nq: i
     ms = start.elapsed_time(stop) / iters
     del graph
     achieved = flops / (ms * 1e-3) / 1e12
-    return {"bound": "mfma", "kernel": f"gemm_x6_kernel ({name}: {row[1]} rows={row[3]} K={row[4]} N={row[5]})",
+    return {"bound": "mfma", "kernel": f"gemm_x6d_kernel<256,128,8,1> ({name}: {row[1]} rows={row[3]} K={row[4]} N={row[5]})",
             "flops_per_launch": flops, "avg_launch_ms": ms, "achieved": round(achieved, 3),
             "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
             "traffic": None,

@@ -1045,19 +1045,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int spli
 // v_mfma_f32_32x32x16_bf16 delivers 16x the FP32 MFMA rate: six of them cost
 // 0.375 of the FP32 instruction time per k.
 // Weights are split once (fm_split_weights) into planes [3][K/16][N][16]
-// stored right after the FP32 W^T; A tiles are split as they are staged: each
-// thread loads one float4 of the 128 x 16 k-tile, splits it and writes the
-// three 8-byte pieces, so each A element is split once per block.  B planes
-// travel global -> LDS directly (global_load_lds_dwordx4; 32 rows of a k-tile
-// are one contiguous 1 KB run of the k16-tile ordered planes).  LDS rows are 32
-// bytes (16 k of bf16) and a wave's fragment read is 1 KB contiguous
-// (row l % 32, k half l / 32), so neither the 8-byte writes nor the 16-byte
-// reads conflict.  Two stages, one barrier per 16-deep k-tile; the epilogue
-// runs one wave row at a time through LDS.  Tiles: 256 x 128 (eight waves of
-// 128 x 32, 72 KB, two blocks per CU) where it gives at least 384 tiles,
-// else 128 x 128 (waves of 64 x 32, 48 KB).  Measured against the FP32
-// direct-load tile on the SEANet shapes: 1.3-1.5x (dec.up4 at C2 55 vs 80 us,
-// at C3 0.81 vs 1.07 ms).
+// stored right after the FP32 W^T; A tiles reach LDS as FP32 and each wave
+// splits its own fragments (gemm_x6d_kernel below).  Measured against the
+// FP32 direct-load tile on the SEANet shapes: 1.3-1.5x.
 // W^T [N][K] fp32 -> three bf16 planes in k16-tile order [3][K/16][N][16]:
 // the 16 k of one row are 32 contiguous bytes and the rows of a k-tile are
 // adjacent, so 32 rows of one k-tile are one 1 KB run.
@@ -1076,231 +1066,26 @@ __global__ __launch_bounds__(256) void split_weights_kernel(const float* __restr
   out[2 * n4 + o] = h2;
 }
 
-template <int BM, int BN, int WM, int WN, int NST, bool ELU>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_x6_kernel(GemmArgs p, const __bf16* __restrict__ w3) {
-  constexpr int NW = WM * WN, NTH = 64 * NW, BK = 16;
-  constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
-  constexpr int APT = BM * BK / (4 * NTH);  // float4 A loads per thread per k-tile
-  static_assert(FM >= 1 && FN >= 1 && APT >= 1 && APT * 4 * NTH == BM * BK && BN % 32 == 0, "tiling");
-  constexpr int PLANE_A = BM * BK * 2, PLANE_B = BN * BK * 2;
-  constexpr int STAGE_B = 3 * (PLANE_A + PLANE_B);
-  constexpr int NBI = 3 * BN / 32;  // 1 KB B load instructions per k-tile
-  constexpr int HM = WTM, PC = BN + 4, TILE_B = HM * PC * 4;
-  __shared__ __attribute__((aligned(16))) char smem[NST * STAGE_B > TILE_B ? NST * STAGE_B : TILE_B];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wr = wave / WN;
-  const int wm0 = wr * WTM, wn0 = (wave % WN) * WTN;
-  const long M = (long)p.batch * p.rows;
-  const int tiles_n = (p.N + BN - 1) / BN;
-  const int tile = tile_index();
-  const long m0 = (long)(tile / tiles_n) * BM;
-  const int n0 = (tile % tiles_n) * BN;
-  const int k_begin = blockIdx.y * p.k_split;
-  const int k_end = min(p.K, k_begin + p.k_split);
-
-  const float* a_row[APT];
-  int a_p0[APT], a_off[APT];
-#pragma unroll
-  for (int i = 0; i < APT; ++i) {
-    const int e = tid + i * NTH;           // float4 index within the k-tile
-    const int ar = e >> 2, ac = e & 3;
-    const long mm = m0 + ar;
-    const int m = (int)min(mm, M - 1);
-    const int b = (int)fm_div((unsigned)m, p.rows_div);
-    const int t = m - b * p.rows;
-    a_p0[i] = mm < M ? t * p.rs - p.padL : INT_MIN / 2;
-    a_row[i] = p.x + (long)b * p.L_in * p.C_in + (long)a_p0[i] * p.C_in + 4 * ac;
-    a_off[i] = ar * (BK * 2) + ac * 8;
-  }
-  const long KN = (long)p.K * p.N;
-  auto issue_b = [&](int stage, int k0) {
-    char* Bs = smem + stage * STAGE_B + 3 * PLANE_A;
-#pragma unroll
-    for (int i = wave; i < NBI; i += NW) {
-      const int pl = i / (BN / 32), rg = i % (BN / 32);
-      const int row = rg * 32 + (lane >> 1);
-      const void* src = (n0 + row < p.N) ? (const void*)(w3 + pl * KN + ((long)(k0 >> 4) * p.N + n0 + row) * 16 + 8 * (lane & 1))
-                                         : (const void*)g_zero16;
-      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)src,
-                                       (__attribute__((address_space(3))) void*)(Bs + pl * PLANE_B + rg * 32 * BK * 2),
-                                       16, 0, 0);
-    }
-  };
-  floatx4 areg[APT];
-  auto load_a = [&](int k0) {
-    const int tap = k0 / p.C_in;
-#pragma unroll
-    for (int i = 0; i < APT; ++i) {
-      const bool ok = (unsigned)(a_p0[i] + tap) < (unsigned)p.L_in;
-      areg[i] = *reinterpret_cast<const floatx4*>(ok ? a_row[i] + k0 : g_zero16);
-    }
-  };
-  constexpr bool elu_in = ELU;  // ELU on load (a separate instantiation)
-  auto store_a = [&](int stage) {
-#pragma unroll
-    for (int i = 0; i < APT; ++i) {
-      bf16x4 h0, h1, h2;
-      floatx4 v = areg[i];
-      if (elu_in) v = floatx4{fm_elu(v[0]), fm_elu(v[1]), fm_elu(v[2]), fm_elu(v[3])};
-      split3(v, h0, h1, h2);
-      char* As = smem + stage * STAGE_B + a_off[i];
-      *reinterpret_cast<bf16x4*>(As) = h0;
-      *reinterpret_cast<bf16x4*>(As + PLANE_A) = h1;
-      *reinterpret_cast<bf16x4*>(As + 2 * PLANE_A) = h2;
-    }
-  };
-
-  floatx16 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  const int lrow = lane & 31, lk = lane >> 5;
-  const int nkt = (k_end - k_begin) / BK;
-  // Prologue: stages 0 .. NST-2 filled.
-#pragma unroll
-  for (int s0 = 0; s0 < NST - 1; ++s0) {
-    if (s0 < nkt) {
-      issue_b(s0, k_begin + s0 * BK);
-      load_a(k_begin + s0 * BK);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      store_a(s0);
-    }
-  }
-  for (int kt = 0; kt < nkt; ++kt) {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    const int kn = kt + NST - 1;
-    const bool more = kn < nkt;
-    if (more) {
-      issue_b(kn % NST, k_begin + kn * BK);
-      load_a(k_begin + kn * BK);
-    }
-    const char* As = smem + (kt % NST) * STAGE_B;
-    const char* Bs = As + 3 * PLANE_A;
-    // Planes in order 0, 1, 2 so at most two planes of fragments are live
-    // (a 128 x 32 wave tile then fits the 128 registers of two blocks per CU).
-    auto rd_a = [&](int pl, bf16x8* a) {
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-        a[i] = *reinterpret_cast<const bf16x8*>(As + pl * PLANE_A + (wm0 + 32 * i + lrow) * (BK * 2) + lk * 16);
-    };
-    auto rd_b = [&](int pl, bf16x8* b) {
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        b[j] = *reinterpret_cast<const bf16x8*>(Bs + pl * PLANE_B + (wn0 + 32 * j + lrow) * (BK * 2) + lk * 16);
-    };
-    bf16x8 a0[FM], b0[FN], a1[FM], b1[FN];
-    rd_a(0, a0); rd_b(0, b0); rd_a(1, a1); rd_b(1, b1);
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        acc[i][j] = fm_mfma32_bf16(a1[i], b1[j], acc[i][j]);
-        acc[i][j] = fm_mfma32_bf16(a1[i], b0[j], acc[i][j]);
-        acc[i][j] = fm_mfma32_bf16(a0[i], b1[j], acc[i][j]);
-      }
-    rd_a(2, a1); rd_b(2, b1);
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        acc[i][j] = fm_mfma32_bf16(a1[i], b0[j], acc[i][j]);
-        acc[i][j] = fm_mfma32_bf16(a0[i], b1[j], acc[i][j]);
-        acc[i][j] = fm_mfma32_bf16(a0[i], b0[j], acc[i][j]);
-      }
-    if (more) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      store_a(kn % NST);
-    }
-  }
-  lds_barrier();
-
-  // Epilogue: WM passes of one wave row (WTM rows) through LDS.
-  float* fsm = reinterpret_cast<float*>(smem);
-  const int lcol = lane & 31;
-  const bool crop = p.y_rows != p.rows;
-  const bool has_res = p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE);
-  float* part = p.partial ? p.partial + (long)blockIdx.y * M * p.N : nullptr;
-  constexpr int CG = BN / 4, RSTEP = NTH / CG, NRUN = HM / RSTEP, RB = NRUN < 2 ? NRUN : 2;
-  static_assert(NTH % CG == 0 && HM % RSTEP == 0 && NRUN % RB == 0, "epilogue runs");
-  const int c = (tid % CG) * 4, r0 = tid / CG;
-  const int n = n0 + c;
-  const bool n_ok = n < p.N;
-  const int ncl = n_ok ? n : 0;
-  const floatx4 bias = (p.bias && !part) ? *reinterpret_cast<const floatx4*>(p.bias + ncl % p.bias_len)
-                                         : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-  const floatx4 scale = ((p.flags & FM_EPI_RES_SCALE) && !part)
-                            ? *reinterpret_cast<const floatx4*>(p.scale + ncl)
-                            : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int hf = 0; hf < WM; ++hf) {
-    if (wr == hf) {
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            fsm[(i * 32 + fm_mfma32_row(r, lane)) * PC + wn0 + j * 32 + lcol] = acc[i][j][r];
-    }
-    lds_barrier();
-    const long mh = m0 + hf * HM;
-#pragma unroll
-    for (int u0 = 0; u0 < NRUN; u0 += RB) {
-      floatx4 v[RB], res[RB];
-#pragma unroll
-      for (int u = 0; u < RB; ++u) {
-        const int r = r0 + (u0 + u) * RSTEP;
-        const long m = min(mh + r, M - 1);
-        v[u] = *reinterpret_cast<const floatx4*>(fsm + r * PC + c);
-        res[u] = (has_res && !part) ? *reinterpret_cast<const floatx4*>(p.res + m * p.N + ncl)
-                                    : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-      }
-#pragma unroll
-      for (int u = 0; u < RB; ++u) {
-        const long m = mh + r0 + (u0 + u) * RSTEP;
-        if (m >= M || !n_ok) continue;
-        if (part) {
-          *reinterpret_cast<floatx4*>(part + m * p.N + n) = v[u];
-          continue;
-        }
-        floatx4 o = v[u];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = epilogue_v(o[e], bias[e], res[u][e], scale[e], p.flags);
-        long dst = m * p.N + n;
-        if (crop) {
-          const int b = (int)(m / p.rows);
-          const int t = (int)(m - (long)b * p.rows);
-          if (t >= p.y_rows) continue;
-          dst = ((long)b * p.y_rows + t) * p.N + n;
-        }
-        *reinterpret_cast<floatx4*>(p.y + dst) = o;
-      }
-    }
-    if (hf + 1 < WM) lds_barrier();
-  }
-}
-
 // ---------------------------------------------------------------------------
 // bf16x6 tile with the FP32 A operand loaded global -> LDS directly: each
 // lane's 16-byte chunk of the 16-deep A k-tile lands in an XOR-swizzled slot
 // (chunk c of row r at position c ^ ((r / 4) & 3), so the 16-lane groups of a
 // fragment read hit distinct banks) with the zero page for out-of-window and
-// past-M rows, next to the B planes as in gemm_x6_kernel; NST-stage ring, one
-// barrier per k-tile.  Each wave splits its own A fragments after the LDS
-// read (32 x 64 wave tiles in two columns, so an A fragment is split by two
-// waves; 4, 8 or 12 waves), which takes the register staging and its wait out of the k-loop.  Same six
-// products in the same order as gemm_x6_kernel, so the same results.
+// past-M rows; the B planes travel global -> LDS directly too
+// (global_load_lds_dwordx4; 32 rows of a k-tile are one contiguous 1 KB run
+// of the k16-tile ordered planes, LDS rows of 32 bytes read as 1 KB
+// fragments).  NST-stage ring, one barrier per k-tile.  Each wave splits its
+// own A fragments after the LDS read, so no register staging or wait sits in
+// the k-loop; a wave tile spanning the block's columns (WN = 1: 32 x 128)
+// splits every A element once, narrower ones (32 x 64) twice.  Products in
+// the order a1b1, a1b0, a0b1, a2b0, a0b2, a0b0 per k-tile.  Tiles: 256 x 128
+// (eight waves of 32 x 128, 56 KB, two blocks per CU) where it gives at least
+// 384 tiles; 128 x 128 / 64 x 128 / 192 x 128 (waves of 32 x 64) for smaller
+// grids.
 template <int BM, int BN, int WM, int WN, int NST, bool ELU>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, const __bf16* __restrict__ w3) {
   constexpr int NW = WM * WN, NTH = 64 * NW, BK = 16;
-  static_assert((NW == 12 || NW == 8 || NW == 4) && NST == 2, "twelve, eight or four waves, two stages");
+  static_assert(NW % 2 == 0 && NW <= 12 && NST == 2, "two to twelve waves, two stages");
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
   constexpr int CPR = 4, RPI = 16, SWR = 4;  // A: chunks per row, rows per load instruction
   constexpr int AI = BM / (NW * RPI);        // A load instructions per wave per stage
@@ -1850,8 +1635,10 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     case 14: hipLaunchKernelGGL((gemm_dl_kernel<192, 128, 4, 32, 2, 4>), grid, dim3(512), 0, s, p); break;
     case 15: hipLaunchKernelGGL((gemm_dl_kernel<64, 128, 4, 64, 2, 4>), grid, dim3(512), 0, s, p); break;
     case 16:
+      // ELU on load: four waves of 32 x 128, so each A element's ELU and
+      // split run once (C3 res512.c1 230 -> 191 us against two 32 x 64 waves).
       if (p.flags & FM_ELU_IN)
-        hipLaunchKernelGGL((gemm_x6d_kernel<128, 128, 4, 2, 2, true>), grid, dim3(512), 0, s, p,
+        hipLaunchKernelGGL((gemm_x6d_kernel<128, 128, 4, 1, 2, true>), grid, dim3(256), 0, s, p,
                            reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
       else
         hipLaunchKernelGGL((gemm_x6d_kernel<128, 128, 4, 2, 2, false>), grid, dim3(512), 0, s, p,
@@ -1859,10 +1646,10 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
       break;
     case 17:
       if (p.flags & FM_ELU_IN)
-        hipLaunchKernelGGL((gemm_x6_kernel<256, 128, 2, 4, 2, true>), grid, dim3(512), 0, s, p,
+        hipLaunchKernelGGL((gemm_x6d_kernel<256, 128, 8, 1, 2, true>), grid, dim3(512), 0, s, p,
                            reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
       else
-        hipLaunchKernelGGL((gemm_x6_kernel<256, 128, 2, 4, 2, false>), grid, dim3(512), 0, s, p,
+        hipLaunchKernelGGL((gemm_x6d_kernel<256, 128, 8, 1, 2, false>), grid, dim3(512), 0, s, p,
                            reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
       break;
     case 18:
