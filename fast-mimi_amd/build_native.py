@@ -46,7 +46,10 @@ def build(jobs: int | None = None) -> Path:
     with ThreadPoolExecutor(max_workers=jobs or min(8, len(sources))) as pool:
         objects = list(pool.map(_compile, sources))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    # --no-undefined: a kernel whose host stub was not emitted fails the
+    # link here instead of the library load on the GPU box.
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,--no-undefined", *map(str, objects),
+           "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")

@@ -141,6 +141,11 @@ FM_DEVICE __amdgpu_buffer_rsrc_t fm_buffer(const void* base, int bytes) {
 FM_DEVICE floatx4 fm_buf_load4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
   return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
+// 16 bytes per lane from a buffer straight into LDS (lane l's bytes at
+// lds + 16 l); out-of-range offsets read zeros.
+FM_DEVICE void fm_buf_load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
 FM_DEVICE float fm_buf_load1(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }

@@ -1127,6 +1127,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
     a_row[i] = p.x + (long)b * p.L_in * p.C_in + (long)a_p0[i] * p.C_in + 4 * (cp ^ ((r / SWR) & (CPR - 1)));
   }
   const long KN = (long)p.K * p.N;
+  // B plane loads through a buffer resource over the three planes: lane
+  // offsets computed once, out-of-range (past-N) lanes read zeros.
+  constexpr int NBW = (NBI + NW - 1) / NW;  // B load instructions per wave (at most)
+  const __amdgpu_buffer_rsrc_t rb = fm_buffer(w3, (int)(3 * KN * 2));
+  int b_voff[NBW], b_lds[NBW];
+#pragma unroll
+  for (int q = 0; q < NBW; ++q) {
+    const int i = min(wave + q * NW, NBI - 1);
+    const int pl = i / (BN / 32), rg = i % (BN / 32);
+    const int row = rg * 32 + (lane >> 1);
+    b_voff[q] = n0 + row < p.N ? (int)((pl * KN + (long)(n0 + row) * 16 + 8 * (lane & 1)) * 2) : INT_MIN;
+    b_lds[q] = pl * PLANE_B + rg * 32 * BK * 2;
+  }
   auto issue = [&](int stage, int k0) {
     char* As = smem + stage * STAGE;
     char* Bs = As + STAGE_A;
@@ -1139,15 +1152,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
                                        (__attribute__((address_space(3))) void*)(As + (wave * AI + i) * RPI * BK * 4),
                                        16, 0, 0);
     }
+    // B: per-lane offsets fixed for the whole loop, the k-tile's place in
+    // the planes as the scalar offset; past-N columns read out of range (zero).
+    const int soff = (k0 >> 4) * p.N * 32;
 #pragma unroll
-    for (int i = wave; i < NBI; i += NW) {
-      const int pl = i / (BN / 32), rg = i % (BN / 32);
-      const int row = rg * 32 + (lane >> 1);
-      const void* src = (n0 + row < p.N) ? (const void*)(w3 + pl * KN + ((long)(k0 >> 4) * p.N + n0 + row) * 16 + 8 * (lane & 1))
-                                         : (const void*)g_zero16;
-      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)src,
-                                       (__attribute__((address_space(3))) void*)(Bs + pl * PLANE_B + rg * 32 * BK * 2),
-                                       16, 0, 0);
+    for (int q = 0; q < NBW; ++q) {
+      const int i = wave + q * NW;
+      if (i < NBI)
+        fm_buf_load_lds16(rb, Bs + b_lds[q], b_voff[q], soff);
     }
   };
 
