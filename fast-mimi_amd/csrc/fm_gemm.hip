@@ -1115,7 +1115,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
   // cp (global chunk cp ^ swizzle).
   const int lr = lane / CPR, cp = lane % CPR;
   const float* a_row[AI];
-  int a_p0[AI];
+  int a_p0[AI], a_voff[AI];
 #pragma unroll
   for (int i = 0; i < AI; ++i) {
     const int r = (wave * AI + i) * RPI + lr;
@@ -1125,7 +1125,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
     const int t = m - b * p.rows;
     a_p0[i] = mm < M ? t * p.rs - p.padL : INT_MIN / 2;
     a_row[i] = p.x + (long)b * p.L_in * p.C_in + (long)a_p0[i] * p.C_in + 4 * (cp ^ ((r / SWR) & (CPR - 1)));
+    a_voff[i] = (int)((a_row[i] - p.x) * 4);
   }
+  // Inputs below 2 GiB load A through a buffer resource too: per k-tile only
+  // the window test and a select on a 32-bit offset (out-of-window and past-M
+  // rows read out of range, i.e. zeros).
+  const long x_bytes = (long)p.batch * p.L_in * p.C_in * 4;
+  const bool a_buf = x_bytes < 0x7fffffffL;
+  const __amdgpu_buffer_rsrc_t ra = fm_buffer(p.x, a_buf ? (int)x_bytes : 0);
   const long KN = (long)p.K * p.N;
   // B plane loads through a buffer resource over the three planes: lane
   // offsets computed once, out-of-range (past-N) lanes read zeros.
@@ -1144,13 +1151,22 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
     char* As = smem + stage * STAGE;
     char* Bs = As + STAGE_A;
     const int tap = k0 / p.C_in;  // uniform: a k-tile lies in one tap
+    if (a_buf) {
+      const int tap_off = tap * p.C_in * 4, soff = k0 * 4 - tap_off;
 #pragma unroll
-    for (int i = 0; i < AI; ++i) {
-      const bool ok = (unsigned)(a_p0[i] + tap) < (unsigned)p.L_in;
-      const float* src = ok ? a_row[i] + k0 : g_zero16;
-      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)src,
-                                       (__attribute__((address_space(3))) void*)(As + (wave * AI + i) * RPI * BK * 4),
-                                       16, 0, 0);
+      for (int i = 0; i < AI; ++i) {
+        const bool ok = (unsigned)(a_p0[i] + tap) < (unsigned)p.L_in;
+        fm_buf_load_lds16(ra, As + (wave * AI + i) * RPI * BK * 4, ok ? a_voff[i] + tap_off : INT_MIN, soff);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < AI; ++i) {
+        const bool ok = (unsigned)(a_p0[i] + tap) < (unsigned)p.L_in;
+        const float* src = ok ? a_row[i] + k0 : g_zero16;
+        __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)src,
+                                         (__attribute__((address_space(3))) void*)(As + (wave * AI + i) * RPI * BK * 4),
+                                         16, 0, 0);
+      }
     }
     // B: per-lane offsets fixed for the whole loop, the k-tile's place in
     // the planes as the scalar offset; past-N columns read out of range (zero).
