@@ -590,25 +590,31 @@ __global__ __launch_bounds__(NT, 3) void resblock_x6_kernel(
   }
   // Weight ring: unit u is 32 k of one 32-row weight slice, three planes,
   // two MFMA steps each.
-  const __bf16* w1p = w1x + (wc * 32 + lcol) * 16 + 8 * h;
-  const __bf16* w2p = w2x + (wc * 64 + lcol) * 16 + 8 * h;
+  // Weight fragments through buffer resources: the lane's offset is fixed,
+  // each unit's place in the planes is a scalar offset, so the streamed
+  // loads take no vector address arithmetic.
+  const __amdgpu_buffer_rsrc_t rw1 = fm_buffer(w1x, 3 * HC * K1 * 2);
+  const __amdgpu_buffer_rsrc_t rw2 = fm_buffer(w2x, 3 * C * HC * 2);
+  const int w1v = ((wc * 32 + lcol) * 16 + 8 * h) * 2, w2v = ((wc * 64 + lcol) * 16 + 8 * h) * 2;
   bf16x8 ring[PD][3][2];
   auto load_unit = [&](int u, bf16x8 (&d)[3][2]) {
-    const __bf16* src;
-    long plane;
+    int base, plane;  // elements
     if (u < T1) {
-      src = w1p + u * 2 * HC * 16;
-      plane = (long)HC * K1;
+      base = u * 2 * HC * 16;
+      plane = HC * K1;
     } else {
       const int v = u - T1, kt = v / FN2, j = v % FN2;
-      src = w2p + (long)(j * 32 + kt * 2 * C) * 16;
-      plane = (long)C * HC;
+      base = (j * 32 + kt * 2 * C) * 16;
+      plane = C * HC;
     }
     const int tile = u < T1 ? HC * 16 : C * 16;  // elements per k16 tile of a plane
 #pragma unroll
     for (int pl = 0; pl < 3; ++pl)
 #pragma unroll
-      for (int s = 0; s < 2; ++s) d[pl][s] = *reinterpret_cast<const bf16x8*>(src + pl * plane + s * tile);
+      for (int s = 0; s < 2; ++s) {
+        const int soff = (base + pl * plane + s * tile) * 2;
+        d[pl][s] = __builtin_bit_cast(bf16x8, u < T1 ? fm_buf_load4(rw1, w1v, soff) : fm_buf_load4(rw2, w2v, soff));
+      }
   };
 #pragma unroll
   for (int d = 0; d < PD; ++d) load_unit(d, ring[d]);
