@@ -1092,11 +1092,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
   static_assert(AI >= 1 && AI * NW * RPI == BM && FM >= 1 && FN >= 1 && BN % 32 == 0, "tiling");
   constexpr int PLANE_B = BN * BK * 2, STAGE_A = BM * BK * 4, STAGE = STAGE_A + 3 * PLANE_B;
   constexpr int NBI = 3 * BN / 32;  // 1 KB B load instructions per stage
-  // Epilogue passes of EG wave rows (EG the fewest that the block's rows
-  // per store step divide).
-  constexpr int CG = BN / 4, RSTEP = NTH / CG;
-  constexpr int EG = (WTM % RSTEP == 0) ? 1 : (2 * WTM % RSTEP == 0 && WM % 2 == 0) ? 2 : 3;
-  constexpr int HM = EG * WTM, PC = BN + 4, TILE_B = HM * PC * 4;
+  // Epilogue passes of EG wave rows: the most that fit in the k-loop's LDS
+  // (fewer passes, fewer barriers), else the fewest that the block's rows
+  // per store step divide.
+  constexpr int CG = BN / 4, RSTEP = NTH / CG, PC = BN + 4;
+  constexpr int EG0 = (WTM % RSTEP == 0) ? 1 : (2 * WTM % RSTEP == 0 && WM % 2 == 0) ? 2 : 3;
+  constexpr auto fits = [](int g) { return WM % g == 0 && (g * WTM) % RSTEP == 0 && g * WTM * PC * 4 <= NST * STAGE; };
+  constexpr int EG = fits(4) ? 4 : fits(3) ? 3 : fits(2) ? 2 : EG0;
+  constexpr int HM = EG * WTM, TILE_B = HM * PC * 4;
   static_assert(WM % EG == 0 && HM % RSTEP == 0, "epilogue passes");
   __shared__ __attribute__((aligned(16))) char smem[NST * STAGE > TILE_B ? NST * STAGE : TILE_B];
 
