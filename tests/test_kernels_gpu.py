@@ -205,6 +205,38 @@ def test_conv1d_direct_load_tiles(B, cin, cout, k, stride, L, y_len, epi, x6, ws
     close(got, want)
 
 
+def test_bf16x6_large_input_loads_agree(ws):
+    """The direct-load bf16x6 tiles read A through a buffer resource when the
+    input is below 2 GiB and through global addresses above it: a 2.3 GiB
+    two-clip input (global path) must give, for its second clip, exactly the
+    output of that clip alone (buffer path), causal edge included."""
+    B, cin, cout, k, stride = 2, 64, 128, 8, 4
+    L = 4_500_000  # 1.15 GB of channels-last input per clip
+    g = torch.Generator(device=DEV).manual_seed(5)
+    x = torch.randn(B, L, cin, device=DEV, generator=g)
+    w = torch.randn(cout, cin, k, generator=torch.Generator().manual_seed(6)) / math.sqrt(cin * k)
+    layer = _Conv(w.to(DEV), None, stride, "constant")
+    wx = with_planes(layer.w)
+    rows = -(-L // stride)
+    outs = []
+    for xb, bb in ((x, B), (x[1:].contiguous(), 1)):
+        y = torch.empty((bb, rows, cout), device=DEV)
+        nat.call("fm_conv1d", xb.data_ptr(), bb, L, cin, wx.data_ptr(), None, cout, k, stride, 0,
+                 nat.WEIGHTS_X6, None, y.data_ptr(), rows, ws.data_ptr(), WS_BYTES, stream())
+        torch.cuda.synchronize()
+        outs.append(y[-1].clone())
+        del y
+    assert torch.equal(outs[0], outs[1])
+    # A few rows against float64 (the causal edge and an interior window):
+    # y[t] = sum_j W[:, :, j] x[t * stride - (k - stride) + j], zero outside.
+    wd = w.double()
+    for t in (0, 1, rows // 2):
+        idx = torch.arange(k) + t * stride - (k - stride)
+        xs = x[1, idx.clamp(0, L - 1)].double().cpu() * ((idx >= 0) & (idx < L)).double()[:, None]
+        want = torch.einsum("jc,ocj->o", xs, wd)
+        close(outs[1][t].cpu()[None], want[None])
+
+
 @pytest.mark.parametrize("B,cin,cout,L", [(1, 512, 256, 2000), (16, 512, 256, 2000), (2, 256, 128, 9001),
                                           (1, 128, 1024, 5000), (1, 512, 256, 16500)])
 def test_conv1d_bf16x6_elu_on_load(B, cin, cout, L, ws):
