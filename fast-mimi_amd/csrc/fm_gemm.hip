@@ -1628,7 +1628,9 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     } else if (t128 * splits >= 192) {
       // 256x128 where it gives >= 384 tiles, else the direct-load 128x128
       // tile (the 2500-row qkv projection 34 us against 40 us for 64x128
-      // tiles, the 8000-row output projection 34 against 37 us).
+      // tiles, the 8000-row output projection 34 against 37 us), or 192x128
+      // (one per CU) where 128x128 would put two on some CUs and 192x128
+      // tiles fit in one round (4000-row qkv 54 -> 45 us).
       cfg = tile_count(M, p.N, kX6Big) >= 384 ? kX6Big : kX6;
       if (cfg.id == kX6.id && t128 > 256 && tile_count(M, p.N, kX6Wide) <= 256) cfg = kX6Wide;
       tiles = tile_count(M, p.N, cfg);
