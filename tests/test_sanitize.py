@@ -1,9 +1,10 @@
 """The C ABI's host-side argument validation under AddressSanitizer and
 UndefinedBehaviorSanitizer (CPU only).
 
-The library sources are compiled with ``-fsanitize=address,undefined`` on
-the host side only (``-Xarch_host``; the gfx950 device code is built plain) and
-linked with
+The library sources are compiled with AddressSanitizer and
+UndefinedBehaviorSanitizer on the host side only (each sanitizer flag scoped by
+``-Xarch_host``; the link line also passes ``-fno-gpu-sanitize``), so the
+gfx950 device code is built plain, and linked with
 ``tests/sanitize/abi_validation.cpp``, which calls every entry point with
 arguments each check must reject (null pointers, negative or unsupported
 sizes, short workspaces, an input past the allocation-free scratch) and the
@@ -48,7 +49,8 @@ def test_abi_validation_under_asan_ubsan():
 
     with ThreadPoolExecutor(max_workers=6) as pool:
         objects = list(pool.map(compile_one, sources + [REPO / "tests" / "sanitize" / "abi_validation.cpp"]))
-    proc = subprocess.run([HIPCC, "--offload-arch=gfx950", "-fsanitize=address,undefined",
+    proc = subprocess.run([HIPCC, "--offload-arch=gfx950", "-fno-gpu-sanitize",
+                           "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
                            *objects, "-o", str(exe)], capture_output=True, text=True)
     assert proc.returncode == 0, proc.stderr[-4000:]
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0",
