@@ -23,7 +23,11 @@ size to calibrate the counters); the figures live in
 ``profiles/dec_up4_convt_c2_hbm_traffic.md`` and are read from there.
 
 The 100 s clip and the RVQ-heavy batch-64 / 32-codebook
-configuration are reported as extra sections.
+configuration are reported as extra sections; the latter also
+times the RVQ kernels alone (``rvq_only``: the split encode's distance
+GEMMs against the FP32 MFMA peak, the decode gather-sum against HBM).
+``c1`` is the 5 s clip on the GPU and ``cpu_baseline_c1`` the CPU oracle on
+it (configs[0], the reference's CPU configuration).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
        python bench.py --dominant-only [--iters N]   (counter runs)
@@ -81,6 +85,7 @@ def dominant_kernel(model: MimiModel, name: str, batch: int, samples: int, nq: i
     for _ in range(3):
         op()
     torch.cuda.synchronize()
+    plan = nat.last_gemm_plan()  # the kernel the selection launched for this shape
     # The launches are captured in one hipGraph and replayed, so the events
     # bracket back-to-back kernels on the capture stream, not host launch gaps.
     graph = torch.cuda.CUDAGraph()
@@ -100,13 +105,76 @@ def dominant_kernel(model: MimiModel, name: str, batch: int, samples: int, nq: i
     ms = start.elapsed_time(stop) / iters
     del graph
     achieved = flops / (ms * 1e-3) / 1e12
-    return {"bound": "mfma", "kernel": f"gemm_x6d_kernel<256,128,8,1> ({name}: {row[1]} rows={row[3]} K={row[4]} N={row[5]})",
+    return {"bound": "mfma", "kernel": f"{plan} ({name}: {row[1]} rows={row[3]} K={row[4]} N={row[5]})",
             "flops_per_launch": flops, "avg_launch_ms": ms, "achieved": round(achieved, 3),
             "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
             "traffic": None,
             "note": ("FP32 contraction run as six bf16 MFMA products per operand pair (FP32-accurate); "
                      "achieved counts the algorithmic FP32 FLOPs against the FP32 MFMA peak"),
             "bf16_mfma_pipe_frac": round(6 * achieved / PEAK_BF16_TFLOPS, 4)}
+
+
+def graph_ms(fn, iters: int) -> float:
+    """Mean time of ``fn`` over ``iters`` back-to-back launches replayed from one
+    hipGraph, by HIP events on the replay stream."""
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.inference_mode(), torch.cuda.graph(graph):
+        for _ in range(iters):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    graph.replay()
+    stop.record()
+    stop.synchronize()
+    del graph
+    return start.elapsed_time(stop) / iters
+
+
+@torch.inference_mode()
+def rvq_only(model: MimiModel, audio: torch.Tensor, nq: int, iters: int = 10) -> dict:
+    """The RVQ kernels alone at their real shape (C5: 8000 frame vectors, 32
+    codebooks): the split encode (distance GEMM + argmin + residual update per
+    codebook, both chains) and the decode gather-sum, on the encoder's own
+    projected RVQ inputs for this audio."""
+    from fast_mimi_amd import ops
+
+    rt = model.runtime()
+    cfg = model.config
+    h, B, T = rt.embeddings(audio)
+    proj = rt.quantizer_inputs(h, B, T)
+    M, vq, E = B * T, rt.vq, cfg.codebook_size
+    n_sem = min(cfg.num_semantic_quantizers, nq)
+    codes = torch.empty((B, nq, T), dtype=torch.int64, device=audio.device)
+    wsb = nat.library().fm_rvq_split_workspace_bytes(M, vq, E)
+    ws = torch.empty((wsb + 3) // 4, device=audio.device)
+    q = torch.empty((M, 2 * vq), device=audio.device)
+
+    def enc():
+        ops.call("fm_rvq_encode_split", proj, 2 * vq, M, T, vq, E, n_sem, nq - n_sem,
+                 rt.embeds, rt.embeds_t, rt.norms, codes, nq * T, ws, wsb)
+
+    def dec():
+        ops.call("fm_rvq_decode", codes, B, nq, T, cfg.num_semantic_quantizers, rt.embeds, E, vq, q)
+
+    enc_ms = graph_ms(enc, iters)
+    dec_ms = graph_ms(dec, iters)
+    dist_flops = 2 * M * E * vq * nq            # distance GEMMs (cross terms x.e)
+    gather_bytes = M * nq * (vq * 4 + 8) + M * 2 * vq * 4  # rows gathered + codes read + sums written
+    enc_tf = dist_flops / (enc_ms * 1e-3) / 1e12
+    dec_gbs = gather_bytes / (dec_ms * 1e-3) / 1e9
+    return {"frames": M, "codebooks": nq, "entries": E, "dim": vq,
+            "encode_ms": round(enc_ms, 4), "distance_gflop": round(dist_flops / 1e9, 2),
+            "distance_tflops": round(enc_tf, 3), "distance_frac_fp32_mfma": round(enc_tf / PEAK_FP32_TFLOPS, 4),
+            "decode_ms": round(dec_ms, 4), "gather_bytes": gather_bytes,
+            "gather_gbs": round(dec_gbs, 1), "gather_frac_hbm": round(dec_gbs / PEAK_HBM_GBS, 4),
+            "note": ("encode time covers every launch of fm_rvq_encode_split (per-codebook distance "
+                     "MFMA + argmin + residual subtract, both chains); FLOPs count 2*M*E*D per codebook")}
 
 
 TRAFFIC_FILE = REPO / "profiles" / "dec_up4_convt_c2_hbm_traffic.md"
@@ -127,7 +195,7 @@ def recorded_traffic() -> dict | None:
             k, v = line.lstrip()[2:].split(":", 1)
             vals[k.strip().strip("`")] = v.strip().strip("`")
     try:
-        return {"bytes": float(vals["traffic_bytes_per_launch"]),
+        return {"kernel": vals["kernel"], "bytes": float(vals["traffic_bytes_per_launch"]),
                 "fetch": float(vals["fetch_bytes_per_launch"]),
                 "write": float(vals["write_bytes_per_launch"])}
     except (KeyError, ValueError):
@@ -149,7 +217,7 @@ def dominant_only(iters: int) -> None:
     print(json.dumps({"dominant": DOMINANT, "iters": iters, "copy_bytes": COPY_BYTES}), flush=True)
 
 
-def cpu_baseline(audio: np.ndarray, mask: np.ndarray, nq: int, runs: int) -> dict:
+def cpu_baseline(audio: np.ndarray, mask: np.ndarray, nq: int, runs: int, what: str) -> dict:
     sys.path.insert(0, str(REPO))
     from oracle.mimi_oracle import MimiOracle
     from fast_mimi_amd.weights import seeded_state_dict
@@ -173,7 +241,7 @@ def cpu_baseline(audio: np.ndarray, mask: np.ndarray, nq: int, runs: int) -> dic
     seconds = audio.shape[0] * audio.shape[-1] / 24_000
     return {"value": round(seconds / (med / 1e3), 3), "unit": "audio-sec/sec", "cores": cores,
             "kind": "port", "median_ms": round(med, 2), "cpu": cpu_model(),
-            "sample": f"B1 x 10 s, nq={nq} (the bench workload itself), CPU oracle (PyTorch "
+            "sample": f"{what}, nq={nq}, CPU oracle (PyTorch "
                       f"eager restatement of the reference model.py path), median of {runs} "
                       f"after 2 warm-ups ({total_s:.1f} s of timed CPU work), {cores} threads"}
 
@@ -265,6 +333,11 @@ def main() -> None:
         "pipeline_tflops": round(flops / (med_ms * 1e-3) / 1e12, 3),
         "pipeline_flops": flops,
     }
+    a1, m1, nq1 = synthetic.config_inputs("c1")
+    a1d, m1d = torch.from_numpy(a1).to(dev), torch.from_numpy(m1).to(dev)
+    t1 = time_steps(lambda: model(a1d, m1d, num_quantizers=nq1), max(10, args.steps // 2), 3)
+    result["c1"] = {"median_ms": round(statistics.median(t1), 4),
+                    "audio_sec_per_sec": round(5.0 / (statistics.median(t1) / 1e3), 2)}
     # Same workload with the input in pageable host memory and codes + audio
     # copied back inside the timed region (PCIe-inclusive; not ``value``).
     a_host, m_host = torch.from_numpy(audio), torch.from_numpy(mask)
@@ -301,17 +374,28 @@ def main() -> None:
                            "num_quantizers": nqx, "median_ms": round(medx, 3),
                            "audio_sec_per_sec": round(ax.shape[0] * ax.shape[-1] / 24_000 / (medx / 1e3), 2),
                            "pipeline_tflops": round(fx / (medx * 1e-3) / 1e12, 3)}
+            if cfg_name == "c5":
+                result[key]["rvq_only"] = rvq_only(model, axd, nqx)
             del axd, mxd
         model.release_graphs()
     result["parity"] = checks
     result["roofline"] = dominant_kernel(model, DOMINANT, 1, audio.shape[-1], nq, 50)
     tr = recorded_traffic()
-    if tr is not None:
+    # The counter figures hold only for the kernel they were measured on.
+    if tr is not None and result["roofline"]["kernel"].startswith(tr["kernel"] + " "):
         result["roofline"]["traffic"] = tr["bytes"]
-        result["roofline"]["traffic_source"] = str(TRAFFIC_FILE.relative_to(REPO))
+        result["roofline"]["traffic_source"] = (f"{TRAFFIC_FILE.relative_to(REPO)} (rocprofv3 FETCH_SIZE + "
+                                                "WRITE_SIZE of the same kernel and shape, not measured "
+                                                "in this run)")
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(audio, mask, nq, args.cpu_runs)
+        result["cpu_baseline"] = cpu_baseline(audio, mask, nq, args.cpu_runs,
+                                              "B1 x 10 s (the bench workload itself)")
         result["speedup_vs_cpu"] = round(result["value"] / result["cpu_baseline"]["value"], 2)
+        # C1 (B1 x 5 s), the configuration the reference's CPU path is quoted on.
+        c1 = cpu_baseline(a1, m1, nq1, args.cpu_runs, "C1: B1 x 5 s")
+        c1["gpu_median_ms"] = result["c1"]["median_ms"]
+        c1["speedup_gpu_vs_cpu"] = round(c1["median_ms"] / result["c1"]["median_ms"], 2)
+        result["cpu_baseline_c1"] = c1
     print(json.dumps(result), flush=True)
 
 

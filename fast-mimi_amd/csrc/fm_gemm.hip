@@ -33,6 +33,7 @@
 // A scalar generic kernel covers the remaining shapes (C_in or K not a
 // multiple of 4: the 1-channel first convolution and tiny test configs).
 
+#include <cstdio>
 #include "fm_common.h"
 
 namespace {
@@ -1484,6 +1485,38 @@ int pick_splits(long tiles, int K, long blocks, int cap, int min_k) {
   return s;
 }
 
+// The kernel the last run_gemm call on this host thread launched (for
+// fm_gemm_last_plan): instantiation name, grid and K-split count.
+thread_local char g_last_plan[160] = "";
+
+const char* kernel_name(int id, bool elu) {
+  switch (id) {
+    case 0: return "gemm_fast_kernel<128,128,2,2,1,64>";
+    case 1: return "gemm_fast_kernel<128,64,4,1,1,64>";
+    case 2: return "gemm_fast_kernel<128,32,4,1,1,64>";
+    case 3: return "gemm_fast_kernel<32,64,1,1,4,32>";
+    case 6: return "gemm_big_kernel<256,64,4,2,false>";
+    case 9: return "gemm_big_kernel<128,128,2,4,true>";
+    case 10: return "gemm_big_kernel<192,128,2,4,true>";
+    case 11: return "gemm_big_kernel<64,128,2,4,true>";
+    case 13: return "gemm_dl_kernel<128,128,4,32,2,4>";
+    case 14: return "gemm_dl_kernel<192,128,4,32,2,4>";
+    case 15: return "gemm_dl_kernel<64,128,4,64,2,4>";
+    case 16: return elu ? "gemm_x6d_kernel<128,128,4,1,2,true>" : "gemm_x6d_kernel<128,128,4,2,2,false>";
+    case 17: return elu ? "gemm_x6d_kernel<256,128,8,1,2,true>" : "gemm_x6d_kernel<256,128,8,1,2,false>";
+    case 18: return elu ? "gemm_x6d_kernel<64,128,2,2,2,true>" : "gemm_x6d_kernel<64,128,2,2,2,false>";
+    case 19: return elu ? "gemm_x6d_kernel<192,128,6,2,2,true>" : "gemm_x6d_kernel<192,128,6,2,2,false>";
+    case 7: return "gemm_mid_kernel<64,64,1>";
+    case 8: return "gemm_mid_kernel<32,32,4>";
+    default: return "gemm_generic_kernel";
+  }
+}
+
+void record_plan(int id, bool elu, long tiles, int splits) {
+  snprintf(g_last_plan, sizeof g_last_plan, "%s tiles=%ld splits=%d%s", kernel_name(id, elu), tiles,
+           splits, splits > 1 ? " +splitk_reduce_kernel" : "");
+}
+
 int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s) {
   if (!p.x || !p.w || !p.y || p.batch < 0 || p.rows < 0 || p.K <= 0 || p.N <= 0 ||
       p.C_in <= 0 || p.L_in < 0 || p.rs <= 0 || p.y_rows < 0 || p.y_rows > p.rows)
@@ -1651,6 +1684,7 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
   p.partial = splits > 1 ? workspace : nullptr;
 
   dim3 grid((unsigned)tiles, splits);
+  record_plan(cfg.id, (p.flags & FM_ELU_IN) != 0, tiles, splits);
   // Zero-page loader of the large tiles (their k-tile is 32).
   const bool zp = !(p.flags & FM_REPLICATE) && p.C_in % 32 == 0;
   switch (cfg.id) {
@@ -1778,6 +1812,12 @@ int fm_conv1d_valid(const float* x, int batch, int length, int in_channels,
 // The bf16x6 planes of a packed weight W^T [rows][cols] (cols % 16 == 0):
 // [3][cols/16][rows][16] bf16.  Callers store them right after the FP32
 // weight and pass FM_WEIGHTS_X6 in flags.
+int fm_gemm_last_plan(char* buf, int size) {
+  if (!buf || size <= 0) return FM_BAD_ARGUMENT;
+  snprintf(buf, (size_t)size, "%s", g_last_plan);
+  return FM_OK;
+}
+
 int fm_split_weights(const float* weight_packed, int rows, int cols, void* planes, hipStream_t stream) {
   if (!weight_packed || !planes || rows <= 0 || cols <= 0) return FM_BAD_ARGUMENT;
   if (cols % 16) return FM_UNSUPPORTED;

@@ -322,9 +322,12 @@ __global__ __launch_bounds__(NT, 3) void resblock_direct_kernel(
   // Interior blocks (halo and rows inside the sequence) address every row
   // through raw buffers: a lane offset plus compile-time row offsets, no
   // per-element bounds checks.  Edge blocks take the checked path.
-  const bool fast = t0 >= 2 && t0 + BM <= L && (long)L * C * 4 <= 0x7fffffffL;
-  const __amdgpu_buffer_rsrc_t rx = fm_buffer(xb, L * C * 4);
-  const __amdgpu_buffer_rsrc_t ry = fm_buffer(y + b * (long)L * C, L * C * 4);
+  // Byte counts in 64-bit: the raw buffers are only used (and only sized)
+  // when a batch item's activation fits a 32-bit offset.
+  const long act_bytes = (long)L * C * 4;
+  const bool fast = t0 >= 2 && t0 + BM <= L && act_bytes <= 0x7fffffffL;
+  const __amdgpu_buffer_rsrc_t rx = fm_buffer(xb, fast ? (int)act_bytes : 0);
+  const __amdgpu_buffer_rsrc_t ry = fm_buffer(y + b * (long)L * C, fast ? (int)act_bytes : 0);
   const int vrow = ((t0 + wr * 32 + 4 * h) * C + wc * 64 + lcol) * 4;  // this lane's first output element
   auto row_off = [&](int r, int j) { return ((8 * (r >> 2) + (r & 3)) * C + j * 32) * 4; };
 
@@ -521,9 +524,10 @@ __global__ __launch_bounds__(NT, 3) void resblock_x6_kernel(
   // residual.  WAVE_OUT: y receives per row the three tap products of the
   // decoder's last conv (w0 = w3 [3][64]) instead of the block output.
   const float* xb = x + b * (long)L * (WAVE_IN ? 1 : C);
-  const bool fast = t0 >= 2 && t0 + BM <= L && (long)L * C * 4 <= 0x7fffffffL;
-  const __amdgpu_buffer_rsrc_t rx = fm_buffer(xb, L * (WAVE_IN ? 1 : C) * 4);
-  const __amdgpu_buffer_rsrc_t ry = fm_buffer(y + b * (long)L * C, L * C * 4);
+  const long act_bytes = (long)L * C * 4;  // 64-bit; see resblock_x6_kernel
+  const bool fast = t0 >= 2 && t0 + BM <= L && act_bytes <= 0x7fffffffL;
+  const __amdgpu_buffer_rsrc_t rx = fm_buffer(xb, fast ? (int)((long)L * (WAVE_IN ? 1 : C) * 4) : 0);
+  const __amdgpu_buffer_rsrc_t ry = fm_buffer(y + b * (long)L * C, fast ? (int)act_bytes : 0);
   const int vrow = ((t0 + wr * 32 + 4 * h) * C + wc * 64 + lcol) * 4;
   auto row_off = [&](int r, int j) { return ((8 * (r >> 2) + (r & 3)) * C + j * 32) * 4; };
   // Byte offset of 16-byte chunk c of row r in a plane of `pitch`-byte rows

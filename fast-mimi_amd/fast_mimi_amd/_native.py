@@ -47,6 +47,7 @@ _S = ctypes.c_size_t
 
 _SIGNATURES = {
     "fm_abi_version": ([], _I),
+    "fm_gemm_last_plan": ([ctypes.c_char_p, _I], _I),
     "fm_split_weights": ([_P, _I, _I, _P, _P], _I),
     "fm_conv1d": ([_P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _S, _P], _I),
     "fm_conv1d_rows_supported": ([_I, _I, _I, _I], _I),
@@ -119,3 +120,10 @@ def check(status: int, name: str) -> None:
 
 def call(name: str, *args) -> None:
     check(getattr(library(), name)(*args), name)
+
+
+def last_gemm_plan() -> str:
+    """Kernel, tiles and K splits of the last GEMM-engine call on this thread."""
+    buf = ctypes.create_string_buffer(160)
+    check(library().fm_gemm_last_plan(buf, len(buf)), "fm_gemm_last_plan")
+    return buf.value.decode()

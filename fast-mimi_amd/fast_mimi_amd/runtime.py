@@ -31,6 +31,7 @@ import torch
 from . import _native as nat
 from . import ops
 from .config import MimiConfig
+from .flops import layer_table
 from .weights import decoder_layer_indices, encoder_layer_indices
 
 _WORKSPACE_BYTES = 64 << 20
@@ -97,6 +98,22 @@ class _Layer:
         self.w2 = g("mlp.fc2.weight").contiguous()
         self.ls1 = g("self_attn_layer_scale.scale").contiguous()
         self.ls2 = g("mlp_layer_scale.scale").contiguous()
+
+
+_PROJECTIONS = ("qkv", "o", "fc1", "fc2")
+
+
+def x6_plan(config: MimiConfig) -> dict[str, bool]:
+    """Which contractions carry bf16x6 weight planes, by ``flops.layer_table``
+    name: every SEANet conv / transposed conv and every transformer projection
+    whose reduction length K (the packed weight's row length) is a multiple of
+    16, the k-tile of the planes.  The RVQ projections keep FP32 weights only.
+    Independent of batch and length; the runtime checks itself against it."""
+    plan = {}
+    for name, kind, _, _, k, _ in layer_table(config, 1, 2 * config.sampling_rate, 1):
+        if kind in ("conv", "convt") or (kind == "gemm" and name.rsplit(".", 1)[-1] in _PROJECTIONS):
+            plan[name] = k % 16 == 0
+    return plan
 
 
 def rope_tables(config: MimiConfig, length: int) -> tuple[torch.Tensor, torch.Tensor]:
@@ -197,6 +214,16 @@ class MimiRuntime:
                 layer.w, layer.flags = w, nat.WEIGHTS_X6
         for w in [m for lay in self.enc_tf + self.dec_tf for m in (lay.wqkv, lay.wo, lay.w1, lay.w2)]:
             self._x6[w.data_ptr()] = self._with_planes(w)
+        # Which layers took planes, checked against the declared plan (a layer
+        # without planes would silently run its FP32 kernels instead).
+        self.x6_layers = {name: bool(layer.flags & nat.WEIGHTS_X6) for name, layer in self._named_conv_layers()}
+        for tag, layers in (("enc.tf", self.enc_tf), ("dec.tf", self.dec_tf)):
+            for i, lay in enumerate(layers):
+                for short, w in zip(_PROJECTIONS, (lay.wqkv, lay.wo, lay.w1, lay.w2)):
+                    self.x6_layers[f"{tag}{i}.{short}"] = self._x6[w.data_ptr()] is not w
+        if self.x6_layers != x6_plan(cfg):
+            raise RuntimeError("bf16x6 weight planes do not follow x6_plan: "
+                               f"{sorted(set(self.x6_layers.items()) ^ set(x6_plan(cfg).items()))}")
         # Few-row long-K convolutions (fm_conv1d_rows, see _ROWCONV_MAX_MACS):
         # on the bf16x6 planes where the layer has them, else on
         # fragment-packed FP32 weights.
@@ -214,15 +241,25 @@ class MimiRuntime:
         self._tag = ""
         torch.cuda.synchronize(device)
 
-    def _conv_layers(self):
-        layers = [self.enc_first, self.enc_last, self.dec_first, self.dec_last]
-        for (c1, c2), down in self.enc_stages:
-            layers += [c1, c2, down]
-        for convt, (c1, c2) in self.dec_stages:
-            layers += [convt, c1, c2]
+    def _named_conv_layers(self):
+        """(``flops.layer_table`` name, layer) of every SEANet / bottleneck conv."""
+        cfg = self.config
+        out = [("enc.first", self.enc_first)]
+        ch = cfg.num_filters
+        for r, ((c1, c2), down) in zip(reversed(cfg.upsampling_ratios), self.enc_stages):
+            out += [(f"enc.res{ch}.c1", c1), (f"enc.res{ch}.c2", c2), (f"enc.down{r}", down)]
+            ch *= 2
+        out.append(("enc.last", self.enc_last))
         if self.bottleneck:
-            layers.append(self.down)
-        return layers
+            out.append(("down", self.down))
+        out.append(("dec.first", self.dec_first))
+        for r, (convt, (c1, c2)) in zip(cfg.upsampling_ratios, self.dec_stages):
+            out += [(f"dec.up{r}", convt), (f"dec.res{convt.c_out}.c1", c1), (f"dec.res{convt.c_out}.c2", c2)]
+        out.append(("dec.last", self.dec_last))
+        return out
+
+    def _conv_layers(self):
+        return [layer for _, layer in self._named_conv_layers()]
 
     def _with_planes(self, w: torch.Tensor) -> torch.Tensor:
         """``w`` [N, K] (FP32 W^T) as the first N*K floats of a buffer that
@@ -234,8 +271,7 @@ class MimiRuntime:
         n = w.numel()
         buf = torch.empty(n + 3 * n // 2, device=self.device)
         buf[:n].copy_(w.reshape(-1))
-        nat.call("fm_split_weights", buf.data_ptr(), rows, cols, buf.data_ptr() + 4 * n,
-                 torch.cuda.current_stream(self.device).cuda_stream)
+        ops.call("fm_split_weights", buf[:n], rows, cols, buf[n:])
         return buf[:n].view(w.shape)
 
     # ------------------------------------------------------------------ ops

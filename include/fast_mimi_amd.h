@@ -52,6 +52,15 @@ enum {
 int fm_abi_version(void);
 
 /*
+ * Diagnostics (no counterpart in the reference, which has no kernel
+ * selection of its own to report): writes into `buf` (at most `size` bytes,
+ * NUL-terminated) the kernel instantiation, tile count and K-split count that
+ * the last fm_conv1d / fm_conv1d_valid / fm_conv_transpose1d / fm_linear call
+ * made on the calling host thread launched ("" before any).  Host only.
+ */
+int fm_gemm_last_plan(char* buf, int size);
+
+/*
  * bf16x6 weights: writes the three round-to-nearest bf16 pieces of each
  * float of a packed weight W^T [rows][cols] (cols a multiple of 16, else
  * FM_UNSUPPORTED) into `planes` in k16-tile order [3][cols/16][rows][16].

@@ -95,3 +95,26 @@ def test_padding_cache_context_rules():
         MimiConv1dPaddingCache(2, [1], ["constant"], [1])
     with pytest.raises(NotImplementedError):
         MimiConv1dPaddingCache(1, [1], ["reflect"], [1])
+
+
+def test_bf16x6_weight_plan_for_the_mimi_config():
+    """Every SEANet conv but the 1-channel first conv (K = 7) and every
+    transformer projection carries bf16x6 planes in the published config; the
+    runtime raises if the layers it built differ from this plan."""
+    from fast_mimi_amd.runtime import x6_plan
+
+    cfg = MimiConfig()
+    plan = x6_plan(cfg)
+    assert [n for n, on in plan.items() if not on] == ["enc.first"]
+    convs = {n for n in plan if not n.startswith(("enc.tf", "dec.tf"))}
+    assert convs == {"enc.first", "enc.res64.c1", "enc.res64.c2", "enc.down4", "enc.res128.c1",
+                     "enc.res128.c2", "enc.down5", "enc.res256.c1", "enc.res256.c2", "enc.down6",
+                     "enc.res512.c1", "enc.res512.c2", "enc.down8", "enc.last", "down", "dec.first",
+                     "dec.up8", "dec.res512.c1", "dec.res512.c2", "dec.up6", "dec.res256.c1",
+                     "dec.res256.c2", "dec.up5", "dec.res128.c1", "dec.res128.c2", "dec.up4",
+                     "dec.res64.c1", "dec.res64.c2", "dec.last"}
+    projections = [n for n in plan if n.startswith(("enc.tf", "dec.tf"))]
+    assert len(projections) == 2 * cfg.num_hidden_layers * 4
+    # A reduction length that is not a multiple of 16 falls out of the plan.
+    odd = x6_plan(MimiConfig(**{**TINY, "hidden_size": 24, "intermediate_size": 40}))
+    assert odd["enc.tf0.fc2"] is False and odd["enc.tf0.qkv"] is False

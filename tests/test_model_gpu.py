@@ -30,7 +30,7 @@ DEV = "cuda"
 
 # Certified near-ties recorded per configuration against the reference fixtures:
 # (code rows, widest relative gap); C5 is per clip.
-NEAR_TIE_BOUND = {"c4": (3, 1.4e-7), "c5": (1, 1.1e-7)}
+NEAR_TIE_BOUND = {"c4": (3, 1.4e-7), "c5": (1, 1.1e-7), "c5_all": (64, 1e-6)}
 
 
 def snr_db(got: torch.Tensor, want: torch.Tensor) -> float:
@@ -227,11 +227,19 @@ def test_c4_long_clip_matches_reference(full, golden_large):
     if torch.equal(codes, want):
         assert_audio(values[..., ::100], torch.from_numpy(golden_large["c4_values_dec100"]))
     assert_audio(values, oracle.decode(codes, m))
+    # The reference's own code chain decoded on the GPU against the reference's
+    # waveform, so a decoder regression cannot hide behind a certified near-tie.
+    ref_dec = model.decode(want.to(DEV)).audio_values.cpu()
+    model.release_graphs()
+    assert_audio(ref_dec[..., ::100], torch.from_numpy(golden_large["c4_values_dec100"]))
 
 
 def test_c5_32_codebooks_matches_reference(full, golden_large):
-    """Batch 64 at 32 codebooks: clips 0 and 63 against the reference's codes
-    (certified near-ties within the recorded bound) and audio."""
+    """Batch 64 at 32 codebooks: all 64 clips' codes against the host oracle's
+    batched encode (certified near-ties within the recorded bound, any other
+    difference fails); clips 0 and 63 against the reference's codes and audio,
+    with the reference's code chain also decoded on the GPU; audio of clips 0,
+    31 and 63 against the oracle's decode of the GPU's codes."""
     model, oracle = full
     audio, mask, nq = synthetic.config_inputs("c5")
     a, m = torch.from_numpy(audio), torch.from_numpy(mask)
@@ -239,6 +247,12 @@ def test_c5_32_codebooks_matches_reference(full, golden_large):
     codes, values = out.audio_codes.cpu(), out.audio_values.cpu()
     model.release_graphs()
     assert codes.shape == (64, 32, 125)
+    trace = Trace()
+    host_codes = oracle.encode(a, nq, trace)
+    compare_codes(model, oracle, trace, codes, host_codes, "c5_all_clips_vs_host_oracle",
+                  NEAR_TIE_BOUND["c5_all"])
+    del trace
+    assert_audio(values[31:32], oracle.decode(codes[31:32], m[31:32]))
     for c in (0, 63):
         trace = Trace()
         ref_codes = oracle.encode(a[c:c + 1], nq, trace)
@@ -249,6 +263,9 @@ def test_c5_32_codebooks_matches_reference(full, golden_large):
         if torch.equal(got, want):
             assert_audio(values[c:c + 1, :, ::10], torch.from_numpy(golden_large[f"c5_clip{c}_values_dec10"]))
         assert_audio(values[c:c + 1], oracle.decode(got, m[c:c + 1]))
+        ref_dec = model.decode(want.to(DEV)).audio_values.cpu()
+        assert_audio(ref_dec[..., ::10], torch.from_numpy(golden_large[f"c5_clip{c}_values_dec10"]))
+    model.release_graphs()
 
 
 def _codes_match_or_near_tie(model, oracle, trace, got, want, what):
