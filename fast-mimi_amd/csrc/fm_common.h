@@ -153,9 +153,43 @@ FM_DEVICE void fm_buf_store1(float v, __amdgpu_buffer_rsrc_t r, int voff, int so
   __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, voff, soff, 0);
 }
 
+// Block barrier for LDS traffic only: this wave's LDS operations complete,
+// then s_barrier.  Unlike __syncthreads it does not wait for the wave's
+// outstanding global loads and stores (prefetches keep flying).
+FM_DEVICE void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Orders this wave's LDS accesses: everything before completes before
 // anything after is issued (the compiler may not move memory ops across).
 FM_DEVICE void wave_lds_fence() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_wave_barrier();
+}
+
+// ---------------------------------------------------------------------------
+// Cross-block exchange inside one launch (persistent kernels).  Data that
+// another block reads is stored and loaded as agent-scope relaxed atomics:
+// the stores write through the caches to memory and the loads bypass them
+// (the sc bits the compiler sets for that scope), so the exchange is coherent
+// whichever XCD each block runs on, with no L2 write-back or invalidate, and
+// the compiler still overlaps independent loads.  Arrivals are atomic adds on
+// a counter; a waiter polls it with coherent loads, at most `spin` times.
+FM_DEVICE void fm_store64_coherent(unsigned long long* p, unsigned long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+FM_DEVICE unsigned long long fm_load64_coherent(const unsigned long long* p) {
+  return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Called by one lane of the wave that issued the block's coherent stores:
+// waits for them to complete, arrives, then polls until `target` arrivals
+// (false on timeout).
+FM_DEVICE bool fm_arrive_and_wait(unsigned* counter, unsigned target, long spin) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (long s = 0; s < spin; ++s)
+    if (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) return true;
+  return false;
 }

@@ -334,13 +334,7 @@ __global__ __launch_bounds__(NTHREADS) void gemm_fast_kernel(GemmArgs p) {
 // phase overlaps the other's MFMAs.  The 128x128 form measured 3-4% faster
 // wherever N >= 128.  Loads are branch-free (clamped address plus a select)
 // so the in-order instruction stream stays short.
-// Block barrier that orders LDS accesses only (outstanding global loads and
-// stores keep flying): this wave's LDS operations complete, then s_barrier.
-FM_DEVICE void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
+// (lds_barrier, the LDS-only block barrier, lives in fm_common.h.)
 
 // Sixteen zero bytes: the source of every out-of-window operand load in the
 // zero-page loader (referenced from device code only).

@@ -15,6 +15,8 @@
 // 0 + e_1[c_1] + e_2[c_2] + ... left to right for the acoustic branch) into
 // the [rows, 2*dim] operand of the fused output projection GEMM.
 
+#include <cstdlib>
+
 #include "fm_common.h"
 
 namespace {
@@ -493,6 +495,246 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a0, const f
   }
 }
 
+// ---------------------------------------------------------------------------
+// Whole split encode in one persistent launch, for few rows (<= 4 tiles of 32
+// rows: the B = 1 clips of up to ~10 s).  The step kernel above needs one
+// launch per codebook and re-resolves the previous step's argmin in each of
+// its blocks; here the residual chain of a (32-row tile, branch) pair stays
+// in one group of CHAIN_BLOCKS blocks that steps through every codebook of
+// the branch:
+//   group g = blockIdx.x % 8 (blocks g, g + 8, ... run on one XCD, so a
+//   group's codebook reads share that XCD's L2), pair g = (tile g / 2,
+//   branch g % 2); block q = blockIdx.x / 8 owns codebook entries
+//   [64 q, 64 q + 64) as two 32-entry sub-tiles;
+//   each step: distances of the 32 residual rows to the block's entries,
+//   block argmin per row -> partial (value, index, step tag) stored
+//   coherently -> every block polls the group's partials of its rows until
+//   all carry the step's tag, resolves the argmin and subtracts the chosen
+//   entry from its own copy of the residual (LDS), so residual rows never
+//   leave the block and no separate barrier is needed.
+// Partials are double-buffered by step parity: a block can only write step
+// s + 2 after every block wrote step s + 1, i.e. after every block has read
+// step s.  The tags of the zeroed slots (0) never match a step (>= 1).
+// The arithmetic is rvq_step_mfma_kernel<256, 4>'s operation for operation
+// (32x32x2 FP32 MFMA chains over four 64-dim k-parts summed in k-part order,
+// |r|^2 over eight lanes per row, the same distance and residual rounding),
+// so the codes are bit-identical to the per-step launches.  Block barriers
+// order LDS only (lds_barrier), so the next codebook's fragment loads stay in
+// flight across them.
+constexpr int CHAIN_BLOCKS = 32;  // blocks per group: 32 x 64 entries
+constexpr int CHAIN_GROUPS = 8;
+constexpr int CHAIN_ENTRIES = CHAIN_BLOCKS * 64;
+constexpr long CHAIN_SPIN = 1L << 20;  // polls before a wait gives up (~1 s)
+constexpr size_t CHAIN_PARTIALS = (size_t)2 * CHAIN_GROUPS * CHAIN_BLOCKS * RB;
+constexpr size_t CHAIN_WORKSPACE_BYTES = CHAIN_PARTIALS * 8 + 256;
+
+struct ChainArgs {
+  const float* x;   // [M][ld_x]: semantic input in columns [0, 256), acoustic in [256, 512)
+  int ld_x, M, rows_per_batch, entries, batch_stride;
+  int count[2];     // codebooks per branch
+  const float* embeds[2];  // branch codebooks [count][entries][256]
+  const float* norms[2];   // [count][entries]
+  int64_t* codes[2];       // codebook 0 of the branch; codebook j at + j * rows_per_batch
+  unsigned long long* partials;  // [2][CHAIN_GROUPS][CHAIN_BLOCKS][32], zeroed before the launch
+  unsigned* status;        // incremented when a wait gives up
+};
+
+__global__ __launch_bounds__(512, 4) void rvq_chain_kernel(ChainArgs a) {
+  constexpr int DIM = 256, PX = DIM + 4, PR = RB + 1, CH = DIM / 32, PER = CHAIN_BLOCKS / 8;
+  __shared__ __attribute__((aligned(16))) float Xs[RB * PX];  // residual rows
+  __shared__ float xnS[RB];
+  __shared__ float red[4][2][32 * PR];   // each wave's k-part dot products [p][st][entry][row]
+  __shared__ float bestv[8][RB];         // per wave (st, p): best over its entries, per row
+  __shared__ int besti[8][RB];
+  __shared__ float normS[64];
+  __shared__ int failS;
+
+  const int g = blockIdx.x % CHAIN_GROUPS, q = blockIdx.x / CHAIN_GROUPS;
+  const int tile = g >> 1, br = g & 1;
+  const long m0 = (long)tile * RB;
+  const int count = a.count[br];
+  if (m0 >= a.M || count == 0) return;  // this pair has no work (the whole group returns)
+  const float* __restrict__ embeds = a.embeds[br];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int st = wave & 1, p = wave >> 1;  // sub-tile, k-part
+  const int h = lane >> 5, col = lane & 31;
+  const int e_begin = q * 64;
+  const int kbase = p * 64;
+  auto slot = [&](int s, int blk, int row) {
+    return a.partials + (((long)(s & 1) * CHAIN_GROUPS + g) * CHAIN_BLOCKS + blk) * RB + row;
+  };
+  if (tid == 0) failS = 0;
+
+  // Codebook fragment of this wave: entry e_begin + 32 st + col, dims
+  // kbase + 32 h .. + 31 (rvq_step_mfma_kernel's load_piece); the block's
+  // 64 norms ride along (one per lane of wave 0).
+  floatx4 cur[8];
+  float nrm = 0.0f;
+  auto load_piece = [&](int j) {
+    const int entry = min(e_begin + 32 * st + col, a.entries - 1);
+    const float* src = embeds + ((long)j * a.entries + entry) * DIM + kbase + 32 * h;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) cur[u] = *reinterpret_cast<const floatx4*>(src + 4 * u);
+    if (tid < 64) nrm = e_begin + tid < a.entries ? a.norms[br][(long)j * a.entries + e_begin + tid] : 0.0f;
+  };
+  load_piece(0);
+
+  // Residual rows of step 0: the branch's input columns.
+  if (tid < 256) {
+    const int r = tid >> 3, pt = tid & 7;
+    const long m = m0 + r;
+    const bool valid = m < a.M;
+    const float* xr = a.x + min(m, (long)a.M - 1) * a.ld_x + br * DIM;
+    float xn = 0.0f;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      floatx4 x = *reinterpret_cast<const floatx4*>(xr + 4 * (pt + 8 * u));
+      if (!valid) x = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xn = fmaf(x[e], x[e], xn);
+      *reinterpret_cast<floatx4*>(Xs + r * PX + 4 * (pt + 8 * u)) = x;
+    }
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) xn += __shfl_xor(xn, o, 64);
+    if (pt == 0) xnS[r] = xn;
+  }
+
+  for (int s = 0; s <= count; ++s) {
+    if (s > 0) {
+      // Only block 0 of the group needs the last step's codes.
+      if (s == count && q != 0) break;
+      // Resolve step s - 1: eight lanes per row, each polling PER partials
+      // until all carry tag s, then a shuffle reduction (`better` is a
+      // total order, so the grouping does not change the result).
+      if (tid < 256) {
+        const int r = tid >> 3, pt = tid & 7;
+        unsigned long long pv[PER];
+        bool ready = false;
+        for (long spin = 0; !ready && spin < CHAIN_SPIN; ++spin) {
+#pragma unroll
+          for (int u = 0; u < PER; ++u) pv[u] = fm_load64_coherent(slot(s - 1, pt + 8 * u, r));
+          ready = true;
+#pragma unroll
+          for (int u = 0; u < PER; ++u) ready &= (unsigned)(pv[u] >> 48) == (unsigned)s;
+        }
+        if (!ready) failS = 1;
+        float bv = INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+          const float v = __uint_as_float((unsigned)pv[u]);
+          const int i = (int)((pv[u] >> 32) & 0xffff);
+          if (better(v, i, bv, bi)) bv = v, bi = i;
+        }
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) {
+          const float ov = __shfl_xor(bv, o, 64);
+          const int oi = __shfl_xor(bi, o, 64);
+          if (better(ov, oi, bv, bi)) bv = ov, bi = oi;
+        }
+        bi = code_index(bi, a.entries);
+        const long m = m0 + r;
+        if (q == 0 && pt == 0 && m < a.M) {
+          const long b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
+          a.codes[br][(long)(s - 1) * a.rows_per_batch + b * a.batch_stride + t] = bi;
+        }
+        if (s < count) {
+          // residual_s = residual_{s-1} - e_{s-1}[code], and its |.|^2.
+          const float* er = embeds + ((long)(s - 1) * a.entries + bi) * DIM;
+          floatx4 ev[CH];
+#pragma unroll
+          for (int u = 0; u < CH; ++u) ev[u] = *reinterpret_cast<const floatx4*>(er + 4 * (pt + 8 * u));
+          const bool valid = m < a.M;
+          float xn = 0.0f;
+#pragma unroll
+          for (int u = 0; u < CH; ++u) {
+            floatx4 x = *reinterpret_cast<const floatx4*>(Xs + r * PX + 4 * (pt + 8 * u));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = __fsub_rn(x[e], ev[u][e]);
+            if (!valid) x = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xn = fmaf(x[e], x[e], xn);
+            *reinterpret_cast<floatx4*>(Xs + r * PX + 4 * (pt + 8 * u)) = x;
+          }
+#pragma unroll
+          for (int o = 1; o < 8; o <<= 1) xn += __shfl_xor(xn, o, 64);
+          if (pt == 0) xnS[r] = xn;
+        }
+      }
+      if (s == count) break;
+    }
+    if (tid < 64) normS[tid] = nrm;
+    lds_barrier();
+    if (failS) {
+      if (tid == 0) __hip_atomic_fetch_add(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+
+    // Distances: 32 entries (A, from registers) x 32 rows (B, from LDS), this wave's k-part.
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const floatx4 b4 = *reinterpret_cast<const floatx4*>(Xs + col * PX + kbase + 32 * h + 4 * j);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = fm_mfma32(cur[j][e], b4[e], acc);
+    }
+    // Next codebook's fragment and norms go out now; their latency hides
+    // behind the reduction and the resolve.
+    if (s + 1 < count) load_piece(s + 1);
+    // Every wave publishes its k-part; then wave (st, p) finishes entries
+    // 8 (r / 4) + 4 h + (r % 4) for r = 4 p .. 4 p + 3 of sub-tile st (four
+    // of the sixteen accumulator rows), summing the k-parts in order 0..3.
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[p][st][fm_mfma32_row(r, lane) * PR + col] = acc[r];
+    lds_barrier();
+    {
+      float best_v = INFINITY;
+      int best_i = 0x7fffffff;
+      const float xq = xnS[col];
+      const int n0 = e_begin + 32 * st;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int row = fm_mfma32_row(4 * p + rr, lane);
+        float v = red[0][st][row * PR + col];
+#pragma unroll
+        for (int pp = 1; pp < 4; ++pp) v = __fadd_rn(v, red[pp][st][row * PR + col]);
+        const int entry = n0 + row;
+        if (entry < a.entries) {
+          const float d = __fadd_rn(__fadd_rn(__fmul_rn(-2.0f, v), xq), normS[entry - e_begin]);
+          const float dist = dist_key(d);
+          if (better(dist, entry, best_v, best_i)) best_v = dist, best_i = entry;
+        }
+      }
+      const float ov = __shfl_xor(best_v, 32, 64);
+      const int oi = __shfl_xor(best_i, 32, 64);
+      if (better(ov, oi, best_v, best_i)) best_v = ov, best_i = oi;
+      if (h == 0) bestv[wave][col] = best_v, besti[wave][col] = best_i;
+    }
+    lds_barrier();
+    if (tid < RB) {
+      float v = bestv[0][tid];
+      int i = besti[0][tid];
+#pragma unroll
+      for (int w = 1; w < 8; ++w)
+        if (better(bestv[w][tid], besti[w][tid], v, i)) v = bestv[w][tid], i = besti[w][tid];
+      // A block with no entries in range publishes +inf (index 0xffff).
+      if (i > 0xffff) i = 0xffff;
+      fm_store64_coherent(slot(s, q, tid), ((unsigned long long)(s + 1) << 48) |
+                                               ((unsigned long long)(unsigned)i << 32) | __float_as_uint(v));
+    }
+  }
+}
+
+// Zeroes the chain kernel's partial slots (so no stale tag can match) and its
+// status word: a kernel, not a memset node, so the pair can be captured in a
+// hipGraph.
+__global__ __launch_bounds__(256) void rvq_chain_reset_kernel(unsigned long long* partials, long n) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) partials[i] = 0ull;
+}
+
 // Resolves the last step: 8 lanes per row (32 rows per block).
 __global__ __launch_bounds__(256) void rvq_finalize_kernel(const float* val, const int* idx,
                                                            int chunks, int M, int64_t* codes,
@@ -683,6 +925,29 @@ int launch_fast_step(const RvqPlan& pl, int dim, dim3 grid, const StepArgs& a0, 
   return (int)hipGetLastError();
 }
 
+// The persistent chain needs all CHAIN_GROUPS * CHAIN_BLOCKS blocks resident
+// at once (its barriers wait on every block of a group): at most two per CU
+// by its LDS, so at least half as many CUs as blocks.  FM_RVQ_CHAIN=0 in the
+// environment selects the per-step launches instead (for comparisons).
+bool chain_eligible(int rows, int dim, int entries) {
+  if (dim != 256 || entries > CHAIN_ENTRIES || rows > (CHAIN_GROUPS / 2) * RB) return false;
+  static const bool enabled = [] {
+    const char* v = getenv("FM_RVQ_CHAIN");
+    return !(v && v[0] == '0');
+  }();
+  if (!enabled) return false;
+  constexpr int kMaxDev = 64;
+  static int cus[kMaxDev] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return false;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
+    cus[dev] = n;
+  }
+  return 2 * cus[dev] >= CHAIN_GROUPS * CHAIN_BLOCKS;
+}
+
 bool rvq_args_ok(const float* x, int ld_x, int rows, int rows_per_batch, int dim, int entries,
                  const float* embeds, const float* embeds_t, const float* norms, const int64_t* codes) {
   return x && embeds && embeds_t && norms && codes && rows >= 0 && dim > 0 && dim % 4 == 0 &&
@@ -748,7 +1013,7 @@ int fm_rvq_encode(const float* x, int ld_x, int rows, int rows_per_batch, int di
 }
 
 size_t fm_rvq_split_workspace_bytes(int rows, int dim, int entries) {
-  return 2 * fm_rvq_workspace_bytes(rows, dim, entries);
+  return std::max(2 * fm_rvq_workspace_bytes(rows, dim, entries), CHAIN_WORKSPACE_BYTES);
 }
 
 // Both branches of the split quantizer in shared launches: launch s runs
@@ -784,6 +1049,23 @@ int fm_rvq_encode_split(const float* x, int ld_x, int rows, int rows_per_batch, 
                            codes + (size_t)n_semantic * rows_per_batch, batch_stride, ws + one, one,
                            stream);
     return FM_OK;
+  }
+  if (chain_eligible(rows, dim, entries)) {
+    // Few rows: the whole chain of both branches in one persistent launch.
+    ChainArgs c{};
+    c.x = x; c.ld_x = ld_x; c.M = rows; c.rows_per_batch = rows_per_batch; c.entries = entries;
+    c.batch_stride = batch_stride;
+    c.count[0] = n_semantic; c.count[1] = n_acoustic;
+    c.embeds[0] = embeds; c.embeds[1] = embeds + n_semantic * cb;
+    c.norms[0] = norms; c.norms[1] = norms + (size_t)n_semantic * entries;
+    c.codes[0] = codes; c.codes[1] = codes + (size_t)n_semantic * rows_per_batch;
+    c.partials = reinterpret_cast<unsigned long long*>(ws);
+    c.status = reinterpret_cast<unsigned*>(ws + CHAIN_PARTIALS * 8);
+    const long words = (long)CHAIN_PARTIALS + 1;  // the status word follows the slots
+    hipLaunchKernelGGL(rvq_chain_reset_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream,
+                       c.partials, words);
+    hipLaunchKernelGGL(rvq_chain_kernel, dim3(CHAIN_GROUPS * CHAIN_BLOCKS), dim3(512), 0, stream, c);
+    return (int)hipGetLastError();
   }
   const RvqPlan pl = rvq_plan(rows, dim, entries);
   if (pl.lds > 64 * 1024) return FM_UNSUPPORTED;

@@ -1014,6 +1014,13 @@ def test_rvq_non_finite_rows_give_reference_codes():
     (1, 33, 1, 0, 2048, 256),     # semantic only
     (1, 33, 0, 3, 2048, 256),     # acoustic only
     (2, 40, 1, 2, 48, 8),         # general kernel: branches one after the other
+    # <= 128 rows at dim 256: the persistent one-launch chain (must equal the
+    # per-step launches bit for bit)
+    (1, 128, 1, 7, 2048, 256),    # four full 32-row tiles
+    (1, 1, 1, 7, 2048, 256),      # one row
+    (1, 97, 2, 5, 1000, 256),     # ragged entries (blocks past the codebook), partial tile
+    (2, 33, 1, 31, 2048, 256),    # long acoustic chain, rows across two batch items
+    (1, 64, 3, 1, 2048, 256),     # longer semantic chain than acoustic
 ])
 def test_rvq_encode_split_matches_two_branches(B, T, nsem, nac, e, d):
     """Shared-launch split encode == the two branches encoded separately (bit-exact codes)."""
