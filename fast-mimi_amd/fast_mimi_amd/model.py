@@ -131,9 +131,13 @@ class _GraphRunner:
             for dst, src in zip(self.static_in, inputs):
                 dst.copy_(src)
             self.graph.replay()
-            if isinstance(self.static_out, tuple):
-                return tuple(t.clone() for t in self.static_out)
-            return self.static_out.clone()
+            outs = self.static_out if isinstance(self.static_out, tuple) else (self.static_out,)
+            # Caller-owned copies of every output in one multi-tensor launch
+            # (byte views share a dtype, so foreach groups them together).
+            copies = tuple(torch.empty_like(t) for t in outs)
+            torch._foreach_copy_([c.view(-1).view(torch.uint8) for c in copies],
+                                 [t.view(-1).view(torch.uint8) for t in outs])
+            return copies if isinstance(self.static_out, tuple) else copies[0]
 
 
 class MimiModel:
