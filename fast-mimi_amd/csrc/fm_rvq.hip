@@ -502,10 +502,12 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a0, const f
 // its blocks; here the residual chain of a (32-row tile, branch) pair stays
 // in one group of CHAIN_BLOCKS blocks that steps through every codebook of
 // the branch:
-//   group g = blockIdx.x % 8 (blocks g, g + 8, ... run on one XCD, so a
-//   group's codebook reads share that XCD's L2), pair g = (tile g / 2,
-//   branch g % 2); block q = blockIdx.x / 8 owns codebook entries
-//   [64 q, 64 q + 64) as two 32-entry sub-tiles;
+//   block b runs on XCD x = b % 8 (the dispatcher's round robin); tile t =
+//   x / 2 owns XCDs 2t and 2t + 1, and of the 64 blocks j = b / 8 each XCD
+//   holds for it, j < 32 serve the acoustic chain and j >= 32 the semantic
+//   one (which ends after its first codebook, leaving each CU one acoustic
+//   block with one wave per SIMD);  block q = 32 (x % 2) + j % 32 of a group
+//   owns codebook entries [32 q, 32 q + 32), four waves = four 64-dim k-parts;
 //   each step: distances of the 32 residual rows to the block's entries,
 //   block argmin per row -> partial (value, index, step tag) stored
 //   coherently -> every block polls the group's partials of its rows until
@@ -521,9 +523,9 @@ __global__ __launch_bounds__(256) void rvq_step_mfma_kernel(StepArgs a0, const f
 // so the codes are bit-identical to the per-step launches.  Block barriers
 // order LDS only (lds_barrier), so the next codebook's fragment loads stay in
 // flight across them.
-constexpr int CHAIN_BLOCKS = 32;  // blocks per group: 32 x 64 entries
-constexpr int CHAIN_GROUPS = 8;
-constexpr int CHAIN_ENTRIES = CHAIN_BLOCKS * 64;
+constexpr int CHAIN_BLOCKS = 64;  // blocks per group: 64 x 32 entries
+constexpr int CHAIN_GROUPS = 8;   // (tile, branch) pairs
+constexpr int CHAIN_ENTRIES = CHAIN_BLOCKS * 32;
 constexpr long CHAIN_SPIN = 1L << 20;  // polls before a wait gives up (~1 s)
 constexpr size_t CHAIN_PARTIALS = (size_t)2 * CHAIN_GROUPS * CHAIN_BLOCKS * RB;
 constexpr size_t CHAIN_WORKSPACE_BYTES = CHAIN_PARTIALS * 8 + 256;
@@ -539,48 +541,47 @@ struct ChainArgs {
   unsigned* status;        // incremented when a wait gives up
 };
 
-__global__ __launch_bounds__(512, 4) void rvq_chain_kernel(ChainArgs a) {
+__global__ __launch_bounds__(256, 4) void rvq_chain_kernel(ChainArgs a) {
   constexpr int DIM = 256, PX = DIM + 4, PR = RB + 1, CH = DIM / 32, PER = CHAIN_BLOCKS / 8;
   __shared__ __attribute__((aligned(16))) float Xs[RB * PX];  // residual rows
   __shared__ float xnS[RB];
-  __shared__ float red[4][2][32 * PR];   // each wave's k-part dot products [p][st][entry][row]
-  __shared__ float bestv[8][RB];         // per wave (st, p): best over its entries, per row
-  __shared__ int besti[8][RB];
-  __shared__ float normS[64];
+  __shared__ float red[4][32 * PR];   // each wave's k-part dot products [p][entry][row]
+  __shared__ float bestv[4][RB];      // per wave: best over its entries, per row
+  __shared__ int besti[4][RB];
+  __shared__ float normS[32];
   __shared__ int failS;
 
-  const int g = blockIdx.x % CHAIN_GROUPS, q = blockIdx.x / CHAIN_GROUPS;
-  const int tile = g >> 1, br = g & 1;
+  const int x = blockIdx.x % 8, j = blockIdx.x / 8;
+  const int tile = x >> 1, br = j >= 32 ? 0 : 1;
+  const int g = tile * 2 + br, q = (x & 1) * 32 + (j & 31);
   const long m0 = (long)tile * RB;
   const int count = a.count[br];
   if (m0 >= a.M || count == 0) return;  // this pair has no work (the whole group returns)
   const float* __restrict__ embeds = a.embeds[br];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int st = wave & 1, p = wave >> 1;  // sub-tile, k-part
+  const int tid = threadIdx.x, lane = tid & 63, p = tid >> 6;  // wave = k-part
   const int h = lane >> 5, col = lane & 31;
-  const int e_begin = q * 64;
+  const int e_begin = q * 32;
   const int kbase = p * 64;
   auto slot = [&](int s, int blk, int row) {
     return a.partials + (((long)(s & 1) * CHAIN_GROUPS + g) * CHAIN_BLOCKS + blk) * RB + row;
   };
   if (tid == 0) failS = 0;
 
-  // Codebook fragment of this wave: entry e_begin + 32 st + col, dims
-  // kbase + 32 h .. + 31 (rvq_step_mfma_kernel's load_piece); the block's
-  // 64 norms ride along (one per lane of wave 0).
+  // Codebook fragment of this wave: entry e_begin + col, dims kbase + 32 h ..
+  // + 31 (rvq_step_mfma_kernel's load_piece); the block's 32 norms ride along.
   floatx4 cur[8];
   float nrm = 0.0f;
-  auto load_piece = [&](int j) {
-    const int entry = min(e_begin + 32 * st + col, a.entries - 1);
-    const float* src = embeds + ((long)j * a.entries + entry) * DIM + kbase + 32 * h;
+  auto load_piece = [&](int jj) {
+    const int entry = min(e_begin + col, a.entries - 1);
+    const float* src = embeds + ((long)jj * a.entries + entry) * DIM + kbase + 32 * h;
 #pragma unroll
     for (int u = 0; u < 8; ++u) cur[u] = *reinterpret_cast<const floatx4*>(src + 4 * u);
-    if (tid < 64) nrm = e_begin + tid < a.entries ? a.norms[br][(long)j * a.entries + e_begin + tid] : 0.0f;
+    if (tid < 32) nrm = e_begin + tid < a.entries ? a.norms[br][(long)jj * a.entries + e_begin + tid] : 0.0f;
   };
   load_piece(0);
 
-  // Residual rows of step 0: the branch's input columns.
-  if (tid < 256) {
+  // Residual rows of step 0: the branch's input columns (eight lanes per row).
+  {
     const int r = tid >> 3, pt = tid & 7;
     const long m = m0 + r;
     const bool valid = m < a.M;
@@ -588,11 +589,11 @@ __global__ __launch_bounds__(512, 4) void rvq_chain_kernel(ChainArgs a) {
     float xn = 0.0f;
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
-      floatx4 x = *reinterpret_cast<const floatx4*>(xr + 4 * (pt + 8 * u));
-      if (!valid) x = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      floatx4 xv = *reinterpret_cast<const floatx4*>(xr + 4 * (pt + 8 * u));
+      if (!valid) xv = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) xn = fmaf(x[e], x[e], xn);
-      *reinterpret_cast<floatx4*>(Xs + r * PX + 4 * (pt + 8 * u)) = x;
+      for (int e = 0; e < 4; ++e) xn = fmaf(xv[e], xv[e], xn);
+      *reinterpret_cast<floatx4*>(Xs + r * PX + 4 * (pt + 8 * u)) = xv;
     }
 #pragma unroll
     for (int o = 1; o < 8; o <<= 1) xn += __shfl_xor(xn, o, 64);
@@ -606,64 +607,65 @@ __global__ __launch_bounds__(512, 4) void rvq_chain_kernel(ChainArgs a) {
       // Resolve step s - 1: eight lanes per row, each polling PER partials
       // until all carry tag s, then a shuffle reduction (`better` is a
       // total order, so the grouping does not change the result).
-      if (tid < 256) {
-        const int r = tid >> 3, pt = tid & 7;
-        unsigned long long pv[PER];
-        bool ready = false;
-        for (long spin = 0; !ready && spin < CHAIN_SPIN; ++spin) {
+      const int r = tid >> 3, pt = tid & 7;
+      // Each lane first polls one of its partials, then loads all of them
+      // (a full re-poll only if one is still missing): eight times fewer
+      // coherent loads while waiting than polling all (measured 49.7 vs
+      // 56.1 us per call at C2; pipelined polls: 60 us).
+      unsigned long long pv[PER];
+      bool ready = false;
+      for (long spin = 0; !ready && spin < CHAIN_SPIN; ++spin) {
+        if ((unsigned)(fm_load64_coherent(slot(s - 1, pt + 8 * (PER - 1), r)) >> 48) != (unsigned)s) continue;
 #pragma unroll
-          for (int u = 0; u < PER; ++u) pv[u] = fm_load64_coherent(slot(s - 1, pt + 8 * u, r));
-          ready = true;
+        for (int u = 0; u < PER; ++u) pv[u] = fm_load64_coherent(slot(s - 1, pt + 8 * u, r));
+        ready = true;
 #pragma unroll
-          for (int u = 0; u < PER; ++u) ready &= (unsigned)(pv[u] >> 48) == (unsigned)s;
-        }
-        if (!ready) failS = 1;
-        float bv = INFINITY;
-        int bi = 0x7fffffff;
+        for (int u = 0; u < PER; ++u) ready &= (unsigned)(pv[u] >> 48) == (unsigned)s;
+      }
+      if (!ready) failS = 1;
+      float bv = INFINITY;
+      int bi = 0x7fffffff;
 #pragma unroll
-        for (int u = 0; u < PER; ++u) {
-          const float v = __uint_as_float((unsigned)pv[u]);
-          const int i = (int)((pv[u] >> 32) & 0xffff);
-          if (better(v, i, bv, bi)) bv = v, bi = i;
-        }
+      for (int u = 0; u < PER; ++u) {
+        const float v = __uint_as_float((unsigned)pv[u]);
+        const int i = (int)((pv[u] >> 32) & 0xffff);
+        if (better(v, i, bv, bi)) bv = v, bi = i;
+      }
 #pragma unroll
-        for (int o = 1; o < 8; o <<= 1) {
-          const float ov = __shfl_xor(bv, o, 64);
-          const int oi = __shfl_xor(bi, o, 64);
-          if (better(ov, oi, bv, bi)) bv = ov, bi = oi;
-        }
-        bi = code_index(bi, a.entries);
-        const long m = m0 + r;
-        if (q == 0 && pt == 0 && m < a.M) {
-          const long b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
-          a.codes[br][(long)(s - 1) * a.rows_per_batch + b * a.batch_stride + t] = bi;
-        }
-        if (s < count) {
-          // residual_s = residual_{s-1} - e_{s-1}[code], and its |.|^2.
-          const float* er = embeds + ((long)(s - 1) * a.entries + bi) * DIM;
-          floatx4 ev[CH];
-#pragma unroll
-          for (int u = 0; u < CH; ++u) ev[u] = *reinterpret_cast<const floatx4*>(er + 4 * (pt + 8 * u));
-          const bool valid = m < a.M;
-          float xn = 0.0f;
-#pragma unroll
-          for (int u = 0; u < CH; ++u) {
-            floatx4 x = *reinterpret_cast<const floatx4*>(Xs + r * PX + 4 * (pt + 8 * u));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) x[e] = __fsub_rn(x[e], ev[u][e]);
-            if (!valid) x = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) xn = fmaf(x[e], x[e], xn);
-            *reinterpret_cast<floatx4*>(Xs + r * PX + 4 * (pt + 8 * u)) = x;
-          }
-#pragma unroll
-          for (int o = 1; o < 8; o <<= 1) xn += __shfl_xor(xn, o, 64);
-          if (pt == 0) xnS[r] = xn;
-        }
+      for (int o = 1; o < 8; o <<= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (better(ov, oi, bv, bi)) bv = ov, bi = oi;
+      }
+      bi = code_index(bi, a.entries);
+      const long m = m0 + r;
+      if (q == 0 && pt == 0 && m < a.M) {
+        const long b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
+        a.codes[br][(long)(s - 1) * a.rows_per_batch + b * a.batch_stride + t] = bi;
       }
       if (s == count) break;
+      // residual_s = residual_{s-1} - e_{s-1}[code], and its |.|^2.
+      const float* er = embeds + ((long)(s - 1) * a.entries + bi) * DIM;
+      floatx4 ev[CH];
+#pragma unroll
+      for (int u = 0; u < CH; ++u) ev[u] = *reinterpret_cast<const floatx4*>(er + 4 * (pt + 8 * u));
+      const bool valid = m < a.M;
+      float xn = 0.0f;
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        floatx4 xv = *reinterpret_cast<const floatx4*>(Xs + r * PX + 4 * (pt + 8 * u));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[e] = __fsub_rn(xv[e], ev[u][e]);
+        if (!valid) xv = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xn = fmaf(xv[e], xv[e], xn);
+        *reinterpret_cast<floatx4*>(Xs + r * PX + 4 * (pt + 8 * u)) = xv;
+      }
+#pragma unroll
+      for (int o = 1; o < 8; o <<= 1) xn += __shfl_xor(xn, o, 64);
+      if (pt == 0) xnS[r] = xn;
     }
-    if (tid < 64) normS[tid] = nrm;
+    if (tid < 32) normS[tid] = nrm;
     lds_barrier();
     if (failS) {
       if (tid == 0) __hip_atomic_fetch_add(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -675,34 +677,33 @@ __global__ __launch_bounds__(512, 4) void rvq_chain_kernel(ChainArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const floatx4 b4 = *reinterpret_cast<const floatx4*>(Xs + col * PX + kbase + 32 * h + 4 * j);
+    for (int jj = 0; jj < 8; ++jj) {
+      const floatx4 b4 = *reinterpret_cast<const floatx4*>(Xs + col * PX + kbase + 32 * h + 4 * jj);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc = fm_mfma32(cur[j][e], b4[e], acc);
+      for (int e = 0; e < 4; ++e) acc = fm_mfma32(cur[jj][e], b4[e], acc);
     }
     // Next codebook's fragment and norms go out now; their latency hides
     // behind the reduction and the resolve.
     if (s + 1 < count) load_piece(s + 1);
-    // Every wave publishes its k-part; then wave (st, p) finishes entries
-    // 8 (r / 4) + 4 h + (r % 4) for r = 4 p .. 4 p + 3 of sub-tile st (four
-    // of the sixteen accumulator rows), summing the k-parts in order 0..3.
+    // Every wave publishes its k-part; then wave p finishes entries
+    // 8 (r / 4) + 4 h + (r % 4) for r = 4 p .. 4 p + 3 (four of the sixteen
+    // accumulator rows), summing the k-parts in order 0..3.
 #pragma unroll
-    for (int r = 0; r < 16; ++r) red[p][st][fm_mfma32_row(r, lane) * PR + col] = acc[r];
+    for (int r = 0; r < 16; ++r) red[p][fm_mfma32_row(r, lane) * PR + col] = acc[r];
     lds_barrier();
     {
       float best_v = INFINITY;
       int best_i = 0x7fffffff;
       const float xq = xnS[col];
-      const int n0 = e_begin + 32 * st;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int row = fm_mfma32_row(4 * p + rr, lane);
-        float v = red[0][st][row * PR + col];
+        float v = red[0][row * PR + col];
 #pragma unroll
-        for (int pp = 1; pp < 4; ++pp) v = __fadd_rn(v, red[pp][st][row * PR + col]);
-        const int entry = n0 + row;
+        for (int pp = 1; pp < 4; ++pp) v = __fadd_rn(v, red[pp][row * PR + col]);
+        const int entry = e_begin + row;
         if (entry < a.entries) {
-          const float d = __fadd_rn(__fadd_rn(__fmul_rn(-2.0f, v), xq), normS[entry - e_begin]);
+          const float d = __fadd_rn(__fadd_rn(__fmul_rn(-2.0f, v), xq), normS[row]);
           const float dist = dist_key(d);
           if (better(dist, entry, best_v, best_i)) best_v = dist, best_i = entry;
         }
@@ -710,14 +711,14 @@ __global__ __launch_bounds__(512, 4) void rvq_chain_kernel(ChainArgs a) {
       const float ov = __shfl_xor(best_v, 32, 64);
       const int oi = __shfl_xor(best_i, 32, 64);
       if (better(ov, oi, best_v, best_i)) best_v = ov, best_i = oi;
-      if (h == 0) bestv[wave][col] = best_v, besti[wave][col] = best_i;
+      if (h == 0) bestv[p][col] = best_v, besti[p][col] = best_i;
     }
     lds_barrier();
     if (tid < RB) {
       float v = bestv[0][tid];
       int i = besti[0][tid];
 #pragma unroll
-      for (int w = 1; w < 8; ++w)
+      for (int w = 1; w < 4; ++w)
         if (better(bestv[w][tid], besti[w][tid], v, i)) v = bestv[w][tid], i = besti[w][tid];
       // A block with no entries in range publishes +inf (index 0xffff).
       if (i > 0xffff) i = 0xffff;
@@ -926,8 +927,8 @@ int launch_fast_step(const RvqPlan& pl, int dim, dim3 grid, const StepArgs& a0, 
 }
 
 // The persistent chain needs all CHAIN_GROUPS * CHAIN_BLOCKS blocks resident
-// at once (its barriers wait on every block of a group): at most two per CU
-// by its LDS, so at least half as many CUs as blocks.  FM_RVQ_CHAIN=0 in the
+// at once (each waits on every block of its group): two per CU, so at least
+// half as many CUs as blocks.  FM_RVQ_CHAIN=0 in the
 // environment selects the per-step launches instead (for comparisons).
 bool chain_eligible(int rows, int dim, int entries) {
   if (dim != 256 || entries > CHAIN_ENTRIES || rows > (CHAIN_GROUPS / 2) * RB) return false;
@@ -1064,7 +1065,7 @@ int fm_rvq_encode_split(const float* x, int ld_x, int rows, int rows_per_batch, 
     const long words = (long)CHAIN_PARTIALS + 1;  // the status word follows the slots
     hipLaunchKernelGGL(rvq_chain_reset_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream,
                        c.partials, words);
-    hipLaunchKernelGGL(rvq_chain_kernel, dim3(CHAIN_GROUPS * CHAIN_BLOCKS), dim3(512), 0, stream, c);
+    hipLaunchKernelGGL(rvq_chain_kernel, dim3(CHAIN_GROUPS * CHAIN_BLOCKS), dim3(256), 0, stream, c);
     return (int)hipGetLastError();
   }
   const RvqPlan pl = rvq_plan(rows, dim, entries);
