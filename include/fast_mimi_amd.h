@@ -347,6 +347,9 @@ size_t fm_rvq_split_workspace_bytes(int rows, int dim, int entries);
  * 2*dim; embeds / embeds_t / norms hold all n_semantic + n_acoustic
  * codebooks contiguously; codebook j's codes land at
  * codes[b * batch_stride + j * rows_per_batch + t].
+ * Up to 128 rows at dim 256 the whole chain is one persistent launch whose
+ * blocks wait on each other: two such calls must not run concurrently on one
+ * GPU (different streams); one stream, or stream-ordered calls, are fine.
  * Replaces MimiSplitResidualVectorQuantizer._encode_eager (model.py:2485-2501).
  */
 int fm_rvq_encode_split(const float* x, int ld_x, int rows, int rows_per_batch, int dim, int entries,
