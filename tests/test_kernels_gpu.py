@@ -1202,3 +1202,16 @@ def test_split_k_repeats_and_graph_replays(rows, k, n, x6, ws):
         torch.cuda.synchronize()
         assert torch.equal(out, first)
         run_linear(other_x, other_w, ws=ws)
+
+
+def test_gemm_plan_names_the_launched_kernel():
+    """fm_gemm_last_plan reports the selection's kernel: the C2 dec.up4
+    transposed conv (60000 x 256 x 256, weights with bf16x6 planes) takes the
+    256x128 bf16x6 tile, one round of 470 tiles."""
+    from fast_mimi_amd import MimiConfig, MimiModel
+
+    rt = MimiModel(MimiConfig(), device=DEV, seed=0).runtime()
+    op = rt.layer_op("dec.up4", 1, 240_000)
+    op()
+    torch.cuda.synchronize()
+    assert nat.last_gemm_plan() == "gemm_x6d_kernel<256,128,8,1,2,false> tiles=470 splits=1"

@@ -92,3 +92,28 @@ def test_torch_ops_trace_as_opaque_mutating_calls():
     gm = make_fx(decode, tracing_mode="fake")(torch.zeros(1, 8, 125, dtype=torch.int64),
                                               torch.zeros(8, 2048, 256), torch.zeros(125, 512))
     assert "fast_mimi_amd.rvq_decode" in gm.code
+
+
+def test_residual_inputs_alias_their_output():
+    """Entry points that add a residual may be called with y == residual (the
+    runtime's in-place LayerScale residual): the schema puts residual in y's
+    alias set, read-only, so functionalization orders the update correctly."""
+    import torch
+
+    from fast_mimi_amd import ops
+
+    names = [e for e, spec in ops.SPECS.items() if "res:residual" in spec]
+    assert {"fm_linear", "fm_row_linear", "fm_row_linear_packed", "fm_conv1d"} <= set(names)
+    for entry in names:
+        args = {a.name: a for a in getattr(torch.ops.fast_mimi_amd, entry[3:]).default._schema.arguments}
+        res, y = args["residual"].alias_info, args["y"].alias_info
+        assert res is not None and not res.is_write and y.is_write, entry
+        assert set(res.before_set) == set(y.before_set), entry
+
+
+def test_gemm_plan_query_is_host_only():
+    if not nat.LIBRARY_PATH.is_file():
+        pytest.skip("library not built")
+    assert isinstance(nat.last_gemm_plan(), str)
+    with pytest.raises(nat.NativeError, match="bad argument"):
+        nat.check(nat.library().fm_gemm_last_plan(None, 0), "fm_gemm_last_plan")
