@@ -1051,7 +1051,8 @@ int fm_rvq_encode_split(const float* x, int ld_x, int rows, int rows_per_batch, 
                            stream);
     return FM_OK;
   }
-  if (chain_eligible(rows, dim, entries)) {
+  // (A workspace sized for the per-step launches only takes them.)
+  if (workspace_bytes >= CHAIN_WORKSPACE_BYTES && chain_eligible(rows, dim, entries)) {
     // Few rows: the whole chain of both branches in one persistent launch.
     ChainArgs c{};
     c.x = x; c.ld_x = ld_x; c.M = rows; c.rows_per_batch = rows_per_batch; c.entries = entries;

@@ -1215,3 +1215,25 @@ def test_gemm_plan_names_the_launched_kernel():
     op()
     torch.cuda.synchronize()
     assert nat.last_gemm_plan() == "gemm_x6d_kernel<256,128,8,1,2,false> tiles=470 splits=1"
+
+
+def test_rvq_split_with_a_per_step_sized_workspace():
+    """A workspace sized by fm_rvq_workspace_bytes alone (smaller than the
+    one-launch chain needs at a few rows) takes the per-step launches: same
+    codes, nothing written past the workspace."""
+    B, T, nsem, nac, e, d = 1, 20, 1, 7, 2048, 256
+    g = torch.Generator().manual_seed(5)
+    n = nsem + nac
+    emb, emb_t, norms = prepare_codebooks(torch.randn(n, e, d, generator=g) / 16, torch.ones(n, e))
+    x = (torch.randn(B * T, 2 * d, generator=g) * 0.3).to(DEV)
+    lib = nat.library()
+    out = []
+    for wsb in (2 * lib.fm_rvq_workspace_bytes(B * T, d, e), lib.fm_rvq_split_workspace_bytes(B * T, d, e)):
+        guard = torch.full(((wsb + 3) // 4 + 4096,), 7.0, device=DEV)
+        codes = torch.full((B, n, T), -1, dtype=torch.int64, device=DEV)
+        nat.call("fm_rvq_encode_split", x.data_ptr(), 2 * d, B * T, T, d, e, nsem, nac, emb.data_ptr(),
+                 emb_t.data_ptr(), norms.data_ptr(), codes.data_ptr(), n * T, guard.data_ptr(), wsb, stream())
+        torch.cuda.synchronize()
+        assert (guard[(wsb + 3) // 4:] == 7.0).all()
+        out.append(codes.cpu())
+    assert torch.equal(out[0], out[1])
