@@ -30,6 +30,12 @@ int main() {
   constexpr int BAD = 1000, WS = 1001, UNSUP = 1002, SCRATCH = 1003;
 
   // Convolutions.
+  {
+    char plan[8];
+    expect("gemm_last_plan null buffer", fm_gemm_last_plan(nullptr, 8), BAD);
+    expect("gemm_last_plan zero size", fm_gemm_last_plan(plan, 0), BAD);
+    expect("gemm_last_plan small buffer", fm_gemm_last_plan(plan, (int)sizeof plan), 0);
+  }
   expect("conv1d null x", fm_conv1d(nullptr, 1, 16, 64, P, nullptr, 64, 3, 1, 0, 0, nullptr, P, 16, P, 1 << 20, S), BAD);
   expect("conv1d negative length", fm_conv1d(P, 1, -1, 64, P, nullptr, 64, 3, 1, 0, 0, nullptr, P, 16, P, 1 << 20, S), BAD);
   expect("conv1d empty batch", fm_conv1d(P, 0, 16, 64, P, nullptr, 64, 3, 1, 0, 0, nullptr, P, 16, P, 1 << 20, S), 0);
