@@ -170,6 +170,8 @@ def rvq_only(model: MimiModel, audio: torch.Tensor, nq: int, iters: int = 10) ->
     dec_gbs = gather_bytes / (dec_ms * 1e-3) / 1e9
     return {"frames": M, "codebooks": nq, "entries": E, "dim": vq,
             "encode_ms": round(enc_ms, 4), "distance_gflop": round(dist_flops / 1e9, 2),
+            # The reference's mm form contracts augmented rows (K = dim + 2).
+            "distance_gflop_mm_form": round(2 * M * E * (vq + 2) * nq / 1e9, 2),
             "distance_tflops": round(enc_tf, 3), "distance_frac_fp32_mfma": round(enc_tf / PEAK_FP32_TFLOPS, 4),
             "decode_ms": round(dec_ms, 4), "gather_bytes": gather_bytes,
             "gather_gbs": round(dec_gbs, 1), "gather_frac_hbm": round(dec_gbs / PEAK_HBM_GBS, 4),
