@@ -612,7 +612,7 @@ __global__ __launch_bounds__(256, 4) void rvq_chain_kernel(ChainArgs a) {
       // (a full re-poll only if one is still missing): eight times fewer
       // coherent loads while waiting than polling all (measured 49.7 vs
       // 56.1 us per call at C2; pipelined polls: 60 us).
-      unsigned long long pv[PER];
+      unsigned long long pv[PER] = {};  // (a wait that gives up resolves zeros: index 0)
       bool ready = false;
       for (long spin = 0; !ready && spin < CHAIN_SPIN; ++spin) {
         if ((unsigned)(fm_load64_coherent(slot(s - 1, pt + 8 * (PER - 1), r)) >> 48) != (unsigned)s) continue;
