@@ -29,7 +29,8 @@ enum FmGemmFlags {
   FM_EPI_GELU = 8,      // exact-erf GELU on the output
   FM_EPI_RES_ADD = 16,  // y = res + (acc + bias)
   FM_EPI_RES_SCALE = 32, // y = res + scale[n] * acc
-  FM_WEIGHTS_X6 = 64     // weight_packed is followed by its three bf16 planes (fm_split_weights)
+  FM_WEIGHTS_X6 = 64,    // weight_packed is followed by its three bf16 planes (fm_split_weights)
+  FM_ACT_EXP = 128       // residual blocks: ELUs as e^x - 1 (fm_elu_exp), for decoder-side calls
 };
 
 // e^x - 1 for x <= 0, branch-free.  Near zero (x > -1/4) x * q(x), q a
@@ -56,6 +57,15 @@ FM_DEVICE float fm_expm1_neg(float x) {
 // almost every wave anyway.
 FM_DEVICE float fm_elu(float x) {
   const float r = fm_expm1_neg(x);
+  return x > 0.0f ? x : r;
+}
+
+// ELU from the hardware exponential alone, e^x - 1 for x <= 0: an absolute
+// error of a few 2^-24 near zero (where fm_elu keeps a relative one), for
+// kernels held to an absolute bar rather than to bit-exact codes (the
+// decoder's waveform).  Five instructions against fm_elu's twelve.
+FM_DEVICE float fm_elu_exp(float x) {
+  const float r = __expf(x) - 1.0f;
   return x > 0.0f ? x : r;
 }
 

@@ -496,7 +496,7 @@ __global__ __launch_bounds__(NT, 3) void resblock_direct_kernel(
 // .. +7, so a wave's weight fragment (32 rows x 16 k) is one contiguous 1 KB
 // run (a [3][N][K] row-major layout spreads it over 32 cache lines, which the
 // per-CU address path, not the MFMAs, then limits: 1.55x slower).
-template <int C, int BM, int WM, int PD, bool WAVE_IN, bool WAVE_OUT>
+template <int C, int BM, int WM, int PD, bool WAVE_IN, bool WAVE_OUT, bool FAST_ACT = false>
 __global__ __launch_bounds__(NT, 3) void resblock_x6_kernel(
     const float* __restrict__ x, int L, const __bf16* __restrict__ w1x, const float* __restrict__ b1,
     const __bf16* __restrict__ w2x, const float* __restrict__ b2, int elu_out, float* __restrict__ y,
@@ -509,6 +509,7 @@ __global__ __launch_bounds__(NT, 3) void resblock_x6_kernel(
   static_assert(3 * HPLANE <= 3 * XPLANE, "hidden planes fit over the ELU(x) planes");
   static_assert(!(WAVE_IN || WAVE_OUT) || (C == 64 && WM == 4), "waveform ends: one wave per 32 rows x 64 channels");
   static_assert(!WAVE_OUT || 4 * 32 * 68 * 4 <= 3 * XPLANE, "output tiles fit");
+  auto act = [](float v) { return FAST_ACT ? fm_elu_exp(v) : fm_elu(v); };
   __shared__ __attribute__((aligned(16))) char smem[3 * XPLANE];
   __shared__ float wins[WAVE_IN ? BM + 8 : 1];  // WAVE_IN: waveform samples t0-8 .. t0+BM-1
 
@@ -628,7 +629,7 @@ __global__ __launch_bounds__(NT, 3) void resblock_x6_kernel(
     if (c >= CH) continue;
     const int r = c / (C / 4), k = (c % (C / 4)) * 4;
     bf16x4 p0, p1, p2;
-    split3(floatx4{fm_elu(xv[u].x), fm_elu(xv[u].y), fm_elu(xv[u].z), fm_elu(xv[u].w)}, p0, p1, p2);
+    split3(floatx4{act(xv[u].x), act(xv[u].y), act(xv[u].z), act(xv[u].w)}, p0, p1, p2);
     char* dst = smem + chunk(r, k >> 3, C * 2) + (k & 4) * 2;
     *reinterpret_cast<bf16x4*>(dst) = p0;
     *reinterpret_cast<bf16x4*>(dst + XPLANE) = p1;
@@ -679,7 +680,7 @@ __global__ __launch_bounds__(NT, 3) void resblock_x6_kernel(
       const floatx4 bb = *reinterpret_cast<const floatx4*>(b1 + wc * 32 + 8 * g + 4 * h);
       floatx4 v;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = fm_elu(__fadd_rn(__fadd_rn(acc1[0][4 * g + e], acc1[1][4 * g + e]), bb[e]));
+      for (int e = 0; e < 4; ++e) v[e] = act(__fadd_rn(__fadd_rn(acc1[0][4 * g + e], acc1[1][4 * g + e]), bb[e]));
       bf16x4 p0, p1, p2;
       split3(v, p0, p1, p2);
       char* dst = smem + chunk(prow, wc * 4 + g, HC * 2) + 8 * h;
@@ -755,7 +756,7 @@ __global__ __launch_bounds__(NT, 3) void resblock_x6_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float v = __fadd_rn(rv[j][r], __fadd_rn(acc2[j][r], bias));
-        if (elu_out) v = fm_elu(v);
+        if (elu_out) v = act(v);
         E[fm_mfma32_row(r, lane) * 68 + j * 32 + lcol] = v;
       }
     }
@@ -790,7 +791,7 @@ __global__ __launch_bounds__(NT, 3) void resblock_x6_kernel(
     for (int r = 0; r < 16; ++r) {
       const int t = t0 + wr * 32 + fm_mfma32_row(r, lane);
       float v = __fadd_rn(rv[j][r], __fadd_rn(acc2[j][r], bias));
-      if (elu_out) v = fm_elu(v);
+      if (elu_out) v = act(v);
       if (fast) {
         fm_buf_store1(v, ry, vrow, row_off(r, j));
       } else if (t < L) {
@@ -822,21 +823,23 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
   if (!fm_resblock_supported(channels)) return FM_UNSUPPORTED;
   if (x == y) return FM_BAD_ARGUMENT;  // the halo rows of other blocks must stay intact
   if (batch == 0 || length == 0) return FM_OK;
-  const int elu = (elu_out & ~FM_WEIGHTS_X6) != 0;
-  const bool x6 = elu_out & FM_WEIGHTS_X6;
+  const int elu = (elu_out & ~(FM_WEIGHTS_X6 | FM_ACT_EXP)) != 0;
+  const bool x6 = elu_out & FM_WEIGHTS_X6, fa = elu_out & FM_ACT_EXP;
   if (x6) {
     // Split planes follow each packed weight (fm_split_weights).
     const __bf16* w1x = planes_after(w1_packed, channels / 2, 3 * channels);
     const __bf16* w2x = planes_after(w2_packed, channels, channels / 2);
-    if (channels == 64)
-      hipLaunchKernelGGL((resblock_x6_kernel<64, 128, 4, 2, false, false>), dim3((length + 127) / 128, batch),
-                         dim3(NT), 0, stream, x, length, w1x, b1, w2x, b2, elu, y, nullptr, nullptr);
-    else if (channels == 128)
-      hipLaunchKernelGGL((resblock_x6_kernel<128, 64, 2, 2, false, false>), dim3((length + 63) / 64, batch),
-                         dim3(NT), 0, stream, x, length, w1x, b1, w2x, b2, elu, y, nullptr, nullptr);
-    else
-      hipLaunchKernelGGL((resblock_x6_kernel<256, 32, 1, 2, false, false>), dim3((length + 31) / 32, batch),
-                         dim3(NT), 0, stream, x, length, w1x, b1, w2x, b2, elu, y, nullptr, nullptr);
+#define FM_RB(C_, BM_, WM_, FA_)                                                                    \
+  hipLaunchKernelGGL((resblock_x6_kernel<C_, BM_, WM_, 2, false, false, FA_>), dim3((length + BM_ - 1) / BM_, batch), \
+                     dim3(NT), 0, stream, x, length, w1x, b1, w2x, b2, elu, y, nullptr, nullptr)
+    if (channels == 64) {
+      if (fa) FM_RB(64, 128, 4, true); else FM_RB(64, 128, 4, false);
+    } else if (channels == 128) {
+      if (fa) FM_RB(128, 64, 2, true); else FM_RB(128, 64, 2, false);
+    } else {
+      if (fa) FM_RB(256, 32, 1, true); else FM_RB(256, 32, 1, false);
+    }
+#undef FM_RB
   } else if (channels == 64) {
     // Persistent: one 12-wave block per CU (LDS-bound), waves stride over 32-row tiles.
     const long tiles = (long)batch * ((length + 31) / 32);
@@ -863,11 +866,16 @@ int fm_conv_resblock64(const float* wav, int batch, int length, const float* w0_
       length < 0)
     return FM_BAD_ARGUMENT;
   if (batch == 0 || length == 0) return FM_OK;
-  const int elu = (elu_out & ~FM_WEIGHTS_X6) != 0;
+  const int elu = (elu_out & ~(FM_WEIGHTS_X6 | FM_ACT_EXP)) != 0;
   if (elu_out & FM_WEIGHTS_X6) {
-    hipLaunchKernelGGL((resblock_x6_kernel<64, 128, 4, 2, true, false>), dim3((length + 127) / 128, batch),
-                       dim3(NT), 0, stream, wav, length, planes_after(w1_packed, 32, 192), b1,
-                       planes_after(w2_packed, 64, 32), b2, elu, y, w0_packed, b0);
+    if (elu_out & FM_ACT_EXP)
+      hipLaunchKernelGGL((resblock_x6_kernel<64, 128, 4, 2, true, false, true>), dim3((length + 127) / 128, batch),
+                         dim3(NT), 0, stream, wav, length, planes_after(w1_packed, 32, 192), b1,
+                         planes_after(w2_packed, 64, 32), b2, elu, y, w0_packed, b0);
+    else
+      hipLaunchKernelGGL((resblock_x6_kernel<64, 128, 4, 2, true, false>), dim3((length + 127) / 128, batch),
+                         dim3(NT), 0, stream, wav, length, planes_after(w1_packed, 32, 192), b1,
+                         planes_after(w2_packed, 64, 32), b2, elu, y, w0_packed, b0);
     return (int)hipGetLastError();
   }
   const long tiles = (long)batch * ((length + 31) / 32);
@@ -894,11 +902,16 @@ int fm_resblock64_conv(const float* x, int batch, int length, const float* w1_pa
   if (batch == 0 || y_len == 0) return FM_OK;
   if (!workspace || workspace_bytes < fm_resblock64_conv_workspace_bytes(batch, length))
     return FM_WORKSPACE_TOO_SMALL;
-  const int elu = (elu_mid & ~FM_WEIGHTS_X6) != 0;
+  const int elu = (elu_mid & ~(FM_WEIGHTS_X6 | FM_ACT_EXP)) != 0;
   if (elu_mid & FM_WEIGHTS_X6) {
-    hipLaunchKernelGGL((resblock_x6_kernel<64, 128, 4, 2, false, true>), dim3((length + 127) / 128, batch),
-                       dim3(NT), 0, stream, x, length, planes_after(w1_packed, 32, 192), b1,
-                       planes_after(w2_packed, 64, 32), b2, elu, workspace, w3_packed, nullptr);
+    if (elu_mid & FM_ACT_EXP)
+      hipLaunchKernelGGL((resblock_x6_kernel<64, 128, 4, 2, false, true, true>), dim3((length + 127) / 128, batch),
+                         dim3(NT), 0, stream, x, length, planes_after(w1_packed, 32, 192), b1,
+                         planes_after(w2_packed, 64, 32), b2, elu, workspace, w3_packed, nullptr);
+    else
+      hipLaunchKernelGGL((resblock_x6_kernel<64, 128, 4, 2, false, true>), dim3((length + 127) / 128, batch),
+                         dim3(NT), 0, stream, x, length, planes_after(w1_packed, 32, 192), b1,
+                         planes_after(w2_packed, 64, 32), b2, elu, workspace, w3_packed, nullptr);
   } else {
     const long tiles = (long)batch * ((length + 31) / 32);
     const int blocks = (int)std::min<long>((tiles + R64_WAVES - 1) / R64_WAVES, 256);

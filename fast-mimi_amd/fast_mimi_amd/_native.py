@@ -26,6 +26,7 @@ EPI_GELU = 8
 EPI_RES_ADD = 16
 EPI_RES_SCALE = 32
 WEIGHTS_X6 = 64
+ACT_EXP = 128  # residual blocks: ELU as e^x - 1 (decoder-side calls)
 
 _STATUS = {1000: "bad argument", 1001: "workspace too small", 1002: "unsupported shape",
            1003: "input larger than the fixed scratch of an allocation-free entry point"}

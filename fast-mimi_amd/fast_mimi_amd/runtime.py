@@ -368,7 +368,10 @@ class MimiRuntime:
         return (c1.k == 3 and c2.c_out == 64 and last.c_in == 64 and last.c_out == 1
                 and last.k == 3 and last.stride == 1 and not last.replicate)
 
-    def _resblock(self, x, B, L, block, elu_after: bool, tag: str = "res"):
+    def _resblock(self, x, B, L, block, elu_after: bool, tag: str = "res", act_exp: bool = False):
+        """act_exp: the bf16x6 block evaluates its ELUs as e^x - 1 (absolute
+        error of a few 1e-8; decoder only: the encoder's codes need exact
+        activations)."""
         c1, c2 = block
         # The fused kernel (hidden tile kept on chip) covers the SEANet widths;
         # other shapes run as two GEMM-engine convs.
@@ -377,6 +380,8 @@ class MimiRuntime:
             self._tag = tag
             y = torch.empty_like(x)
             flags = (1 if elu_after else 0) | (c1.flags & c2.flags & nat.WEIGHTS_X6)
+            if act_exp and flags & nat.WEIGHTS_X6:
+                flags |= nat.ACT_EXP
             self._call("fm_resblock", x, B, L, c2.c_out, c1.w, c1.b, c2.w, c2.b, flags, y)
             return y
         self._tag = f"{tag}.c1"
@@ -672,10 +677,10 @@ class MimiRuntime:
                 y = torch.empty((B, out_length), device=self.device)
                 last = self.dec_last
                 self._call("fm_resblock64_conv", h, B, L, c1.w, c1.b,
-                           c2.w, c2.b, 1 | (c1.flags & c2.flags & nat.WEIGHTS_X6), last.w, last.b,
+                           c2.w, c2.b, 1 | nat.ACT_EXP | (c1.flags & c2.flags & nat.WEIGHTS_X6), last.w, last.b,
                            out_length, y, d, d.numel() * 4)
                 return y.view(B, 1, out_length)
-            h = self._resblock(h, B, L, block, elu_after=True, tag=f"dec.res{convt.c_out}")
+            h = self._resblock(h, B, L, block, elu_after=True, tag=f"dec.res{convt.c_out}", act_exp=True)
         full = L
         out_length = full if out_length is None else min(out_length, full)
         self._tag = "dec.last"

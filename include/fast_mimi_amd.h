@@ -45,7 +45,8 @@ enum {
   FM_EPI_GELU = 8,      /* exact-erf GELU on the output                        */
   FM_EPI_RES_ADD = 16,  /* y = residual + (acc + bias)                         */
   FM_EPI_RES_SCALE = 32, /* y = residual + scale[n] * acc   (fm_linear only)    */
-  FM_WEIGHTS_X6 = 64     /* weight is followed by its bf16 planes (fm_split_weights) */
+  FM_WEIGHTS_X6 = 64,    /* weight is followed by its bf16 planes (fm_split_weights) */
+  FM_ACT_EXP = 128       /* residual blocks: ELU as e^x - 1 (see fm_resblock)     */
 };
 
 /* ABI version of the library (bumped when a contract changes). */
@@ -164,9 +165,14 @@ int fm_resblock_supported(int channels);
 int fm_resblock(const float* x, int batch, int length, int channels, const float* w1_packed,
                 const float* b1, const float* w2_packed, const float* b2, int elu_out, float* y,
                 hipStream_t stream);
-/* elu_out: nonzero (other than the FM_WEIGHTS_X6 bit) applies the trailing
- * ELU; FM_WEIGHTS_X6 says both packed weights carry their fm_split_weights
- * planes (channels 128 and 256 then run on the bf16 matrix cores). */
+/* elu_out: nonzero (other than the FM_WEIGHTS_X6 and FM_ACT_EXP bits)
+ * applies the trailing ELU; FM_WEIGHTS_X6 says both packed weights carry
+ * their fm_split_weights planes (the block then runs on the bf16 matrix
+ * cores).  FM_ACT_EXP (with FM_WEIGHTS_X6) evaluates the block's ELUs as
+ * e^x - 1 from the hardware exponential: about half the vector instructions,
+ * an absolute error of a few 1e-8 near zero instead of a relative one.  For
+ * callers held to an absolute bar (the decoder's waveform), not for the
+ * encoder, whose codes depend on exact activations. */
 
 /*
  * The SEANet encoder's first conv (1 -> 64 channels, kernel 7, causal, no
@@ -175,7 +181,7 @@ int fm_resblock(const float* x, int batch, int length, int channels, const float
  * w0_packed is the conv's packed [64][7] weight.  The 64-channel conv output
  * is formed on chip and never stored.
  * Replaces MimiEncoder layers.0 + layers.1 (model.py:1013-1031).
- * elu_out may carry FM_WEIGHTS_X6 as in fm_resblock (w1/w2 with planes).
+ * elu_out may carry FM_WEIGHTS_X6 and FM_ACT_EXP as in fm_resblock.
  */
 int fm_conv_resblock64(const float* wav, int batch, int length, const float* w0_packed,
                        const float* b0, const float* w1_packed, const float* b1,
@@ -193,7 +199,7 @@ int fm_conv_resblock64(const float* wav, int batch, int length, const float* w0_
  * Replaces MimiDecoder's last MimiResnetBlock + ELU + MimiConv1d
  * (model.py:1269-1285).
  */
-/* elu_mid may carry FM_WEIGHTS_X6 as in fm_resblock (w1/w2 with planes). */
+/* elu_mid may carry FM_WEIGHTS_X6 and FM_ACT_EXP as in fm_resblock. */
 size_t fm_resblock64_conv_workspace_bytes(int batch, int length);
 int fm_resblock64_conv(const float* x, int batch, int length, const float* w1_packed,
                        const float* b1, const float* w2_packed, const float* b2, int elu_mid,

@@ -421,10 +421,11 @@ def test_long_k_epilogues(B, C, L, ws):
                                    (1, 256, 300), (2, 256, 33), (1, 64, 240000), (2, 128, 6001),
                                    (2, 256, 12001)])
 @pytest.mark.parametrize("elu_out", [1, 0])
-@pytest.mark.parametrize("x6", [False, True])
+@pytest.mark.parametrize("x6", [False, True, "act_exp"])
 def test_fused_resblock(B, C, L, elu_out, x6):
     """fm_resblock equals the reference block x + conv1x1(ELU(conv_k3(ELU(x)))),
-    on FP32 weights and on weights followed by their bf16x6 planes."""
+    on FP32 weights, on weights followed by their bf16x6 planes, and with the
+    e^x - 1 ELUs of FM_ACT_EXP (same bar: their error is absolute, ~1e-7)."""
     g = torch.Generator().manual_seed(C + L)
     x = torch.randn(B, C, L, generator=g)
     w1 = torch.randn(C // 2, C, 3, generator=g) / math.sqrt(3 * C)
@@ -435,7 +436,7 @@ def test_fused_resblock(B, C, L, elu_out, x6):
     flags = elu_out
     if x6:
         c1.w, c2.w = with_planes(c1.w), with_planes(c2.w)
-        flags |= nat.WEIGHTS_X6
+        flags |= nat.WEIGHTS_X6 | (nat.ACT_EXP if x6 == "act_exp" else 0)
     xd = x.transpose(1, 2).contiguous().to(DEV)
     y = torch.empty_like(xd)
     nat.call("fm_resblock", xd.data_ptr(), B, L, C, c1.w.data_ptr(), c1.b.data_ptr(), c2.w.data_ptr(),
@@ -451,10 +452,11 @@ def test_fused_resblock(B, C, L, elu_out, x6):
 
 @pytest.mark.parametrize("B,L", [(1, 240000), (2, 1001), (1, 1), (3, 33), (1, 31), (2, 32), (1, 70000)])
 @pytest.mark.parametrize("elu_out", [1, 0])
-@pytest.mark.parametrize("x6", [False, True], ids=["fp32", "bf16x6"])
+@pytest.mark.parametrize("x6", [False, True, "act_exp"], ids=["fp32", "bf16x6", "act_exp"])
 def test_conv_resblock64_equals_conv_then_block(B, L, elu_out, x6, ws):
     """fm_conv_resblock64 == fm_conv1d (1 -> 64, k 7) then fm_resblock, bit for
-    bit, on FP32 weights and on weights with their bf16x6 planes."""
+    bit, on FP32 weights and on weights with their bf16x6 planes (with and
+    without FM_ACT_EXP on both calls)."""
     g = torch.Generator().manual_seed(B * 31 + L)
     wav = torch.randn(B, 1, L, generator=g) * 0.5
     w0 = torch.randn(64, 1, 7, generator=g) / 3
@@ -468,7 +470,7 @@ def test_conv_resblock64_equals_conv_then_block(B, L, elu_out, x6, ws):
     flags = elu_out
     if x6:
         c1.w, c2.w = with_planes(c1.w), with_planes(c2.w)
-        flags |= nat.WEIGHTS_X6
+        flags |= nat.WEIGHTS_X6 | (nat.ACT_EXP if x6 == "act_exp" else 0)
     wd = wav.reshape(B, L).contiguous().to(DEV)
     h = torch.empty(B, L, 64, device=DEV)
     nat.call("fm_conv1d", wd.data_ptr(), B, L, 1, c0.w.data_ptr(), c0.b.data_ptr(), 64, 7, 1, 0, 0,
@@ -493,10 +495,12 @@ def test_conv_resblock64_equals_conv_then_block(B, L, elu_out, x6, ws):
 
 @pytest.mark.parametrize("B,L,y_len", [(1, 240000, 240000), (2, 1001, 990), (1, 1, 1), (3, 33, 33),
                                        (1, 31, 2), (2, 32, 32), (1, 70000, 69999)])
-@pytest.mark.parametrize("x6", [False, True], ids=["fp32", "bf16x6"])
+@pytest.mark.parametrize("x6", [False, True, "act_exp"], ids=["fp32", "bf16x6", "act_exp"])
 def test_resblock64_conv_matches_reference(B, L, y_len, x6):
     """fm_resblock64_conv == block (ELU after) then the 64 -> 1, k = 3 conv,
-    cropped; the bf16x6 form also against the FP32 form at every size."""
+    cropped; the bf16x6 form (with the exact ELU, and with the e^x - 1 ELU of
+    FM_ACT_EXP that the decoder uses) also against the FP32 form at every
+    size."""
     g = torch.Generator().manual_seed(B * 17 + L + y_len)
     x = torch.randn(B, 64, L, generator=g)
     w1 = torch.randn(32, 64, 3, generator=g) / math.sqrt(192)
@@ -519,7 +523,8 @@ def test_resblock64_conv_matches_reference(B, L, y_len, x6):
         c1.w, c2.w = with_planes(c1.w), with_planes(c2.w)
         out.fill_(float("nan"))
         nat.call("fm_resblock64_conv", xd.data_ptr(), B, L, c1.w.data_ptr(), c1.b.data_ptr(), c2.w.data_ptr(),
-                 c2.b.data_ptr(), 1 | nat.WEIGHTS_X6, c3.w.data_ptr(), c3.b.data_ptr(), y_len, out.data_ptr(),
+                 c2.b.data_ptr(), 1 | nat.WEIGHTS_X6 | (nat.ACT_EXP if x6 == "act_exp" else 0),
+                 c3.w.data_ptr(), c3.b.data_ptr(), y_len, out.data_ptr(),
                  d.data_ptr(), wsb, stream())
         torch.cuda.synchronize()
         assert not torch.isnan(out).any()
