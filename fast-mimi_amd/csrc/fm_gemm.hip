@@ -1647,8 +1647,11 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
         cfg = kX6;
         splits = s128;
         // Unsplit with two tiles on some CUs: 192x128 tiles, one per CU,
-        // when they fit in one round (C4 res512.c1 at 20000 rows).
+        // when they fit in one round (C4 res512.c1 at 20000 rows); unsplit
+        // with at most one tile per CU: 64x128 tiles, so every CU works
+        // (C2 enc.down5 65 -> 57 us, C2 dec.up6 52 -> 47 us).
         if (s128 == 1 && t128 > 256 && tile_count(M, p.N, kX6Wide) <= 256) cfg = kX6Wide;
+        if (s128 == 1 && t128 <= 256) cfg = kX6Small;
       } else {
         cfg = kX6Small;
         splits = fewest(kX6Small, 8);
@@ -1656,12 +1659,16 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
       tiles = tile_count(M, p.N, cfg);
     } else if (t128 * splits >= 192) {
       // 256x128 where it gives >= 384 tiles, else the direct-load 128x128
-      // tile (the 2500-row qkv projection 34 us against 40 us for 64x128
-      // tiles, the 8000-row output projection 34 against 37 us), or 192x128
-      // (one per CU) where 128x128 would put two on some CUs and 192x128
-      // tiles fit in one round (4000-row qkv 54 -> 45 us).
+      // tile (the 8000-row output projection 34 against 37 us for 64x128
+      // tiles), or 192x128 (one per CU) where 128x128 would put two on some
+      // CUs and 192x128 tiles fit in one round (4000-row qkv 54 -> 45 us), or
+      // 64x128 where unsplit 128x128 tiles would leave CUs idle (2500-row qkv
+      // 32-33 -> 29.6 us, C1 enc.down4 33.5-35 -> 30.7 us, C1 dec.up5
+      // 33-34 -> 30.5 us).  Every bf16x6 tile accumulates an output element
+      // in the same order, so the choice never changes a result.
       cfg = tile_count(M, p.N, kX6Big) >= 384 ? kX6Big : kX6;
       if (cfg.id == kX6.id && t128 > 256 && tile_count(M, p.N, kX6Wide) <= 256) cfg = kX6Wide;
+      if (cfg.id == kX6.id && t128 <= 256 && splits == 1) cfg = kX6Small;
       tiles = tile_count(M, p.N, cfg);
     }
   }

@@ -1222,6 +1222,34 @@ def test_gemm_plan_names_the_launched_kernel():
     assert nat.last_gemm_plan() == "gemm_x6d_kernel<256,128,8,1,2,false> tiles=470 splits=1"
 
 
+@pytest.mark.parametrize("rows,k,n,flags", [(2000, 512, 1536, 0), (2500, 512, 1536, 0),
+                                           (1500, 1024, 2048, 0), (2000, 512, 2048, nat.EPI_GELU)])
+def test_x6_tile_choice_leaves_results_unchanged(rows, k, n, flags, ws):
+    """Every bf16x6 tile accumulates an output element in the same order, so
+    the tile picked for a grid never changes a result: rows computed in a
+    grid of at most 256 128x128 tiles (64x128 tiles) equal, bit for bit, the
+    same rows computed inside a grid twice as tall (192x128 or 128x128
+    tiles)."""
+    g = torch.Generator().manual_seed(rows + k + n)
+    x = torch.randn(rows, k, generator=g).to(DEV)
+    w = with_planes((torch.randn(n, k, generator=g) / math.sqrt(k)).to(DEV))
+    f = flags | nat.WEIGHTS_X6
+    small = torch.empty(rows, n, device=DEV)
+    nat.call("fm_linear", x.data_ptr(), rows, k, w.data_ptr(), n, f, None, None, small.data_ptr(),
+             ws.data_ptr(), WS_BYTES, stream())
+    plan_small = nat.last_gemm_plan()
+    x2 = torch.cat([x, x.flip(0)])
+    big = torch.empty(2 * rows, n, device=DEV)
+    nat.call("fm_linear", x2.data_ptr(), 2 * rows, k, w.data_ptr(), n, f, None, None, big.data_ptr(),
+             ws.data_ptr(), WS_BYTES, stream())
+    plan_big = nat.last_gemm_plan()
+    torch.cuda.synchronize()
+    assert "gemm_x6d_kernel<64,128" in plan_small and "splits=1" in plan_small, plan_small
+    assert "gemm_x6d_kernel<64,128" not in plan_big and "splits=1" in plan_big, plan_big
+    assert torch.equal(small, big[:rows])
+    assert torch.equal(small.flip(0), big[rows:])
+
+
 def test_rvq_split_with_a_per_step_sized_workspace():
     """A workspace sized by fm_rvq_workspace_bytes alone (smaller than the
     one-launch chain needs at a few rows) takes the per-step launches: same
