@@ -74,6 +74,7 @@ _SIGNATURES = {
     "fm_rvq_encode_split_noalloc": ([_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P], _I),
     "fm_rvq_decode": ([_P, _I, _I, _I, _I, _P, _I, _I, _P, _P], _I),
     "fm_upsample_depthwise": ([_P, _I, _I, _I, _P, _I, _I, _P, _P], _I),
+    "fm_copy_buffers": ([_P, _P, _S, _P, _P, _S, _P], _I),
     "fm_resblock_supported": ([_I], _I),
     "fm_resblock": ([_P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P], _I),
     "fm_conv_resblock64": ([_P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P], _I),

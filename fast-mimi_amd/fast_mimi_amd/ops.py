@@ -48,6 +48,7 @@ SPECS = {
     "fm_rvq_encode_split_noalloc": "in:x i:ld_x i:rows i:rows_per_batch i:dim i:entries i:n_semantic i:n_acoustic in:embeds in:embeds_t in:norms out:codes i:batch_stride",
     "fm_rvq_decode": "in:codes i:batch i:num_codebooks i:frames i:num_semantic in:embeds i:entries i:dim out:out",
     "fm_upsample_depthwise": "in:x i:batch i:length i:channels in:weight i:kernel i:stride out:y",
+    "fm_copy_buffers": "in:src0 out:dst0 i:bytes0 in:src1 out:dst1 i:bytes1",
 }
 
 _TYPE = {"i": "int", "f": "float"}

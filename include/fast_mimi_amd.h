@@ -402,6 +402,18 @@ int fm_upsample_depthwise(const float* x, int batch, int length, int channels,
                           const float* weight, int kernel, int stride, float* y,
                           hipStream_t stream);
 
+/*
+ * Copies bytes0 bytes from src0 to dst0 and bytes1 from src1 to dst1 (device
+ * memory, buffers not overlapping; a zero size skips its pair) in one launch
+ * on `stream`.  No reference counterpart: the hipGraph runner uses it to move
+ * a call's input into the graph's static buffer and the graph's outputs into
+ * caller-owned tensors, one launch for what would otherwise be one copy
+ * launch per tensor (the role of the tensor copies around
+ * _MimiCudaGraphRunner.replay, model.py:322-343).
+ */
+int fm_copy_buffers(const void* src0, void* dst0, size_t bytes0, const void* src1, void* dst1,
+                    size_t bytes1, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

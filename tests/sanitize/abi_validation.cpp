@@ -88,6 +88,9 @@ int main() {
   expect("rvq decode null codes", fm_rvq_decode(nullptr, 1, 8, 125, 1, P, 2048, 256, P, S), BAD);
   expect("rvq decode empty", fm_rvq_decode(C, 0, 8, 125, 1, P, 2048, 256, P, S), 0);
   expect("upsample zero kernel", fm_upsample_depthwise(P, 1, 125, 512, P, 0, 2, P, S), BAD);
+  expect("copy null source", fm_copy_buffers(nullptr, P, 16, nullptr, nullptr, 0, S), BAD);
+  expect("copy null second target", fm_copy_buffers(P, P, 0, P, nullptr, 4, S), BAD);
+  expect("copy nothing", fm_copy_buffers(nullptr, nullptr, 0, nullptr, nullptr, 0, S), 0);
 
   // Size queries at the edges of int: computed in size_t, monotone, no overflow.
   const size_t a = fm_rvq_workspace_bytes(INT_MAX, 256, 2048);

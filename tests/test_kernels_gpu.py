@@ -1250,6 +1250,25 @@ def test_x6_tile_choice_leaves_results_unchanged(rows, k, n, flags, ws):
     assert torch.equal(small.flip(0), big[rows:])
 
 
+@pytest.mark.parametrize("n0,n1,off0,off1", [(240000 * 4, 8 * 250 * 8, 0, 0), (1, 17, 0, 0), (1000, 0, 3, 0),
+                                           (4096 + 5, 333, 1, 7), (0, 64, 0, 0), (16 << 20, 12345, 0, 5)])
+def test_copy_buffers(n0, n1, off0, off1):
+    """fm_copy_buffers copies both byte ranges exactly (16-byte vectors when
+    every pointer is aligned, bytes otherwise, zero sizes skipped) and writes
+    nothing outside them."""
+    g = torch.Generator().manual_seed(n0 + n1)
+    src = [torch.randint(0, 256, (n + 16,), generator=g, dtype=torch.uint8).to(DEV) for n in (n0, n1)]
+    dst = [torch.full((n + 32,), 0xA5, dtype=torch.uint8, device=DEV) for n in (n0, n1)]
+    offs = (off0, off1)
+    ptr = lambda t, o: t.data_ptr() + o
+    nat.call("fm_copy_buffers", ptr(src[0], offs[0]), ptr(dst[0], offs[0]), n0,
+             ptr(src[1], offs[1]), ptr(dst[1], offs[1]), n1, stream())
+    torch.cuda.synchronize()
+    for s_, d_, n, o in zip(src, dst, (n0, n1), offs):
+        assert torch.equal(d_[o:o + n], s_[o:o + n])
+        assert bool((d_[:o] == 0xA5).all()) and bool((d_[o + n:] == 0xA5).all())
+
+
 def test_rvq_split_with_a_per_step_sized_workspace():
     """A workspace sized by fm_rvq_workspace_bytes alone (smaller than the
     one-launch chain needs at a few rows) takes the per-step launches: same
