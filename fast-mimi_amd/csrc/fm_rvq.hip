@@ -538,7 +538,8 @@ struct ChainArgs {
   const float* norms[2];   // [count][entries]
   int64_t* codes[2];       // codebook 0 of the branch; codebook j at + j * rows_per_batch
   unsigned long long* partials;  // [2][CHAIN_GROUPS][CHAIN_BLOCKS][32], zeroed before the launch
-  unsigned* status;        // incremented when a wait gives up
+  unsigned* status;        // counts blocks whose wait gave up (block 0 then recomputes alone)
+  long spin_limit;         // polls before a wait gives up
 };
 
 __global__ __launch_bounds__(256, 4) void rvq_chain_kernel(ChainArgs a) {
@@ -567,16 +568,74 @@ __global__ __launch_bounds__(256, 4) void rvq_chain_kernel(ChainArgs a) {
   };
   if (tid == 0) failS = 0;
 
-  // Codebook fragment of this wave: entry e_begin + col, dims kbase + 32 h ..
-  // + 31 (rvq_step_mfma_kernel's load_piece); the block's 32 norms ride along.
+  // Codebook fragment of this wave: entry eb + col, dims kbase + 32 h .. + 31
+  // (rvq_step_mfma_kernel's load_piece); the slice's 32 norms ride along.
   floatx4 cur[8];
   float nrm = 0.0f;
-  auto load_piece = [&](int jj) {
-    const int entry = min(e_begin + col, a.entries - 1);
+  auto load_slice = [&](int jj, int eb) {
+    const int entry = min(eb + col, a.entries - 1);
     const float* src = embeds + ((long)jj * a.entries + entry) * DIM + kbase + 32 * h;
 #pragma unroll
     for (int u = 0; u < 8; ++u) cur[u] = *reinterpret_cast<const floatx4*>(src + 4 * u);
-    if (tid < 32) nrm = e_begin + tid < a.entries ? a.norms[br][(long)jj * a.entries + e_begin + tid] : 0.0f;
+    if (tid < 32) nrm = eb + tid < a.entries ? a.norms[br][(long)jj * a.entries + eb + tid] : 0.0f;
+  };
+  auto load_piece = [&](int jj) { load_slice(jj, e_begin); };
+  // Distances of the 32 residual rows (Xs) to the 32 entries in `cur`, this
+  // wave's k-part: entries on the MFMA rows.
+  auto distances = [&]() {
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const floatx4 b4 = *reinterpret_cast<const floatx4*>(Xs + col * PX + kbase + 32 * h + 4 * jj);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = fm_mfma32(cur[jj][e], b4[e], acc);
+    }
+    // 19 wait states before anything reads the accumulators (a 16-pass
+    // 32x32 MFMA needs 18).  The compiler's own count missed two reads
+    // placed behind a branch, so the wait is explicit, and the tile passes
+    // through the asm so that no read can move above it.
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 2" : "+a"(acc));
+    return acc;
+  };
+  // Every wave publishes its k-part; then wave p finishes entries
+  // 8 (r / 4) + 4 h + (r % 4) for r = 4 p .. 4 p + 3 (four of the sixteen
+  // accumulator rows), summing the k-parts in order 0..3, and leaves its best
+  // entry of slice `eb` per row in bestv / besti[p] (norms from normS).
+  auto slice_best = [&](const floatx16& acc, int eb) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[p][fm_mfma32_row(r, lane) * PR + col] = acc[r];
+    lds_barrier();
+    float best_v = INFINITY;
+    int best_i = 0x7fffffff;
+    const float xq = xnS[col];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int row = fm_mfma32_row(4 * p + rr, lane);
+      float v = red[0][row * PR + col];
+#pragma unroll
+      for (int pp = 1; pp < 4; ++pp) v = __fadd_rn(v, red[pp][row * PR + col]);
+      const int entry = eb + row;
+      if (entry < a.entries) {
+        const float d = __fadd_rn(__fadd_rn(__fmul_rn(-2.0f, v), xq), normS[row]);
+        const float dist = dist_key(d);
+        if (better(dist, entry, best_v, best_i)) best_v = dist, best_i = entry;
+      }
+    }
+    const float ov = __shfl_xor(best_v, 32, 64);
+    const int oi = __shfl_xor(best_i, 32, 64);
+    if (better(ov, oi, best_v, best_i)) best_v = ov, best_i = oi;
+    if (h == 0) bestv[p][col] = best_v, besti[p][col] = best_i;
+    lds_barrier();
+  };
+  // Row `row`'s best over the four waves of the last slice_best.
+  auto block_best = [&](int row, float& v, int& i) {
+    v = bestv[0][row];
+    i = besti[0][row];
+#pragma unroll
+    for (int w = 1; w < 4; ++w)
+      if (better(bestv[w][row], besti[w][row], v, i)) v = bestv[w][row], i = besti[w][row];
   };
   load_piece(0);
 
@@ -600,6 +659,7 @@ __global__ __launch_bounds__(256, 4) void rvq_chain_kernel(ChainArgs a) {
     if (pt == 0) xnS[r] = xn;
   }
 
+  int s_fail = -1;  // step at which a wait of this block gave up
   for (int s = 0; s <= count; ++s) {
     if (s > 0) {
       // Only block 0 of the group needs the last step's codes.
@@ -614,7 +674,7 @@ __global__ __launch_bounds__(256, 4) void rvq_chain_kernel(ChainArgs a) {
       // 56.1 us per call at C2; pipelined polls: 60 us).
       unsigned long long pv[PER] = {};  // (a wait that gives up resolves zeros: index 0)
       bool ready = false;
-      for (long spin = 0; !ready && spin < CHAIN_SPIN; ++spin) {
+      for (long spin = 0; !ready && spin < a.spin_limit; ++spin) {
         if ((unsigned)(fm_load64_coherent(slot(s - 1, pt + 8 * (PER - 1), r)) >> 48) != (unsigned)s) continue;
 #pragma unroll
         for (int u = 0; u < PER; ++u) pv[u] = fm_load64_coherent(slot(s - 1, pt + 8 * u, r));
@@ -643,7 +703,13 @@ __global__ __launch_bounds__(256, 4) void rvq_chain_kernel(ChainArgs a) {
         const long b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
         a.codes[br][(long)(s - 1) * a.rows_per_batch + b * a.batch_stride + t] = bi;
       }
-      if (s == count) break;
+      if (s == count) {
+        // The last resolve (block 0 only): one barrier per call to learn
+        // whether one of its waits gave up.
+        lds_barrier();
+        if (failS) s_fail = s;
+        break;
+      }
       // residual_s = residual_{s-1} - e_{s-1}[code], and its |.|^2.
       const float* er = embeds + ((long)(s - 1) * a.entries + bi) * DIM;
       floatx4 ev[CH];
@@ -668,63 +734,95 @@ __global__ __launch_bounds__(256, 4) void rvq_chain_kernel(ChainArgs a) {
     if (tid < 32) normS[tid] = nrm;
     lds_barrier();
     if (failS) {
-      if (tid == 0) __hip_atomic_fetch_add(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return;
+      s_fail = s;
+      break;
     }
 
     // Distances: 32 entries (A, from registers) x 32 rows (B, from LDS), this wave's k-part.
-    floatx16 acc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      const floatx4 b4 = *reinterpret_cast<const floatx4*>(Xs + col * PX + kbase + 32 * h + 4 * jj);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc = fm_mfma32(cur[jj][e], b4[e], acc);
-    }
+    const floatx16 acc = distances();
     // Next codebook's fragment and norms go out now; their latency hides
-    // behind the reduction and the resolve.
-    if (s + 1 < count) load_piece(s + 1);
-    // Every wave publishes its k-part; then wave p finishes entries
-    // 8 (r / 4) + 4 h + (r % 4) for r = 4 p .. 4 p + 3 (four of the sixteen
-    // accumulator rows), summing the k-parts in order 0..3.
-#pragma unroll
-    for (int r = 0; r < 16; ++r) red[p][fm_mfma32_row(r, lane) * PR + col] = acc[r];
-    lds_barrier();
-    {
-      float best_v = INFINITY;
-      int best_i = 0x7fffffff;
-      const float xq = xnS[col];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int row = fm_mfma32_row(4 * p + rr, lane);
-        float v = red[0][row * PR + col];
-#pragma unroll
-        for (int pp = 1; pp < 4; ++pp) v = __fadd_rn(v, red[pp][row * PR + col]);
-        const int entry = e_begin + row;
-        if (entry < a.entries) {
-          const float d = __fadd_rn(__fadd_rn(__fmul_rn(-2.0f, v), xq), normS[row]);
-          const float dist = dist_key(d);
-          if (better(dist, entry, best_v, best_i)) best_v = dist, best_i = entry;
-        }
-      }
-      const float ov = __shfl_xor(best_v, 32, 64);
-      const int oi = __shfl_xor(best_i, 32, 64);
-      if (better(ov, oi, best_v, best_i)) best_v = ov, best_i = oi;
-      if (h == 0) bestv[p][col] = best_v, besti[p][col] = best_i;
-    }
-    lds_barrier();
+    // behind the reduction and the resolve (the last step reloads its own
+    // piece: no branch between the MFMAs and the accumulator reads).
+    load_piece(min(s + 1, count - 1));
+    slice_best(acc, e_begin);
     if (tid < RB) {
-      float v = bestv[0][tid];
-      int i = besti[0][tid];
-#pragma unroll
-      for (int w = 1; w < 4; ++w)
-        if (better(bestv[w][tid], besti[w][tid], v, i)) v = bestv[w][tid], i = besti[w][tid];
+      float v;
+      int i;
+      block_best(tid, v, i);
       // A block with no entries in range publishes +inf (index 0xffff).
       if (i > 0xffff) i = 0xffff;
       fm_store64_coherent(slot(s, q, tid), ((unsigned long long)(s + 1) << 48) |
                                                ((unsigned long long)(unsigned)i << 32) | __float_as_uint(v));
     }
+  }
+  if (s_fail < 0) return;
+  if (tid == 0) __hip_atomic_fetch_add(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // A wait gave up (a block of the group never became resident in time,
+  // say).  Only block 0 writes codes: the others leave, and block 0 (whose
+  // own waits then give up too, if they had not) computes the whole chain
+  // again alone, from the input rows, with every slice's distances and the
+  // arithmetic above, so the codes are the ones the group would have
+  // resolved.  Slower, never wrong; every wait is bounded, so the grid
+  // drains.
+  if (q != 0) return;
+  const int r = tid >> 3, pt = tid & 7;
+  const long m = m0 + r;
+  const bool valid = m < a.M;
+  {
+    const float* xr = a.x + min(m, (long)a.M - 1) * a.ld_x + br * DIM;
+    float xn = 0.0f;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      floatx4 xv = *reinterpret_cast<const floatx4*>(xr + 4 * (pt + 8 * u));
+      if (!valid) xv = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xn = fmaf(xv[e], xv[e], xn);
+      *reinterpret_cast<floatx4*>(Xs + r * PX + 4 * (pt + 8 * u)) = xv;
+    }
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) xn += __shfl_xor(xn, o, 64);
+    if (pt == 0) xnS[r] = xn;
+  }
+  for (int jj = 0; jj < count; ++jj) {
+    float fv = INFINITY;
+    int fi = 0x7fffffff;
+    for (int qs = 0; qs * 32 < a.entries; ++qs) {
+      load_slice(jj, qs * 32);
+      if (tid < 32) normS[tid] = nrm;
+      lds_barrier();
+      slice_best(distances(), qs * 32);
+      if (tid < RB) {
+        float v;
+        int i;
+        block_best(tid, v, i);
+        if (better(v, i, fv, fi)) fv = v, fi = i;
+      }
+    }
+    if (tid < RB) besti[0][tid] = fi;
+    lds_barrier();
+    const int bi = code_index(besti[0][r], a.entries);
+    if (pt == 0 && valid) {
+      const long b = m / a.rows_per_batch, t = m - b * a.rows_per_batch;
+      a.codes[br][(long)jj * a.rows_per_batch + b * a.batch_stride + t] = bi;
+    }
+    if (jj + 1 == count) break;
+    const float* er = embeds + ((long)jj * a.entries + bi) * DIM;
+    float xn = 0.0f;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const floatx4 ev = *reinterpret_cast<const floatx4*>(er + 4 * (pt + 8 * u));
+      floatx4 xv = *reinterpret_cast<const floatx4*>(Xs + r * PX + 4 * (pt + 8 * u));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xv[e] = __fsub_rn(xv[e], ev[e]);
+      if (!valid) xv = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xn = fmaf(xv[e], xv[e], xn);
+      *reinterpret_cast<floatx4*>(Xs + r * PX + 4 * (pt + 8 * u)) = xv;
+    }
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) xn += __shfl_xor(xn, o, 64);
+    if (pt == 0) xnS[r] = xn;
+    lds_barrier();
   }
 }
 
@@ -1063,6 +1161,10 @@ int fm_rvq_encode_split(const float* x, int ld_x, int rows, int rows_per_batch, 
     c.codes[0] = codes; c.codes[1] = codes + (size_t)n_semantic * rows_per_batch;
     c.partials = reinterpret_cast<unsigned long long*>(ws);
     c.status = reinterpret_cast<unsigned*>(ws + CHAIN_PARTIALS * 8);
+    // FM_RVQ_CHAIN_SPIN (tests) lowers the polls a wait may take before its
+    // block goes solo; 0 sends every block down that path.
+    c.spin_limit = CHAIN_SPIN;
+    if (const char* v = getenv("FM_RVQ_CHAIN_SPIN")) c.spin_limit = std::max(0L, atol(v));
     const long words = (long)CHAIN_PARTIALS + 1;  // the status word follows the slots
     hipLaunchKernelGGL(rvq_chain_reset_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream,
                        c.partials, words);

@@ -1057,6 +1057,42 @@ def test_rvq_encode_split_matches_two_branches(B, T, nsem, nac, e, d):
              emb_t.data_ptr(), norms.data_ptr(), codes.data_ptr(), n * T, ws.data_ptr(), wsb, stream())
 
 
+@pytest.mark.parametrize("B,T,nsem,nac,e,spin", [
+    (1, 128, 1, 7, 2048, "0"),    # every wait gives up at the first resolve
+    (1, 97, 2, 5, 1000, "0"),     # ragged entries and a partial tile
+    (2, 33, 1, 31, 2048, "0"),    # long acoustic chain
+    (1, 125, 1, 7, 2048, "3"),    # a few polls: waits give up at different steps
+])
+def test_rvq_chain_recomputes_alone_when_a_wait_gives_up(B, T, nsem, nac, e, spin, monkeypatch):
+    """When a wait of the one-launch chain for other blocks' partials gives
+    up, block 0 of the group computes the whole chain again alone, from all
+    entries' distances with the same arithmetic: the codes still equal the
+    per-branch launches bit for bit.  The wait limit is lowered from the
+    host (FM_RVQ_CHAIN_SPIN), so every kernel still ends normally."""
+    monkeypatch.setenv("FM_RVQ_CHAIN_SPIN", spin)
+    d = 256
+    g = torch.Generator().manual_seed(B * T + nsem + nac + e)
+    n = nsem + nac
+    emb, emb_t, norms = prepare_codebooks(torch.randn(n, e, d, generator=g) / 16, torch.ones(n, e))
+    M = B * T
+    x = (torch.randn(M, 2 * d, generator=g) * 0.3).to(DEV)
+    lib = nat.library()
+    codes = torch.full((B, n, T), -1, dtype=torch.int64, device=DEV)
+    wsb = lib.fm_rvq_split_workspace_bytes(M, d, e)
+    ws = torch.empty((wsb + 3) // 4, device=DEV)
+    nat.call("fm_rvq_encode_split", x.data_ptr(), 2 * d, M, T, d, e, nsem, nac, emb.data_ptr(),
+             emb_t.data_ptr(), norms.data_ptr(), codes.data_ptr(), n * T, ws.data_ptr(), wsb, stream())
+    want = torch.full((B, n, T), -2, dtype=torch.int64, device=DEV)
+    wsb1 = lib.fm_rvq_workspace_bytes(M, d, e)
+    ws1 = torch.empty((wsb1 + 3) // 4, device=DEV)
+    for col, first, count in ((0, 0, nsem), (d, nsem, nac)):
+        nat.call("fm_rvq_encode", x.data_ptr() + col * 4, 2 * d, M, T, d, e, count,
+                 emb[first].data_ptr(), emb_t[first].data_ptr(), norms[first].data_ptr(),
+                 want.data_ptr() + first * T * 8, n * T, ws1.data_ptr(), wsb1, stream())
+    torch.cuda.synchronize()
+    assert torch.equal(codes.cpu(), want.cpu())
+
+
 def test_rvq_tie_picks_lowest_index():
     e, d = 256, 256
     g = torch.Generator().manual_seed(9)
