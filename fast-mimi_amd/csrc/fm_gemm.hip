@@ -1090,7 +1090,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
   // Epilogue passes of EG wave rows: the most that fit in the k-loop's LDS
   // (fewer passes, fewer barriers), else the fewest that the block's rows
   // per store step divide.
-  constexpr int CG = BN / 4, RSTEP = NTH / CG, PC = BN + 4;
+  // Output tile pitch: rows four apart (the two half-waves of an
+  // accumulator store) 32 banks apart, so the stores do not conflict.
+  constexpr int CG = BN / 4, RSTEP = NTH / CG, PC = BN + 8;
   constexpr int EG0 = (WTM % RSTEP == 0) ? 1 : (2 * WTM % RSTEP == 0 && WM % 2 == 0) ? 2 : 3;
   constexpr auto fits = [](int g) { return WM % g == 0 && (g * WTM) % RSTEP == 0 && g * WTM * PC * 4 <= NST * STAGE; };
   constexpr int EG = fits(4) ? 4 : fits(3) ? 3 : fits(2) ? 2 : EG0;
@@ -1141,8 +1143,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
   for (int q = 0; q < NBW; ++q) {
     const int i = min(wave + q * NW, NBI - 1);
     const int pl = i / (BN / 32), rg = i % (BN / 32);
-    const int row = rg * 32 + (lane >> 1);
-    b_voff[q] = n0 + row < p.N ? (int)((pl * KN + (long)(n0 + row) * 16 + 8 * (lane & 1)) * 2) : INT_MIN;
+    // Lane l carries k-half l / 32 of row l % 32, so each 32-row group lands
+    // in LDS as [k-half][row][16 bytes] and a fragment read (16 lanes = 16
+    // consecutive rows of one half) covers 256 contiguous bytes: no bank
+    // conflicts ([row][half] order gave every pass a two-way conflict).
+    const int row = rg * 32 + (lane & 31);
+    b_voff[q] = n0 + row < p.N ? (int)((pl * KN + (long)(n0 + row) * 16 + 8 * (lane >> 5)) * 2) : INT_MIN;
     b_lds[q] = pl * PLANE_B + rg * 32 * BK * 2;
   }
   auto issue = [&](int stage, int k0) {
@@ -1218,7 +1224,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
     }
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const char* bb = Bs + (wn0 + 32 * j + lrow) * (BK * 2) + lk * 16;
+      const char* bb = Bs + (wn0 + 32 * j) * (BK * 2) + lk * 512 + lrow * 16;
       b0[j] = *reinterpret_cast<const bf16x8*>(bb);
       b1[j] = *reinterpret_cast<const bf16x8*>(bb + PLANE_B);
       b2[j] = *reinterpret_cast<const bf16x8*>(bb + 2 * PLANE_B);
