@@ -30,7 +30,8 @@ enum FmGemmFlags {
   FM_EPI_RES_ADD = 16,  // y = res + (acc + bias)
   FM_EPI_RES_SCALE = 32, // y = res + scale[n] * acc
   FM_WEIGHTS_X6 = 64,    // weight_packed is followed by its three bf16 planes (fm_split_weights)
-  FM_ACT_EXP = 128       // residual blocks: ELUs as e^x - 1 (fm_elu_exp), for decoder-side calls
+  FM_ACT_EXP = 128,      // residual blocks: ELUs as e^x - 1 (fm_elu_exp), for decoder-side calls
+  FM_EPI_ROPE = 256      // internal (fm_linear_rope): RoPE on the first rope_cols output columns
 };
 
 // e^x - 1 for x <= 0, branch-free.  Near zero (x > -1/4) x * q(x), q a

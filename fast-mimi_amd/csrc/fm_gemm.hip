@@ -36,6 +36,10 @@
 #include <cstdio>
 #include "fm_common.h"
 
+extern "C" int fm_apply_rope(float* x, long rows, int ld, int rope_cols, int head_dim,
+                             const float* cos_table, const float* sin_table, int rows_per_seq,
+                             hipStream_t stream);
+
 namespace {
 
 struct GemmArgs {
@@ -48,6 +52,11 @@ struct GemmArgs {
   float* partial;  // global split-K partials [splits][M][N], or null
   int batch, L_in, C_in, rows, rs, padL, K, N, y_rows, bias_len, k_split, flags;
   FmDivisor rows_div;  // division by `rows` (set by run_gemm)
+  // FM_EPI_ROPE: cos/sin tables [*][64] at position row % rows_per_seq for
+  // output columns < rope_cols (heads of 64 columns).
+  const float* rope_cos;
+  const float* rope_sin;
+  int rope_cols, rows_per_seq;
 };
 
 constexpr int KT = 32;  // k granularity of K-splits (every tile's BK divides it or is 64)
@@ -1259,6 +1268,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
   const int c = (tid % CG) * 4, r0 = tid / CG;
   const int n = n0 + c;
   const bool n_ok = n < p.N;
+  const bool rope = (p.flags & FM_EPI_ROPE) && n < p.rope_cols;
+  const bool rope_lo = (c & 32) == 0;  // first half of a 64-column head
   const int ncl = n_ok ? n : 0;
   const floatx4 bias = (p.bias && !part) ? *reinterpret_cast<const floatx4*>(p.bias + ncl % p.bias_len)
                                          : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1289,6 +1300,23 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
         v[u] = *reinterpret_cast<const floatx4*>(fsm + r * PC + c);
         res[u] = (has_res && !part) ? *reinterpret_cast<const floatx4*>(p.res + m * p.N + ncl)
                                     : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+      if (rope) {
+        // RoPE with the partner columns of the same 64-column head (c ^ 32,
+        // in this tile), each product and the sum rounded separately:
+        // x*cos - x[d+32]*sin for d < 32, x*cos + x[d-32]*sin after.
+#pragma unroll
+        for (int u = 0; u < RB; ++u) {
+          const int r = r0 + (u0 + u) * RSTEP;
+          const long m = min(mh + r, M - 1);
+          const int t = (int)(m % p.rows_per_seq);
+          const floatx4 pv = *reinterpret_cast<const floatx4*>(fsm + r * PC + (c ^ 32));
+          const floatx4 cs = *reinterpret_cast<const floatx4*>(p.rope_cos + (long)t * 64 + (c & 63));
+          const floatx4 sn = *reinterpret_cast<const floatx4*>(p.rope_sin + (long)t * 64 + (c & 63));
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            v[u][e] = __fadd_rn(__fmul_rn(v[u][e], cs[e]), __fmul_rn(rope_lo ? -pv[e] : pv[e], sn[e]));
+        }
       }
 #pragma unroll
       for (int u = 0; u < RB; ++u) {
@@ -1678,6 +1706,12 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
       tiles = tile_count(M, p.N, cfg);
     }
   }
+  // The RoPE epilogue needs whole unsplit bf16x6 tiles (the partner columns
+  // of a head sit in the block's output tile in LDS).  Any other plan stays
+  // as selected, so the projection rounds as fm_linear's, and RoPE follows
+  // as its own launch.
+  const bool rope_after = (p.flags & FM_EPI_ROPE) && (!(cfg.id >= 16 && cfg.id <= 19) || splits != 1);
+  if (rope_after) p.flags &= ~FM_EPI_ROPE;
   if (splits > 1) {
     const size_t per = (size_t)M * p.N * sizeof(float);
     while (splits > 1 && per * splits > workspace_bytes) --splits;
@@ -1755,7 +1789,10 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     const int blocks = (int)std::min<long>((total + 255) / 256, 2048);
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, p, splits);
     e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
   }
+  if (rope_after)
+    return fm_apply_rope(p.y, M, p.N, p.rope_cols, 64, p.rope_cos, p.rope_sin, p.rows_per_seq, s);
   return (int)e;
 }
 
@@ -1856,7 +1893,24 @@ int fm_linear(const float* x, int rows, int in_features, const float* weight_pac
   p.x = x; p.w = weight_packed; p.bias = nullptr; p.res = residual; p.scale = scale; p.y = y;
   p.batch = 1; p.L_in = rows; p.C_in = in_features; p.rows = rows; p.rs = 1; p.padL = 0;
   p.K = in_features; p.N = out_features; p.y_rows = rows; p.bias_len = 0;
-  p.flags = flags & ~(FM_REPLICATE | FM_ELU_IN);
+  p.flags = flags & ~(FM_REPLICATE | FM_ELU_IN | FM_EPI_ROPE);
+  return run_gemm(p, workspace, workspace_bytes, stream);
+}
+
+int fm_linear_rope(const float* x, int rows, int in_features, const float* weight_packed,
+                   int out_features, int flags, const float* cos_table, const float* sin_table,
+                   int rope_cols, int rows_per_seq, float* y, float* workspace, size_t workspace_bytes,
+                   hipStream_t stream) {
+  if (!cos_table || !sin_table || rope_cols <= 0 || rope_cols % 64 || rope_cols > out_features ||
+      out_features % 64 || rows_per_seq <= 0)
+    return FM_BAD_ARGUMENT;
+  if (flags != FM_WEIGHTS_X6) return FM_UNSUPPORTED;  // bf16x6 tiles only, no other epilogue
+  GemmArgs p{};
+  p.x = x; p.w = weight_packed; p.bias = nullptr; p.res = nullptr; p.scale = nullptr; p.y = y;
+  p.batch = 1; p.L_in = rows; p.C_in = in_features; p.rows = rows; p.rs = 1; p.padL = 0;
+  p.K = in_features; p.N = out_features; p.y_rows = rows; p.bias_len = 0;
+  p.flags = FM_WEIGHTS_X6 | FM_EPI_ROPE;
+  p.rope_cos = cos_table; p.rope_sin = sin_table; p.rope_cols = rope_cols; p.rows_per_seq = rows_per_seq;
   return run_gemm(p, workspace, workspace_bytes, stream);
 }
 

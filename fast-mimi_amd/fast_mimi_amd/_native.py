@@ -56,6 +56,7 @@ _SIGNATURES = {
     "fm_conv1d_valid": ([_P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _S, _P], _I),
     "fm_conv_transpose1d": ([_P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _S, _P], _I),
     "fm_linear": ([_P, _I, _I, _P, _I, _I, _P, _P, _P, _P, _S, _P], _I),
+    "fm_linear_rope": ([_P, _I, _I, _P, _I, _I, _P, _P, _I, _I, _P, _P, _S, _P], _I),
     "fm_row_linear_supported": ([_I, _I], _I),
     "fm_row_linear": ([_P, _I, _I, _P, _P, _F, _P, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P], _I),
     "fm_row_linear_packed": ([_P, _I, _I, _P, _P, _F, _P, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P], _I),

@@ -31,6 +31,7 @@ SPECS = {
     "fm_conv1d_valid": "in:x i:batch i:length i:in_channels in:weight_packed in:bias i:out_channels i:kernel i:stride i:flags res:residual out:y out:workspace i:workspace_bytes",
     "fm_conv_transpose1d": "in:x i:batch i:length i:in_channels in:weight_packed in:bias i:out_channels i:kernel i:stride i:flags res:residual out:y out:workspace i:workspace_bytes",
     "fm_linear": "in:x i:rows i:in_features in:weight_packed i:out_features i:flags res:residual in:scale out:y out:workspace i:workspace_bytes",
+    "fm_linear_rope": "in:x i:rows i:in_features in:weight_packed i:out_features i:flags in:cos_table in:sin_table i:rope_cols i:rows_per_seq out:y out:workspace i:workspace_bytes",
     "fm_resblock": "in:x i:batch i:length i:channels in:w1_packed in:b1 in:w2_packed in:b2 i:elu_out out:y",
     "fm_conv_resblock64": "in:wav i:batch i:length in:w0_packed in:b0 in:w1_packed in:b1 in:w2_packed in:b2 i:elu_out out:y",
     "fm_resblock64_conv": "in:x i:batch i:length in:w1_packed in:b1 in:w2_packed in:b2 i:elu_mid in:w3_packed in:b3 i:y_len out:out out:workspace i:workspace_bytes",

@@ -328,6 +328,15 @@ class MimiRuntime:
                  scale, y, self.workspace, _WORKSPACE_BYTES)
         return y
 
+    def _linear_rope(self, x, rows, w, cos, sin, rope_cols, per_seq):
+        """q/k/v projection with RoPE in the bf16x6 GEMM's epilogue (the
+        attention then reads rotated q / k)."""
+        n, k = w.shape
+        y = torch.empty((rows, n), device=self.device)
+        self._call("fm_linear_rope", x, rows, k, self._x6[w.data_ptr()], n, nat.WEIGHTS_X6, cos, sin,
+                   rope_cols, per_seq, y, self.workspace, _WORKSPACE_BYTES)
+        return y
+
     def _proj(self, x, rows, w, flags=0, residual=None, scale=None, out=None):
         """Plain projection: row-block kernel for few rows, tiled GEMM otherwise."""
         n, k = w.shape
@@ -420,6 +429,11 @@ class MimiRuntime:
                  and lib.fm_row_linear_supported(nh * hd, C))
         rope_cols = (nh + nkv) * hd
         for li, lay in enumerate(layers):
+            # Above the row-block sizes RoPE rides in the tiled qkv GEMM's
+            # epilogue when its weight carries bf16x6 planes (4 us per layer
+            # less than rotating in the attention kernels at 2500-4000 rows).
+            rope_gemm = (not fused and hd == 64 and rope_cols % 64 == 0
+                         and self._x6.get(lay.wqkv.data_ptr(), lay.wqkv) is not lay.wqkv)
             if fused:
                 self._tag = f"{tag}{li}.qkv"
                 qkv = self._row_linear(h, M, lay.wqkv, ln=lay.ln1, rope=(cos, sin, rope_cols, T))
@@ -428,10 +442,13 @@ class MimiRuntime:
                 self._call("fm_layer_norm", h, lay.ln1[0],
                            lay.ln1[1], M, C, cfg.norm_eps, xln)
                 self._tag = f"{tag}{li}.qkv"
-                qkv = self._linear(xln, M, lay.wqkv)
+                if rope_gemm:
+                    qkv = self._linear_rope(xln, M, lay.wqkv, cos, sin, rope_cols, T)
+                else:
+                    qkv = self._linear(xln, M, lay.wqkv)
             ld = qkv.shape[1]
             self._tag = f"{tag}{li}.attn"
-            tabs = (None, None) if fused else (cos, sin)
+            tabs = (None, None) if fused or rope_gemm else (cos, sin)
             self._call("fm_window_attention", qkv, ld, 0, nh * hd, (nh + nkv) * hd,
                        tabs[0], tabs[1], B, T, nh, nkv, hd, cfg.sliding_window,
                        1.0 / (hd ** 0.5), att, nh * hd)

@@ -267,6 +267,25 @@ int fm_pack_row_weights(const float* weight, int out_features, int in_features, 
                         hipStream_t stream);
 
 /*
+ * fm_linear (no residual, no other epilogue) with RoPE applied in the
+ * epilogue: output columns 0 .. rope_cols-1 form heads of 64 columns, and
+ * column d of a head at row position t = row % rows_per_seq becomes
+ * y[d] * cos[t][d] - y[d + 32] * sin[t][d] (d < 32) or
+ * y[d] * cos[t][d] + y[d - 32] * sin[t][d] (d >= 32), each product and the
+ * sum rounded separately, as fm_apply_rope.  cos/sin tables [*][64].
+ * flags must be FM_WEIGHTS_X6 (weights with planes); out_features and
+ * rope_cols multiples of 64.  Equal, bit for bit, to fm_linear followed by
+ * fm_apply_rope: one launch when fm_linear's plan is an unsplit bf16x6 tile
+ * (RoPE in its epilogue), else that plan and then fm_apply_rope.
+ * Replaces the q / k projections of MimiAttention with _apply_rope
+ * (model.py:1870-1961, :1551-1569).
+ */
+int fm_linear_rope(const float* x, int rows, int in_features, const float* weight_packed,
+                   int out_features, int flags, const float* cos_table, const float* sin_table,
+                   int rope_cols, int rows_per_seq, float* y, float* workspace,
+                   size_t workspace_bytes, hipStream_t stream);
+
+/*
  * In-place RoPE on columns 0 .. rope_cols-1 of each row (heads of head_dim;
  * position row % rows_per_seq into the [*, head_dim] cos/sin tables), for
  * projections computed without fm_row_linear's fused epilogue (e.g. cached

@@ -88,6 +88,10 @@ int main() {
   expect("rvq decode null codes", fm_rvq_decode(nullptr, 1, 8, 125, 1, P, 2048, 256, P, S), BAD);
   expect("rvq decode empty", fm_rvq_decode(C, 0, 8, 125, 1, P, 2048, 256, P, S), 0);
   expect("upsample zero kernel", fm_upsample_depthwise(P, 1, 125, 512, P, 0, 2, P, S), BAD);
+  expect("linear rope null table", fm_linear_rope(P, 4000, 512, P, 1536, 64, nullptr, P, 1024, 250, P, P, 1 << 20, S), BAD);
+  expect("linear rope ragged head", fm_linear_rope(P, 4000, 512, P, 1536, 64, P, P, 1000, 250, P, P, 1 << 20, S), BAD);
+  expect("linear rope past the columns", fm_linear_rope(P, 4000, 512, P, 1536, 64, P, P, 1600, 250, P, P, 1 << 20, S), BAD);
+  expect("linear rope FP32 weights", fm_linear_rope(P, 4000, 512, P, 1536, 0, P, P, 1024, 250, P, P, 1 << 20, S), UNSUP);
   expect("copy null source", fm_copy_buffers(nullptr, P, 16, nullptr, nullptr, 0, S), BAD);
   expect("copy null second target", fm_copy_buffers(P, P, 0, P, nullptr, 4, S), BAD);
   expect("copy nothing", fm_copy_buffers(nullptr, nullptr, 0, nullptr, nullptr, 0, S), 0);

@@ -1305,6 +1305,38 @@ def test_copy_buffers(n0, n1, off0, off1):
         assert bool((d_[:o] == 0xA5).all()) and bool((d_[o + n:] == 0xA5).all())
 
 
+@pytest.mark.parametrize("rows,per_seq,k,n,rope_cols,fused", [
+    (2500, 2500, 512, 1536, 1024, True),   # C4 qkv: 64x128 tiles
+    (4000, 250, 512, 1536, 1024, True),    # C3 qkv: 192x128 tiles, 16 sequences
+    (16000, 250, 512, 1536, 1024, True),   # C5 qkv: 256x128 tiles
+    (1100, 100, 512, 1536, 512, False),    # an FP32 tile: the GEMM, then fm_apply_rope
+    (1500, 250, 2048, 512, 512, False),    # a split plan: likewise
+])
+def test_linear_rope_equals_linear_then_rope(rows, per_seq, k, n, rope_cols, fused, ws):
+    """fm_linear_rope equals fm_linear followed by fm_apply_rope bit for bit:
+    RoPE in the epilogue of an unsplit bf16x6 tile, else fm_linear's own
+    plan and then the RoPE kernel (so the projection rounds the same)."""
+    from fast_mimi_amd import MimiConfig
+    from fast_mimi_amd.runtime import rope_tables
+
+    g = torch.Generator().manual_seed(rows + k + n)
+    x = torch.randn(rows, k, generator=g).to(DEV)
+    w = with_planes((torch.randn(n, k, generator=g) / math.sqrt(k)).to(DEV))
+    cos, sin = (t.to(DEV) for t in rope_tables(MimiConfig(), per_seq))
+    want = torch.empty(rows, n, device=DEV)
+    nat.call("fm_linear", x.data_ptr(), rows, k, w.data_ptr(), n, nat.WEIGHTS_X6, None, None,
+             want.data_ptr(), ws.data_ptr(), WS_BYTES, stream())
+    nat.call("fm_apply_rope", want.data_ptr(), rows, n, rope_cols, 64, cos.data_ptr(), sin.data_ptr(),
+             per_seq, stream())
+    got = torch.full((rows, n), float("nan"), device=DEV)
+    nat.call("fm_linear_rope", x.data_ptr(), rows, k, w.data_ptr(), n, nat.WEIGHTS_X6, cos.data_ptr(),
+             sin.data_ptr(), rope_cols, per_seq, got.data_ptr(), ws.data_ptr(), WS_BYTES, stream())
+    plan = nat.last_gemm_plan()
+    torch.cuda.synchronize()
+    assert ("gemm_x6d_kernel" in plan and "splits=1" in plan) == fused, plan
+    assert torch.equal(got, want)
+
+
 def test_rvq_split_with_a_per_step_sized_workspace():
     """A workspace sized by fm_rvq_workspace_bytes alone (smaller than the
     one-launch chain needs at a few rows) takes the per-step launches: same
