@@ -1086,16 +1086,19 @@ __global__ __launch_bounds__(256) void split_weights_kernel(const float* __restr
 // (eight waves of 32 x 128, 56 KB, two blocks per CU) where it gives at least
 // 384 tiles; 128 x 128 / 64 x 128 / 192 x 128 (waves of 32 x 64) for smaller
 // grids.
-template <int BM, int BN, int WM, int WN, int NST, bool ELU>
+template <int BM, int BN, int WM, int WN, int NST, bool ELU, int KS = 1>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, const __bf16* __restrict__ w3) {
-  constexpr int NW = WM * WN, NTH = 64 * NW, BK = 16;
+  // KS 16-deep k sub-tiles per stage (BK = 16 KS), run in k order.
+  constexpr int NW = WM * WN, NTH = 64 * NW, BK = 16 * KS;
   static_assert(NW % 2 == 0 && NW <= 12 && NST == 2, "two to twelve waves, two stages");
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 32, FN = WTN / 32;
-  constexpr int CPR = 4, RPI = 16, SWR = 4;  // A: chunks per row, rows per load instruction
+  // A: 16-byte chunks per row, rows per load instruction, and the swizzle
+  // period that gives 16 consecutive rows 16 distinct bank groups.
+  constexpr int CPR = 4 * KS, RPI = 64 / CPR, SWR = 16 / CPR;
   constexpr int AI = BM / (NW * RPI);        // A load instructions per wave per stage
   static_assert(AI >= 1 && AI * NW * RPI == BM && FM >= 1 && FN >= 1 && BN % 32 == 0, "tiling");
   constexpr int PLANE_B = BN * BK * 2, STAGE_A = BM * BK * 4, STAGE = STAGE_A + 3 * PLANE_B;
-  constexpr int NBI = 3 * BN / 32;  // 1 KB B load instructions per stage
+  constexpr int NBI = 3 * KS * BN / 32;  // 1 KB B load instructions per stage
   // Epilogue passes of EG wave rows: the most that fit in the k-loop's LDS
   // (fewer passes, fewer barriers), else the fewest that the block's rows
   // per store step divide.
@@ -1151,14 +1154,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
 #pragma unroll
   for (int q = 0; q < NBW; ++q) {
     const int i = min(wave + q * NW, NBI - 1);
-    const int pl = i / (BN / 32), rg = i % (BN / 32);
+    const int pl = i / (KS * BN / 32), kt = i % (KS * BN / 32) / (BN / 32), rg = i % (BN / 32);
     // Lane l carries k-half l / 32 of row l % 32, so each 32-row group lands
     // in LDS as [k-half][row][16 bytes] and a fragment read (16 lanes = 16
     // consecutive rows of one half) covers 256 contiguous bytes: no bank
     // conflicts ([row][half] order gave every pass a two-way conflict).
     const int row = rg * 32 + (lane & 31);
-    b_voff[q] = n0 + row < p.N ? (int)((pl * KN + (long)(n0 + row) * 16 + 8 * (lane >> 5)) * 2) : INT_MIN;
-    b_lds[q] = pl * PLANE_B + rg * 32 * BK * 2;
+    b_voff[q] = n0 + row < p.N ? (int)((pl * KN + (long)kt * p.N * 16 + (long)(n0 + row) * 16 + 8 * (lane >> 5)) * 2)
+                               : INT_MIN;
+    b_lds[q] = pl * PLANE_B + kt * BN * 32 + rg * 1024;
   }
   auto issue = [&](int stage, int k0) {
     char* As = smem + stage * STAGE;
@@ -1213,47 +1217,50 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
     if (kt + 1 < nkt) issue((kt + 1) % NST, k_begin + (kt + 1) * BK);
     const char* As = smem + (kt % NST) * STAGE;
     const char* Bs = As + STAGE_A;
-    bf16x8 a0[FM], a1[FM], a2[FM], b0[FN], b1[FN], b2[FN];
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int row = wm0 + 32 * i + lrow;
-      const int sw = (row / SWR) & (CPR - 1);
-      floatx4 v0 = *reinterpret_cast<const floatx4*>(As + row * BK * 4 + 16 * ((2 * lk) ^ sw));
-      floatx4 v1 = *reinterpret_cast<const floatx4*>(As + row * BK * 4 + 16 * ((2 * lk + 1) ^ sw));
-      if (elu_in) {
+    for (int ks = 0; ks < KS; ++ks) {
+      bf16x8 a0[FM], a1[FM], a2[FM], b0[FN], b1[FN], b2[FN];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v0[e] = fm_elu(v0[e]), v1[e] = fm_elu(v1[e]);
+      for (int i = 0; i < FM; ++i) {
+        const int row = wm0 + 32 * i + lrow;
+        const int sw = (row / SWR) & (CPR - 1);
+        floatx4 v0 = *reinterpret_cast<const floatx4*>(As + row * BK * 4 + 16 * ((4 * ks + 2 * lk) ^ sw));
+        floatx4 v1 = *reinterpret_cast<const floatx4*>(As + row * BK * 4 + 16 * ((4 * ks + 2 * lk + 1) ^ sw));
+        if (elu_in) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v0[e] = fm_elu(v0[e]), v1[e] = fm_elu(v1[e]);
+        }
+        bf16x4 l0, l1, l2, h0, h1, h2;
+        split3(v0, l0, l1, l2);
+        split3(v1, h0, h1, h2);
+        a0[i] = __builtin_shufflevector(l0, h0, 0, 1, 2, 3, 4, 5, 6, 7);
+        a1[i] = __builtin_shufflevector(l1, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+        a2[i] = __builtin_shufflevector(l2, h2, 0, 1, 2, 3, 4, 5, 6, 7);
       }
-      bf16x4 l0, l1, l2, h0, h1, h2;
-      split3(v0, l0, l1, l2);
-      split3(v1, h0, h1, h2);
-      a0[i] = __builtin_shufflevector(l0, h0, 0, 1, 2, 3, 4, 5, 6, 7);
-      a1[i] = __builtin_shufflevector(l1, h1, 0, 1, 2, 3, 4, 5, 6, 7);
-      a2[i] = __builtin_shufflevector(l2, h2, 0, 1, 2, 3, 4, 5, 6, 7);
-    }
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const char* bb = Bs + (wn0 + 32 * j) * (BK * 2) + lk * 512 + lrow * 16;
-      b0[j] = *reinterpret_cast<const bf16x8*>(bb);
-      b1[j] = *reinterpret_cast<const bf16x8*>(bb + PLANE_B);
-      b2[j] = *reinterpret_cast<const bf16x8*>(bb + 2 * PLANE_B);
-    }
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        acc[i][j] = fm_mfma32_bf16(a1[i], b1[j], acc[i][j]);
-        acc[i][j] = fm_mfma32_bf16(a1[i], b0[j], acc[i][j]);
-        acc[i][j] = fm_mfma32_bf16(a0[i], b1[j], acc[i][j]);
+        const char* bb = Bs + ks * BN * 32 + (wn0 + 32 * j) * 32 + lk * 512 + lrow * 16;
+        b0[j] = *reinterpret_cast<const bf16x8*>(bb);
+        b1[j] = *reinterpret_cast<const bf16x8*>(bb + PLANE_B);
+        b2[j] = *reinterpret_cast<const bf16x8*>(bb + 2 * PLANE_B);
       }
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        acc[i][j] = fm_mfma32_bf16(a2[i], b0[j], acc[i][j]);
-        acc[i][j] = fm_mfma32_bf16(a0[i], b2[j], acc[i][j]);
-        acc[i][j] = fm_mfma32_bf16(a0[i], b0[j], acc[i][j]);
-      }
+        for (int j = 0; j < FN; ++j) {
+          acc[i][j] = fm_mfma32_bf16(a1[i], b1[j], acc[i][j]);
+          acc[i][j] = fm_mfma32_bf16(a1[i], b0[j], acc[i][j]);
+          acc[i][j] = fm_mfma32_bf16(a0[i], b1[j], acc[i][j]);
+        }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          acc[i][j] = fm_mfma32_bf16(a2[i], b0[j], acc[i][j]);
+          acc[i][j] = fm_mfma32_bf16(a0[i], b2[j], acc[i][j]);
+          acc[i][j] = fm_mfma32_bf16(a0[i], b0[j], acc[i][j]);
+        }
+    }
   }
   lds_barrier();
 
@@ -1476,6 +1483,10 @@ constexpr TileCfg kX6 = {128, 128, 1, 32, 16, 0};     // bf16x6 tiles (k-tile 16
 constexpr TileCfg kX6Big = {256, 128, 1, 32, 17, 0};
 constexpr TileCfg kX6Small = {64, 128, 1, 32, 18, 0};  // direct-load A, four waves of 32x64
 constexpr TileCfg kX6Wide = {192, 128, 1, 32, 19, 0};  // direct-load A, twelve waves, one block per CU
+// kX6 / kX6Wide with 32-deep k-tiles (80 / 96 KB of LDS: still two / one
+// block per CU).
+constexpr TileCfg kX6K32 = {128, 128, 1, 32, 20, 0};
+constexpr TileCfg kX6WideK32 = {192, 128, 1, 32, 22, 0};
 constexpr TileCfg kDl192 = {192, 128, 1, 32, 14, 0};
 // 64x128 runs one block per CU: 64-deep k-tiles (96 KB ring) halve its barriers.
 constexpr TileCfg kDl64 = {64, 128, 1, 64, 15, 0};
@@ -1534,6 +1545,8 @@ const char* kernel_name(int id, bool elu) {
     case 17: return elu ? "gemm_x6d_kernel<256,128,8,1,2,true>" : "gemm_x6d_kernel<256,128,8,1,2,false>";
     case 18: return elu ? "gemm_x6d_kernel<64,128,2,2,2,true>" : "gemm_x6d_kernel<64,128,2,2,2,false>";
     case 19: return elu ? "gemm_x6d_kernel<192,128,6,2,2,true>" : "gemm_x6d_kernel<192,128,6,2,2,false>";
+    case 20: return "gemm_x6d_kernel<128,128,4,2,2,false,2>";
+    case 22: return "gemm_x6d_kernel<192,128,6,2,2,false,2>";
     case 7: return "gemm_mid_kernel<64,64,1>";
     case 8: return "gemm_mid_kernel<32,32,4>";
     default: return "gemm_generic_kernel";
@@ -1710,7 +1723,17 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
   // of a head sit in the block's output tile in LDS).  Any other plan stays
   // as selected, so the projection rounds as fm_linear's, and RoPE follows
   // as its own launch.
-  const bool rope_after = (p.flags & FM_EPI_ROPE) && (!(cfg.id >= 16 && cfg.id <= 19) || splits != 1);
+  // 32-deep k-tiles (two 16-deep sub-tiles per stage, in k order, so the
+  // result is the 16-deep tile's bit for bit) halve the barriers of the
+  // 128x128 and 192x128 tiles at the same blocks per CU: C2 dec.up5 51.6 ->
+  // 50.2 us, C3 enc.down8 368 -> 353 us, 4000-row qkv 40.9 -> 40.0 us,
+  // 2500-row fc1 42.9 -> 41.4 us.  The 64x128 tile keeps 16 (its 64 KB ring
+  // would cost blocks per CU: 2500-row fc2 46 -> 50 us).
+  if (!(p.flags & FM_ELU_IN) && p.C_in % 32 == 0 && p.K % 32 == 0) {
+    if (cfg.id == kX6.id) cfg = kX6K32;
+    else if (cfg.id == kX6Wide.id) cfg = kX6WideK32;
+  }
+  const bool rope_after = (p.flags & FM_EPI_ROPE) && (!(cfg.id >= 16 && cfg.id <= 22) || splits != 1);
   if (rope_after) p.flags &= ~FM_EPI_ROPE;
   if (splits > 1) {
     const size_t per = (size_t)M * p.N * sizeof(float);
@@ -1777,6 +1800,14 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
       else
         hipLaunchKernelGGL((gemm_x6d_kernel<192, 128, 6, 2, 2, false>), grid, dim3(768), 0, s, p,
                            reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
+      break;
+    case 20:
+      hipLaunchKernelGGL((gemm_x6d_kernel<128, 128, 4, 2, 2, false, 2>), grid, dim3(512), 0, s, p,
+                         reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
+      break;
+    case 22:
+      hipLaunchKernelGGL((gemm_x6d_kernel<192, 128, 6, 2, 2, false, 2>), grid, dim3(768), 0, s, p,
+                         reinterpret_cast<const __bf16*>(p.w + (long)p.N * p.K));
       break;
     case 7: hipLaunchKernelGGL((gemm_mid_kernel<64, 64, 1>), grid, dim3(NTHREADS), 0, s, p); break;
     case 8: hipLaunchKernelGGL((gemm_mid_kernel<32, 32, 4>), grid, dim3(NTHREADS), 0, s, p); break;
