@@ -34,6 +34,8 @@
 // multiple of 4: the 1-channel first convolution and tiny test configs).
 
 #include <cstdio>
+#include <type_traits>
+
 #include "fm_common.h"
 
 extern "C" int fm_apply_rope(float* x, long rows, int ld, int rope_cols, int head_dim,
@@ -57,6 +59,7 @@ struct GemmArgs {
   const float* rope_cos;
   const float* rope_sin;
   int rope_cols, rows_per_seq;
+  FmDivisor seq_div;  // division by `rows_per_seq` (set by run_gemm)
 };
 
 constexpr int KT = 32;  // k granularity of K-splits (every tile's BK divides it or is 64)
@@ -1082,12 +1085,36 @@ __global__ __launch_bounds__(256) void split_weights_kernel(const float* __restr
 // own A fragments after the LDS read, so no register staging or wait sits in
 // the k-loop; a wave tile spanning the block's columns (WN = 1: 32 x 128)
 // splits every A element once, narrower ones (32 x 64) twice.  Products in
-// the order a1b1, a1b0, a0b1, a2b0, a0b2, a0b0 per k-tile.  Tiles: 256 x 128
-// (eight waves of 32 x 128, 56 KB, two blocks per CU) where it gives at least
-// 384 tiles; 128 x 128 / 64 x 128 / 192 x 128 (waves of 32 x 64) for smaller
-// grids.
+// the order a1b1, a1b0, a0b1, a2b0, a0b2, a0b0 per k-tile.  The epilogue
+// stores straight from the accumulators.  Tiles: 256 x 128 (eight waves of
+// 32 x 128, 56 KB, two blocks per CU) where it gives at least 384 tiles;
+// 128 x 128 / 64 x 128 / 192 x 128 (waves of 32 x 64) for smaller grids.
+// Blocks per CU of the bf16x6 tiles, set explicitly (register budget below,
+// LDS floor in the kernel), measured per tile on the C2-C4 shapes:
+//   256x128: two (held to 128 VGPRs; at its natural 138 only one fits:
+//            dec.up4 at C4 633 -> 411 us);
+//   64x128: four (an LDS floor above 32 KB and 128 VGPRs; at three the
+//            K-split shapes ran 14% slower);
+//   192x128 with 16-deep k-tiles: one (an LDS floor above 80 KB; two per CU
+//            ran the ELU-on-load form 13% slower);
+//   128x128 of four 32x128 waves: three (an LDS floor above 40 KB and 168
+//            VGPRs; four ran 9% slower);
+//   the rest as their LDS ring and natural register use give.
+constexpr int x6d_min_waves_per_simd(int BM, int NW, int WN) {
+  if (BM == 256 && WN == 1) return 4;
+  if (BM == 64) return 4;
+  if (BM == 128 && WN == 1) return 3;
+  return (NW + 3) / 4;  // what the block size implies (the compiler's default)
+}
+constexpr int x6d_lds_floor(int BM, int WN, int KS) {
+  if (BM == 192 && KS == 1) return 80 * 1024 + 1024;
+  if (BM == 128 && WN == 1) return 40 * 1024 + 1024;
+  if (BM == 64) return 32 * 1024 + 1024;
+  return 0;
+}
 template <int BM, int BN, int WM, int WN, int NST, bool ELU, int KS = 1>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, const __bf16* __restrict__ w3) {
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(x6d_min_waves_per_simd(BM, WM * WN, WN))))
+void gemm_x6d_kernel(GemmArgs p, const __bf16* __restrict__ w3) {
   // KS 16-deep k sub-tiles per stage (BK = 16 KS), run in k order.
   constexpr int NW = WM * WN, NTH = 64 * NW, BK = 16 * KS;
   static_assert(NW % 2 == 0 && NW <= 12 && NST == 2, "two to twelve waves, two stages");
@@ -1099,18 +1126,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
   static_assert(AI >= 1 && AI * NW * RPI == BM && FM >= 1 && FN >= 1 && BN % 32 == 0, "tiling");
   constexpr int PLANE_B = BN * BK * 2, STAGE_A = BM * BK * 4, STAGE = STAGE_A + 3 * PLANE_B;
   constexpr int NBI = 3 * KS * BN / 32;  // 1 KB B load instructions per stage
-  // Epilogue passes of EG wave rows: the most that fit in the k-loop's LDS
-  // (fewer passes, fewer barriers), else the fewest that the block's rows
-  // per store step divide.
-  // Output tile pitch: rows four apart (the two half-waves of an
-  // accumulator store) 32 banks apart, so the stores do not conflict.
-  constexpr int CG = BN / 4, RSTEP = NTH / CG, PC = BN + 8;
-  constexpr int EG0 = (WTM % RSTEP == 0) ? 1 : (2 * WTM % RSTEP == 0 && WM % 2 == 0) ? 2 : 3;
-  constexpr auto fits = [](int g) { return WM % g == 0 && (g * WTM) % RSTEP == 0 && g * WTM * PC * 4 <= NST * STAGE; };
-  constexpr int EG = fits(4) ? 4 : fits(3) ? 3 : fits(2) ? 2 : EG0;
-  constexpr int HM = EG * WTM, TILE_B = HM * PC * 4;
-  static_assert(WM % EG == 0 && HM % RSTEP == 0, "epilogue passes");
-  __shared__ __attribute__((aligned(16))) char smem[NST * STAGE > TILE_B ? NST * STAGE : TILE_B];
+  constexpr int LDS = NST * STAGE > x6d_lds_floor(BM, WN, KS) ? NST * STAGE : x6d_lds_floor(BM, WN, KS);
+  __shared__ __attribute__((aligned(16))) char smem[LDS];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = wave / WN;
@@ -1262,91 +1279,100 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_x6d_kernel(GemmArgs p, cons
         }
     }
   }
-  lds_barrier();
-
-  // Epilogue: WM passes of one wave row (WTM rows) through LDS.
-  float* fsm = reinterpret_cast<float*>(smem);
+  // Epilogue straight from the accumulators (no LDS pass, no barrier): lane
+  // l of a 32x32 accumulator holds column l % 32 of rows
+  // 8 (r / 4) + 4 (l / 32) + r % 4, so each store instruction writes two
+  // 128-byte row segments.  Stores and residual loads go through buffer
+  // resources over this tile's rows, so past-M rows and past-N columns
+  // (offset INT_MIN) are dropped / read as zero without a branch.  An
+  // accumulator's residuals and RoPE factors are all loaded before its first
+  // store: the compiler does not move a load above a store to y (which may
+  // alias the residual), so each would otherwise wait out a memory round
+  // trip.  RoPE's partner column c ^ 32 of a 64-column head is the same
+  // lane's accumulator of the neighbouring 32-column tile (wave tiles start
+  // on 64-column boundaries).
   const int lcol = lane & 31;
-  const bool crop = p.y_rows != p.rows;
-  const bool has_res = p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE);
   float* part = p.partial ? p.partial + (long)blockIdx.y * M * p.N : nullptr;
-  constexpr int NRUN = HM / RSTEP, RB = NRUN < 2 ? NRUN : 2;
-  static_assert(NTH % CG == 0 && HM % RSTEP == 0 && NRUN % RB == 0, "epilogue runs");
-  const int c = (tid % CG) * 4, r0 = tid / CG;
-  const int n = n0 + c;
-  const bool n_ok = n < p.N;
-  const bool rope = (p.flags & FM_EPI_ROPE) && n < p.rope_cols;
-  const bool rope_lo = (c & 32) == 0;  // first half of a 64-column head
-  const int ncl = n_ok ? n : 0;
-  const floatx4 bias = (p.bias && !part) ? *reinterpret_cast<const floatx4*>(p.bias + ncl % p.bias_len)
-                                         : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-  const floatx4 scale = ((p.flags & FM_EPI_RES_SCALE) && !part)
-                            ? *reinterpret_cast<const floatx4*>(p.scale + ncl)
-                            : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  const bool has_res = (p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE)) && !part;
+  const bool scaled = (p.flags & FM_EPI_RES_SCALE) && !part;
+  const int tile_bytes = (int)min((long)BM, M - m0) * p.N * 4;
+  const __amdgpu_buffer_rsrc_t ry = fm_buffer((part ? part : p.y) + m0 * p.N, tile_bytes);
+  const __amdgpu_buffer_rsrc_t rr = fm_buffer(has_res ? p.res + m0 * p.N : p.y, has_res ? tile_bytes : 0);
+  // Cropped outputs: row m = b rows + t goes to row b y_rows + t when
+  // t < y_rows; over a tile those rows rise by at most one per row, so they
+  // lie within BM + 1 rows of the tile's first one (crop0).
+  int crop0 = 0;
+  if (p.y_rows != p.rows) {
+    const int b0 = (int)fm_div((unsigned)m0, p.rows_div);
+    crop0 = b0 * p.y_rows + min((int)m0 - b0 * p.rows, p.y_rows);
+  }
+  const __amdgpu_buffer_rsrc_t rc = fm_buffer(p.y + (long)crop0 * p.N, (BM + 1) * p.N * 4);
+  static_assert(WTN % 64 == 0, "RoPE partners within the wave tile");
+  auto epilogue = [&](auto crop_c, auto rope_c) {
+    constexpr bool CROP = decltype(crop_c)::value, ROPE = decltype(rope_c)::value;
 #pragma unroll
-  for (int hf = 0; hf < WM / EG; ++hf) {
-    if (wr / EG == hf) {
-      const int rb = (wr % EG) * WTM;
+    for (int j = 0; j < FN; ++j) {
+      const int c = wn0 + 32 * j + lcol;
+      const int n = n0 + c;
+      const bool n_ok = n < p.N;
+      const int ncl = n_ok ? n : 0;
+      const bool rope = ROPE && n < p.rope_cols;
+      const float bias = (p.bias && !part) ? p.bias[ncl % p.bias_len] : 0.0f;
+      const float scale = scaled ? p.scale[ncl] : 0.0f;
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+      for (int i = 0; i < FM; ++i) {
+        const int rb = wm0 + 32 * i;
+        // Lane offset of the accumulator's first row; row 8 (r / 4) + r % 4
+        // further down is a wave-uniform scalar offset.
+        const int voff = n_ok ? ((rb + 4 * (lane >> 5)) * p.N + n) * 4 : INT_MIN;
+        auto soff = [&](int r) { return (8 * (r >> 2) + (r & 3)) * p.N * 4; };
+        float res[16];
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
+        for (int r = 0; r < 16; ++r) res[r] = (!ROPE && has_res) ? fm_buf_load1(rr, voff, soff(r)) : 0.0f;
+        // RoPE factors in two halves of eight rows (all sixteen at once
+        // would spill).
+        float cs[8], sn[8];
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            fsm[(rb + i * 32 + fm_mfma32_row(r, lane)) * PC + wn0 + j * 32 + lcol] = acc[i][j][r];
-    }
-    lds_barrier();
-    const long mh = m0 + hf * HM;
+        for (int r = 0; r < 16; ++r) {
+          float v = acc[i][j][r];
+          if constexpr (ROPE) {
+            if (r % 8 == 0) {
 #pragma unroll
-    for (int u0 = 0; u0 < NRUN; u0 += RB) {
-      floatx4 v[RB], res[RB];
-#pragma unroll
-      for (int u = 0; u < RB; ++u) {
-        const int r = r0 + (u0 + u) * RSTEP;
-        const long m = min(mh + r, M - 1);
-        v[u] = *reinterpret_cast<const floatx4*>(fsm + r * PC + c);
-        res[u] = (has_res && !part) ? *reinterpret_cast<const floatx4*>(p.res + m * p.N + ncl)
-                                    : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-      }
-      if (rope) {
-        // RoPE with the partner columns of the same 64-column head (c ^ 32,
-        // in this tile), each product and the sum rounded separately:
-        // x*cos - x[d+32]*sin for d < 32, x*cos + x[d-32]*sin after.
-#pragma unroll
-        for (int u = 0; u < RB; ++u) {
-          const int r = r0 + (u0 + u) * RSTEP;
-          const long m = min(mh + r, M - 1);
-          const int t = (int)(m % p.rows_per_seq);
-          const floatx4 pv = *reinterpret_cast<const floatx4*>(fsm + r * PC + (c ^ 32));
-          const floatx4 cs = *reinterpret_cast<const floatx4*>(p.rope_cos + (long)t * 64 + (c & 63));
-          const floatx4 sn = *reinterpret_cast<const floatx4*>(p.rope_sin + (long)t * 64 + (c & 63));
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            v[u][e] = __fadd_rn(__fmul_rn(v[u][e], cs[e]), __fmul_rn(rope_lo ? -pv[e] : pv[e], sn[e]));
+              for (int q = 0; q < 8; ++q) {
+                const int m = (int)min(m0 + rb + fm_mfma32_row(r + q, lane), M - 1);
+                const int t = m - (int)fm_div((unsigned)m, p.seq_div) * p.rows_per_seq;
+                cs[q] = rope ? p.rope_cos[t * 64 + (c & 63)] : 1.0f;
+                sn[q] = rope ? p.rope_sin[t * 64 + (c & 63)] : 0.0f;
+              }
+            }
+            // x*cos - x[d+32]*sin for d < 32, x*cos + x[d-32]*sin after; each
+            // product and the sum rounded separately.
+            const float pv = acc[i][j ^ 1][r];
+            if (rope) v = __fadd_rn(__fmul_rn(v, cs[r % 8]), __fmul_rn((j & 1) ? pv : -pv, sn[r % 8]));
+          }
+          if (!part) v = epilogue_v(v, bias, res[r], scale, p.flags);
+          if constexpr (CROP) {
+            const int m = (int)m0 + rb + fm_mfma32_row(r, lane);
+            const int b = (int)fm_div((unsigned)m, p.rows_div);
+            const int t = m - b * p.rows;
+            const bool ok = m < M && n_ok && t < p.y_rows;
+            fm_buf_store1(v, rc, ok ? ((b * p.y_rows + t - crop0) * p.N + n) * 4 : INT_MIN, 0);
+          } else {
+            fm_buf_store1(v, ry, voff, soff(r));
+          }
         }
-      }
-#pragma unroll
-      for (int u = 0; u < RB; ++u) {
-        const long m = mh + r0 + (u0 + u) * RSTEP;
-        if (m >= M || !n_ok) continue;
-        if (part) {
-          *reinterpret_cast<floatx4*>(part + m * p.N + n) = v[u];
-          continue;
-        }
-        floatx4 o = v[u];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = epilogue_v(o[e], bias[e], res[u][e], scale[e], p.flags);
-        long dst = m * p.N + n;
-        if (crop) {
-          const int b = (int)(m / p.rows);
-          const int t = (int)(m - (long)b * p.rows);
-          if (t >= p.y_rows) continue;
-          dst = ((long)b * p.y_rows + t) * p.N + n;
-        }
-        *reinterpret_cast<floatx4*>(p.y + dst) = o;
       }
     }
-    if (hf + 1 < WM / EG) lds_barrier();
+  };
+  using yes = std::true_type;
+  using no = std::false_type;
+  const bool crop = p.y_rows != p.rows && !part;
+  if (!ELU && (p.flags & FM_EPI_ROPE)) {
+    if (crop) epilogue(yes{}, yes{});
+    else epilogue(no{}, yes{});
+  } else {
+    if (crop) epilogue(yes{}, no{});
+    else epilogue(no{}, no{});
   }
 }
 
@@ -1564,12 +1590,16 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     return FM_BAD_ARGUMENT;
   if ((p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE)) && !p.res) return FM_BAD_ARGUMENT;
   if ((p.flags & FM_EPI_RES_SCALE) && !p.scale) return FM_BAD_ARGUMENT;
+  // RoPE rides only on plain projections (no ELU on load, no residual).
+  if ((p.flags & FM_EPI_ROPE) && (p.flags & (FM_ELU_IN | FM_EPI_RES_ADD | FM_EPI_RES_SCALE)))
+    return FM_UNSUPPORTED;
   if (p.bias && p.bias_len <= 0) return FM_BAD_ARGUMENT;
   const long M = (long)p.batch * p.rows;
   if (M == 0 || p.y_rows == 0) return FM_OK;
   if (p.L_in == 0 || M > INT_MAX / 2) return FM_BAD_ARGUMENT;
 
   p.rows_div = fm_divisor((unsigned)p.rows);
+  p.seq_div = fm_divisor((unsigned)(p.rows_per_seq > 0 ? p.rows_per_seq : 1));
   const bool fast = (p.C_in % 4 == 0) && (p.K % 4 == 0);
   TileCfg cfg = kSplitTile;
   long tiles = 0;
