@@ -1724,10 +1724,13 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
         cfg = kX6;
         splits = s128;
         // Unsplit with two tiles on some CUs: 192x128 tiles, one per CU,
-        // when they fit in one round (C4 res512.c1 at 20000 rows); unsplit
-        // with at most one tile per CU: 64x128 tiles, so every CU works
-        // (C2 enc.down5 65 -> 57 us, C2 dec.up6 52 -> 47 us).
-        if (s128 == 1 && t128 > 256 && tile_count(M, p.N, kX6Wide) <= 256) cfg = kX6Wide;
+        // when they fit in one round, but not with ELU on load (there the
+        // four-wave 128x128 tile at three blocks per CU wins: C4 res512.c1
+        // at 20000 rows 124 against 130 us); unsplit with at most one tile
+        // per CU: 64x128 tiles, so every CU works (C2 enc.down5 65 -> 57 us,
+        // C2 dec.up6 52 -> 47 us).
+        if (s128 == 1 && t128 > 256 && tile_count(M, p.N, kX6Wide) <= 256 && !(p.flags & FM_ELU_IN))
+          cfg = kX6Wide;
         if (s128 == 1 && t128 <= 256) cfg = kX6Small;
       } else {
         cfg = kX6Small;
@@ -1750,7 +1753,7 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
     }
   }
   // The RoPE epilogue needs whole unsplit bf16x6 tiles (the partner columns
-  // of a head sit in the block's output tile in LDS).  Any other plan stays
+  // of a head sit in the neighbouring accumulator of the same wave).  Any other plan stays
   // as selected, so the projection rounds as fm_linear's, and RoPE follows
   // as its own launch.
   // 32-deep k-tiles (two 16-deep sub-tiles per stage, in k order, so the
