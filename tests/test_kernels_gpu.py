@@ -177,6 +177,7 @@ DL_CASES = [
     (1, 2048, 512, 1, 1, 2500, 2499),   # long K, 80 tiles: 64x128 bf16x6 tiles split along K
     (1, 128, 1024, 3, 1, 5000, 4990),   # 320 128x128 tiles: 192x128 bf16x6 tiles, partial, crop
     (1, 256, 1024, 8, 1, 2500, None),   # 160 128x128 tiles, K 2048: bf16x6 split in two
+    (4, 64, 256, 4, 1, 6000, 2000),     # crop to a third: tiles span dropped rows and clip seams
 ]
 
 
