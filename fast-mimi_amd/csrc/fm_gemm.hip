@@ -1694,10 +1694,12 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
   // shapes keep the FP32 tile
   // picked for them (measured: the 512-column projections at 2500-4000 rows,
   // 64x128 FP32 tiles on all CUs against 80-128 bf16x6 tiles).
-  // (The bf16x6 tiles address the weight planes through a buffer resource:
-  // at most 2 GiB of planes.)
+  // (The bf16x6 tiles address the weight planes through a buffer resource,
+  // at most 2 GiB of planes, and store a tile's rows through 32-bit offsets:
+  // 257 rows of N columns below 2 GiB.)
   const bool x6_ok = (p.flags & FM_WEIGHTS_X6) && big_ok && !(p.flags & FM_REPLICATE) &&
-                     p.C_in % 16 == 0 && p.K % 16 == 0 && 6L * p.K * p.N <= 0x7fffffffL;
+                     p.C_in % 16 == 0 && p.K % 16 == 0 && 6L * p.K * p.N <= 0x7fffffffL &&
+                     257L * p.N * 4 <= 0x7fffffffL;
   if (x6_ok && cfg.id >= 9 && cfg.id <= 15 && cfg.id != 12) {
     const long t128 = tile_count(M, p.N, kX6);
     if (p.K >= 1024 && M >= 1024 && t128 < 360 && workspace) {
