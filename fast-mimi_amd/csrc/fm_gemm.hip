@@ -1039,6 +1039,44 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int spli
   }
 }
 
+// Vector form (N and bias_len multiples of 4, fewer than 2^31 float4s): each
+// thread sums four adjacent outputs of one row over the splits, in split
+// order as above, and applies the same epilogue; its row comes from a
+// magic-number division instead of a 64-bit one per element.
+__global__ __launch_bounds__(256) void splitk_reduce4_kernel(GemmArgs p, int splits, FmDivisor n4_div) {
+  const long M = (long)p.batch * p.rows;
+  const long total = M * p.N;
+  const unsigned total4 = (unsigned)(total / 4);
+  const int N4 = p.N / 4;
+  const bool res_in = p.flags & (FM_EPI_RES_ADD | FM_EPI_RES_SCALE);
+  const bool crop = p.y_rows != p.rows;
+  for (unsigned e4 = blockIdx.x * blockDim.x + threadIdx.x; e4 < total4; e4 += gridDim.x * blockDim.x) {
+    const long e = 4L * e4;
+    floatx4 s = *reinterpret_cast<const floatx4*>(p.partial + e);
+    for (int k = 1; k < splits; ++k) {
+      const floatx4 q = *reinterpret_cast<const floatx4*>(p.partial + (long)k * total + e);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) s[c] = __fadd_rn(s[c], q[c]);
+    }
+    const int m = (int)fm_div(e4, n4_div);
+    const int n = 4 * ((int)e4 - m * N4);
+    const floatx4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    const floatx4 bias = p.bias ? *reinterpret_cast<const floatx4*>(p.bias + n % p.bias_len) : zero;
+    const floatx4 scale = (p.flags & FM_EPI_RES_SCALE) ? *reinterpret_cast<const floatx4*>(p.scale + n) : zero;
+    const floatx4 res = res_in ? *reinterpret_cast<const floatx4*>(p.res + e) : zero;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s[c] = epilogue_v(s[c], bias[c], res[c], scale[c], p.flags);
+    long dst = e;
+    if (crop) {
+      const int b = (int)fm_div((unsigned)m, p.rows_div);
+      const int t = m - b * p.rows;
+      if (t >= p.y_rows) continue;
+      dst = ((long)b * p.y_rows + t) * p.N + n;
+    }
+    *reinterpret_cast<floatx4*>(p.y + dst) = s;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // FP32 contraction on the bf16 matrix cores ("bf16x6").  Every FP32 operand
 // is the sum of three round-to-nearest bf16 pieces, v = v0 + v1 + v2, exact to
@@ -1581,7 +1619,7 @@ const char* kernel_name(int id, bool elu) {
 
 void record_plan(int id, bool elu, long tiles, int splits) {
   snprintf(g_last_plan, sizeof g_last_plan, "%s tiles=%ld splits=%d%s", kernel_name(id, elu), tiles,
-           splits, splits > 1 ? " +splitk_reduce_kernel" : "");
+           splits, splits > 1 ? " +split-K reduce" : "");
 }
 
 int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s) {
@@ -1852,8 +1890,14 @@ int run_gemm(GemmArgs p, float* workspace, size_t workspace_bytes, hipStream_t s
   if (e != hipSuccess) return (int)e;
   if (splits > 1) {
     const long total = M * p.N;
-    const int blocks = (int)std::min<long>((total + 255) / 256, 2048);
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, p, splits);
+    if (p.N % 4 == 0 && !(p.bias && p.bias_len % 4) && total / 4 < 0x7fffffffL) {
+      const int blocks = (int)std::min<long>((total / 4 + 255) / 256, 2048);
+      hipLaunchKernelGGL(splitk_reduce4_kernel, dim3(blocks), dim3(256), 0, s, p, splits,
+                         fm_divisor((unsigned)(p.N / 4)));
+    } else {
+      const int blocks = (int)std::min<long>((total + 255) / 256, 2048);
+      hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, p, splits);
+    }
     e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }
