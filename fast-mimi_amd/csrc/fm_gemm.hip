@@ -1323,10 +1323,10 @@ void gemm_x6d_kernel(GemmArgs p, const __bf16* __restrict__ w3) {
   // 128-byte row segments.  Stores and residual loads go through buffer
   // resources over this tile's rows, so past-M rows and past-N columns
   // (offset INT_MIN) are dropped / read as zero without a branch.  An
-  // accumulator's residuals and RoPE factors are all loaded before its first
-  // store: the compiler does not move a load above a store to y (which may
-  // alias the residual), so each would otherwise wait out a memory round
-  // trip.  RoPE's partner column c ^ 32 of a 64-column head is the same
+  // accumulator's residuals are all loaded before its first store, its RoPE
+  // factors eight rows at a time: the compiler does not move a load above a
+  // store to y (which may alias the residual), so each would otherwise wait
+  // out a memory round trip.  RoPE's partner column c ^ 32 of a 64-column head is the same
   // lane's accumulator of the neighbouring 32-column tile (wave tiles start
   // on 64-column boundaries).
   const int lcol = lane & 31;
