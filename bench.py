@@ -13,6 +13,8 @@ float64 top-2 distance margins along the GPU's code chain.
 
 ``roofline`` describes the dominant kernel: its algorithmic FLOPs per launch
 over its mean launch time, timed with HIP events on the stream it runs on.
+``batch16.dominant_kernel`` times the same layer at the C3 shape, where its
+grid runs many rounds of tiles (at C2 it is a single round).
 ``cpu_baseline`` times the repository's CPU oracle (the reference's portable
 PyTorch path restated op for op) on the host cores, on the same 10 s input.
 
@@ -363,7 +365,10 @@ def main() -> None:
         f16 = roundtrip_flops(cfg, 16, a16.shape[-1], nq16)
         result["batch16"] = {"audio_sec_per_sec": round(16 * 10 / (med16 / 1e3), 2),
                              "median_ms": round(med16, 3),
-                             "pipeline_tflops": round(f16 / (med16 * 1e-3) / 1e12, 3)}
+                             "pipeline_tflops": round(f16 / (med16 * 1e-3) / 1e12, 3),
+                             # The dominant kernel where its grid runs many rounds
+                             # (at C2 it is one round of tiles).
+                             "dominant_kernel": dominant_kernel(model, DOMINANT, 16, a16.shape[-1], nq16, 10)}
     if not args.no_extra:
         for key, cfg_name, steps in (("long100s", "c4", 10), ("rvq_b64_nq32", "c5", 5)):
             ax, mx, nqx = synthetic.config_inputs(cfg_name)
