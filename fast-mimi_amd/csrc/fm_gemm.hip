@@ -1299,6 +1299,14 @@ void gemm_x6d_kernel(GemmArgs p, const __bf16* __restrict__ w3) {
         b1[j] = *reinterpret_cast<const bf16x8*>(bb + PLANE_B);
         b2[j] = *reinterpret_cast<const bf16x8*>(bb + 2 * PLANE_B);
       }
+      // Waves issuing their products run at raised priority, so a SIMD's
+      // MFMA pipe is fed before another wave's split: in the 64- and 128-row
+      // tiles (C3 128x128 ELU-on-load 172 -> 159 us, split 32-deep 128x128
+      // 352 -> 333 us).  Not in the 192x128 tile (1-2% slower) nor the
+      // 256x128 one (at its 128-VGPR budget the change made it spill in the
+      // k-loop).
+      constexpr bool PRIO = BM <= 128;
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -1315,6 +1323,7 @@ void gemm_x6d_kernel(GemmArgs p, const __bf16* __restrict__ w3) {
           acc[i][j] = fm_mfma32_bf16(a0[i], b2[j], acc[i][j]);
           acc[i][j] = fm_mfma32_bf16(a0[i], b0[j], acc[i][j]);
         }
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     }
   }
   // Epilogue straight from the accumulators (no LDS pass, no barrier): lane
