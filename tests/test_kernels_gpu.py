@@ -11,6 +11,8 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
+
 import pytest
 import torch
 import torch.nn.functional as F
@@ -201,6 +203,52 @@ def test_conv1d_direct_load_tiles(B, cin, cout, k, stride, L, y_len, epi, x6, ws
         got = run_conv(x, w, b, stride, "constant", nat.EPI_RES_ADD | nat.EPI_ELU, ws,
                        residual_ncl=res, y_len=y_len, x6=x6)
         want = F.elu(res.double() + want)
+    want = want[..., :y_len] if y_len is not None else want
+    assert got.shape == want.shape
+    close(got, want)
+
+
+def _random_x6_cases(n, seed=11):
+    """Seeded conv shapes large enough for the bf16x6 tiles (>= 192 tiles of
+    128 x 128 counting splits), with crops, residual epilogues, batch seams,
+    partial row and column tiles."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        B = int(rng.integers(1, 4))
+        cin = int(rng.choice([16, 32, 48, 64, 96, 128]))
+        cout = 4 * int(rng.integers(32, 160))
+        k = int(rng.integers(1, 9))
+        stride = int(rng.integers(1, k + 1))
+        rows = int(rng.integers(8000, 30000)) // B
+        L = rows * stride - int(rng.integers(0, stride))
+        rows = -(-L // stride)
+        if B * rows * cout < 192 * 128 * 128:
+            continue
+        y_len = None if rng.random() < 0.5 else int(rng.integers(rows // 2, rows + 1))
+        epi = "plain" if rng.random() < 0.5 else "res_elu"
+        out.append((B, cin, cout, k, stride, L, y_len, epi))
+    return out
+
+
+@pytest.mark.parametrize("B,cin,cout,k,stride,L,y_len,epi", _random_x6_cases(12))
+def test_conv1d_bf16x6_random_shapes(B, cin, cout, k, stride, L, y_len, epi, ws):
+    """Randomised shapes through the bf16x6 tiles (register epilogue: buffer
+    stores over a tile's rows, crop remap, residual loads) against float64."""
+    g = torch.Generator().manual_seed(B * 7 + cin + cout + k + L)
+    x = torch.randn(B, cin, L, generator=g)
+    w = torch.randn(cout, cin, k, generator=g) / math.sqrt(cin * k)
+    b = torch.randn(cout, generator=g) * 0.1
+    rows = -(-L // stride)
+    want = causal_conv1d(x.double(), w.double(), b.double(), stride)
+    if epi == "plain":
+        got = run_conv(x, w, b, stride, "constant", 0, ws, y_len=y_len, x6=True)
+    else:
+        res = torch.randn(B, cout, rows, generator=g)
+        got = run_conv(x, w, b, stride, "constant", nat.EPI_RES_ADD | nat.EPI_ELU, ws,
+                       residual_ncl=res, y_len=y_len, x6=True)
+        want = F.elu(res.double() + want)
+    assert "x6d" in nat.last_gemm_plan(), nat.last_gemm_plan()
     want = want[..., :y_len] if y_len is not None else want
     assert got.shape == want.shape
     close(got, want)
